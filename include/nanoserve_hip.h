@@ -1,0 +1,108 @@
+/*
+ * nanoserve_hip.h — C ABI of libnanoserve_hip.so, the gfx950 kernels of the decode token loop.
+ *
+ * Every entry point:
+ *   - takes raw device pointers and sizes (no framework types), plus the hipStream_t to launch on
+ *     (passed as void*; torch's torch.cuda.current_stream().cuda_stream on PyTorch-ROCm);
+ *   - only enqueues work: it never synchronises, never allocates or frees device memory, and its
+ *     launch grid depends on its integer arguments only, so it can be recorded into a hipGraph;
+ *   - returns 0 on success or a nonzero status (NS_E_* below, or a hipError_t value + 1000). The
+ *     message for the last failure on the calling thread is returned by ns_last_error().
+ *
+ * dtype codes: NS_DTYPE_F32 = 0, NS_DTYPE_BF16 = 1. Pool layout of one layer's K or V cache:
+ * [num_blocks, block_size, n_kv_heads, head_dim] with head_dim contiguous (strides in elements).
+ *
+ * Each function cites the reference interface it replaces (darshanseenivasakumar/nanoserve,
+ * Triton kernels called from nanoserve/model.py).
+ */
+#ifndef NANOSERVE_HIP_H
+#define NANOSERVE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NS_DTYPE_F32 0
+#define NS_DTYPE_BF16 1
+
+#define NS_OK 0
+#define NS_E_INVALID 1      /* argument outside what the kernels support (message says which) */
+#define NS_E_WORKSPACE 2    /* workspace pointer missing or smaller than ns_decode_workspace_bytes */
+#define NS_E_HIP_BASE 1000  /* 1000 + hipError_t of a failed launch */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* ns_last_error(void);
+
+/* Library version string (build id of the kernels). */
+const char* ns_version(void);
+
+/*
+ * Paged-attention decode: for each row b and query head h (KV head g = h / (n_heads / n_kv_heads)),
+ *   out[b, h, :] = softmax(q[b, h, :] . K[0:ctx_b]^T * scale) . V[0:ctx_b]
+ * where token t of row b lives at pool block block_tables[b, t / block_size], position t % block_size.
+ * Online softmax with fp32 running max / sum / accumulator; probabilities are rounded to the value
+ * dtype before the P.V product. Table entries past ceil(ctx_b / block_size) are never read.
+ * Replaces nanoserve/kernels/paged_attention.py:85 paged_attention_decode (kernel :34-82).
+ *
+ * Limits: head_dim in {64, 128}; block_size == 16; n_heads / n_kv_heads <= 16; ctx_b >= 1
+ * (a row with ctx_b <= 0 gets zeros). Guards that keep every access inside the caller's buffers:
+ * a row's page count is clamped to max_blocks (the table width), and a table entry outside
+ * [0, num_blocks) is read as an all-zero page.
+ * Long contexts are split into partitions that run in parallel (split-K); their partial results
+ * are merged in-kernel by the last partition to finish. That needs `workspace` of at least
+ * ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype) bytes whose counter
+ * region (the first ns_decode_counter_bytes(B, n_kv_heads) bytes) is ZERO before the first call;
+ * each call leaves the counters at zero again, so one workspace serves every later call and every
+ * replay of a captured graph. Calls that share a workspace must not overlap in time.
+ */
+int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
+                         const void* k_pool, const void* v_pool,
+                         int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                         const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                         void* out, int64_t o_sb, int64_t o_sh,
+                         int B, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                         int max_blocks, int num_blocks, float scale, int dtype,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype);
+size_t ns_decode_counter_bytes(int B, int n_kv_heads);
+
+/*
+ * RMSNorm over rows of length n (row-major, contiguous):
+ *   if residual != NULL: r = round(residual + x) is stored to res_out and replaces x;
+ *   out = round(w * round(x * rsqrt(mean(x^2) + eps)))     (statistics in fp32)
+ * round() = to the tensor dtype, where PyTorch's unfused ops round.
+ * Replaces nanoserve/kernels/fused.py:45 rms_norm (kernel :26-42).
+ */
+int ns_rms_norm(const void* x, const void* residual, const void* weight, void* out, void* res_out,
+                int64_t rows, int n, float eps, int dtype, void* stream);
+
+/*
+ * SwiGLU activation on the merged gate/up projection: x = [rows, 2n] holding [gate | up],
+ *   out[r, c] = round(round(silu(gate[r, c])) * up[r, c]),  silu(g) = g / (1 + exp(-g)) in fp32.
+ * Replaces nanoserve/kernels/fused.py:75 silu_mul (kernel :63-72).
+ */
+int ns_silu_mul(const void* x, void* out, int64_t rows, int n, int dtype, void* stream);
+
+/*
+ * RoPE on the merged QKV projection + paged KV write, one token per row of qkv
+ * [n_tok, (n_heads + 2 n_kv) head_dim]:
+ *   q/k heads: out_lo = r(r(x_lo c_lo) - r(x_hi s_lo)), out_hi = r(r(x_hi c_hi) + r(x_lo s_hi))
+ *   (r = round to bf16, ties to even, for bf16; identity for fp32; no fused multiply-add),
+ *   v heads copied. q -> [n_tok, n_heads, hd], k, v -> [n_tok, n_kv, hd].
+ *   If k_cache != NULL: k and v of token t are also stored at flat pool position slots[t]
+ *   (pool viewed as [num_blocks * block_size, n_kv, hd]). cos/sin: [n_tok, hd] in the same dtype.
+ * Replaces nanoserve/kernels/fused.py:156 rope_qkv (kernel :107-153, rounding :87-104).
+ */
+int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, void* q, void* k, void* v,
+                void* k_cache, void* v_cache, const int64_t* slots,
+                int64_t n_tok, int n_heads, int n_kv_heads, int head_dim, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOSERVE_HIP_H */

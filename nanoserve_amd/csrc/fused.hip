@@ -1,0 +1,247 @@
+// Token-wise fused kernels of the decode step for gfx950: RMSNorm (+ residual add), SiLU*mul, and
+// RoPE on the merged QKV projection with the paged KV write.
+//
+// Every kernel rounds to the tensor dtype exactly where PyTorch's unfused ops round, so bf16
+// outputs equal the unfused ops bit for bit apart from RMSNorm's fp32 sum order (<= 1 bf16 ulp).
+// Semantics follow nanoserve/kernels/fused.py (rms_norm :26-59, silu_mul :63-83, rope_qkv
+// :87-175); this file is built with -ffp-contract=off so no product is fused into an add.
+#include "ns_common.h"
+
+namespace ns {
+
+// ------------------------------------------------------------------------------------------ RMSNorm
+// One workgroup of 256 threads (4 waves) per row. Each thread holds VEC consecutive elements per
+// pass (16-byte loads for bf16); rows up to 256 * VEC * NPASS elements stay in registers, so x is
+// read from HBM once and written once.
+template <typename T>
+struct io;
+template <>
+struct io<float> {
+  static __device__ __forceinline__ float ld(const float* p) { return *p; }
+  static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+  static __device__ __forceinline__ float rnd(float v) { return v; }
+};
+template <>
+struct io<bf16_t> {
+  static __device__ __forceinline__ float ld(const bf16_t* p) { return bf16_to_f32(*p); }
+  static __device__ __forceinline__ void st(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+  static __device__ __forceinline__ float rnd(float v) { return round_bf16(v); }
+};
+
+constexpr int RMS_THREADS = 256;
+constexpr int RMS_MAX_PER_THREAD = 16;  // n <= 4096 elements per row
+
+template <typename T>
+__global__ __launch_bounds__(RMS_THREADS) void rms_norm_kernel(const T* __restrict__ x, const T* __restrict__ res,
+                                                               const T* __restrict__ w, T* __restrict__ out,
+                                                               T* __restrict__ res_out, int n, float eps) {
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * n;
+  float v[RMS_MAX_PER_THREAD];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < RMS_MAX_PER_THREAD; ++i) {
+    const int c = i * RMS_THREADS + threadIdx.x;
+    float a = 0.f;
+    if (c < n) {
+      a = io<T>::ld(xr + c);
+      if (res != nullptr) {
+        // residual + x, rounded to the dtype (PyTorch's `x + a`), kept for the next layer.
+        a = io<T>::rnd(io<T>::ld(res + row * n + c) + a);
+        io<T>::st(res_out + row * n + c, a);
+      }
+    }
+    v[i] = a;
+    ss += a * a;
+  }
+  __shared__ float part[RMS_THREADS / 64];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < RMS_THREADS / 64; ++i) tot += part[i];
+  const float inv = rsqrtf(tot / float(n) + eps);
+#pragma unroll
+  for (int i = 0; i < RMS_MAX_PER_THREAD; ++i) {
+    const int c = i * RMS_THREADS + threadIdx.x;
+    if (c < n) {
+      const float y = io<T>::rnd(v[i] * inv);  // HF casts back BEFORE the weight multiply
+      io<T>::st(out + row * n + c, io<T>::ld(w + c) * y);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------ SiLU*mul
+// Elementwise over [rows, n] outputs; each thread produces 8 consecutive outputs when n % 8 == 0.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ x, T* __restrict__ out, int64_t rows,
+                                                       int n) {
+  const int64_t total = rows * int64_t(n);
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / n;
+    const int64_t c = i - r * n;
+    const float g = io<T>::ld(x + r * 2 * n + c);
+    const float u = io<T>::ld(x + r * 2 * n + n + c);
+    const float s = io<T>::rnd(g / (1.0f + expf(-g)));  // F.silu: fp32 math, rounded to the dtype
+    io<T>::st(out + i, s * u);
+  }
+}
+
+// bf16 fast path: 8 outputs per thread with 16-byte loads and stores.
+__global__ __launch_bounds__(256) void silu_mul_bf16x8_kernel(const uint4* __restrict__ x, uint4* __restrict__ out,
+                                                              int64_t rows, int n8) {
+  const int64_t total = rows * int64_t(n8);
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / n8;
+    const int64_t c = i - r * n8;
+    const uint4 gv = x[r * 2 * n8 + c];
+    const uint4 uv = x[r * 2 * n8 + n8 + c];
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float o2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float g = bf16_to_f32(bf16_t(gw[j] >> (16 * h)));
+        const float u = bf16_to_f32(bf16_t(uw[j] >> (16 * h)));
+        const float s = round_bf16(g / (1.0f + expf(-g)));
+        o2[h] = s * u;
+      }
+      ow[j] = uint32_t(f32_to_bf16(o2[0])) | (uint32_t(f32_to_bf16(o2[1])) << 16);
+    }
+    out[i] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
+// ------------------------------------------------------------------------------------- RoPE + cache
+// One workgroup per token. Work item = (head, d) with d < hd/2 for the rotated q and k heads (the
+// pair d, d + hd/2 is produced together), then (head, d) < n_kv * hd for the value copy.
+// rotate_half(x) = [-x_hi, x_lo], so with lo/hi halves of each head:
+//   out_lo = x_lo*cos_lo - x_hi*sin_lo,   out_hi = x_hi*cos_hi + x_lo*sin_hi
+// with a rounding after each product and after the sum (PyTorch's q*c + rotate_half(q)*s in bf16).
+template <typename T>
+__global__ __launch_bounds__(256) void rope_qkv_kernel(const T* __restrict__ qkv, const T* __restrict__ cosb,
+                                                       const T* __restrict__ sinb, T* __restrict__ q,
+                                                       T* __restrict__ k, T* __restrict__ v, T* __restrict__ kc,
+                                                       T* __restrict__ vc, const int64_t* __restrict__ slots, int nh,
+                                                       int nkv, int hd) {
+  const int64_t t = blockIdx.x;
+  const int half = hd >> 1;
+  const int width = (nh + 2 * nkv) * hd;
+  const T* row = qkv + t * width;
+  const T* cr = cosb + t * hd;
+  const T* sr = sinb + t * hd;
+  const int64_t slot = kc != nullptr ? slots[t] : 0;
+  const int n_rot = (nh + nkv) * half;
+  for (int i = threadIdx.x; i < n_rot; i += blockDim.x) {
+    const int head = i / half;
+    const int d = i - head * half;
+    const float xl = io<T>::ld(row + head * hd + d);
+    const float xh = io<T>::ld(row + head * hd + half + d);
+    const float cl = io<T>::ld(cr + d), ch = io<T>::ld(cr + half + d);
+    const float sl = io<T>::ld(sr + d), sh = io<T>::ld(sr + half + d);
+    const float lo = io<T>::rnd(io<T>::rnd(xl * cl) - io<T>::rnd(xh * sl));
+    const float hi = io<T>::rnd(io<T>::rnd(xh * ch) + io<T>::rnd(xl * sh));
+    if (head < nh) {
+      T* dst = q + (t * nh + head) * hd;
+      io<T>::st(dst + d, lo);
+      io<T>::st(dst + half + d, hi);
+    } else {
+      const int kh = head - nh;
+      T* dst = k + (t * nkv + kh) * hd;
+      io<T>::st(dst + d, lo);
+      io<T>::st(dst + half + d, hi);
+      if (kc != nullptr) {
+        T* cd = kc + (slot * nkv + kh) * hd;
+        io<T>::st(cd + d, lo);
+        io<T>::st(cd + half + d, hi);
+      }
+    }
+  }
+  const int n_v = nkv * hd;
+  const T* vrow = row + (nh + nkv) * hd;
+  for (int i = threadIdx.x; i < n_v; i += blockDim.x) {
+    const T val = vrow[i];
+    v[t * n_v + i] = val;
+    if (vc != nullptr) vc[slot * n_v + i] = val;
+  }
+}
+
+}  // namespace ns
+
+using namespace ns;
+
+extern "C" int ns_rms_norm(const void* x, const void* residual, const void* weight, void* out, void* res_out,
+                           int64_t rows, int n, float eps, int dtype, void* stream) {
+  NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "rms_norm: dtype %d not supported", dtype);
+  NS_REQUIRE(n > 0 && n <= RMS_THREADS * RMS_MAX_PER_THREAD, "rms_norm: row length %d outside 1..%d", n,
+             RMS_THREADS * RMS_MAX_PER_THREAD);
+  NS_REQUIRE(residual == nullptr || res_out != nullptr, "rms_norm: residual given without res_out");
+  NS_REQUIRE(rows >= 0 && rows < (int64_t(1) << 31), "rms_norm: rows %lld out of range", (long long)rows);
+  if (rows == 0) return NS_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == NS_DTYPE_BF16)
+    hipLaunchKernelGGL(rms_norm_kernel<bf16_t>, dim3(unsigned(rows)), dim3(RMS_THREADS), 0, s,
+                       static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(residual),
+                       static_cast<const bf16_t*>(weight), static_cast<bf16_t*>(out), static_cast<bf16_t*>(res_out),
+                       n, eps);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<float>, dim3(unsigned(rows)), dim3(RMS_THREADS), 0, s,
+                       static_cast<const float*>(x), static_cast<const float*>(residual),
+                       static_cast<const float*>(weight), static_cast<float*>(out), static_cast<float*>(res_out), n,
+                       eps);
+  return check_launch("rms_norm");
+}
+
+extern "C" int ns_silu_mul(const void* x, void* out, int64_t rows, int n, int dtype, void* stream) {
+  NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "silu_mul: dtype %d not supported", dtype);
+  NS_REQUIRE(n > 0 && rows >= 0, "silu_mul: bad shape rows=%lld n=%d", (long long)rows, n);
+  if (rows == 0) return NS_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = dtype == NS_DTYPE_BF16 && n % 8 == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+  const int64_t items = vec ? rows * (n / 8) : rows * int64_t(n);
+  int64_t blocks = (items + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (vec)
+    hipLaunchKernelGGL(silu_mul_bf16x8_kernel, dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const uint4*>(x), static_cast<uint4*>(out), rows, n / 8);
+  else if (dtype == NS_DTYPE_BF16)
+    hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), rows, n);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<float>, dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const float*>(x), static_cast<float*>(out), rows, n);
+  return check_launch("silu_mul");
+}
+
+extern "C" int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, void* q, void* k, void* v,
+                           void* k_cache, void* v_cache, const int64_t* slots, int64_t n_tok, int n_heads,
+                           int n_kv_heads, int head_dim, int dtype, void* stream) {
+  NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "rope_qkv: dtype %d not supported", dtype);
+  NS_REQUIRE(n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
+             "rope_qkv: bad heads nh=%d nkv=%d hd=%d", n_heads, n_kv_heads, head_dim);
+  NS_REQUIRE((k_cache == nullptr) == (v_cache == nullptr), "rope_qkv: give both caches or neither");
+  NS_REQUIRE(k_cache == nullptr || slots != nullptr, "rope_qkv: cache write needs slots");
+  NS_REQUIRE(n_tok >= 0 && n_tok < (int64_t(1) << 31), "rope_qkv: n_tok %lld out of range", (long long)n_tok);
+  if (n_tok == 0) return NS_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == NS_DTYPE_BF16)
+    hipLaunchKernelGGL(rope_qkv_kernel<bf16_t>, dim3(unsigned(n_tok)), dim3(256), 0, s,
+                       static_cast<const bf16_t*>(qkv), static_cast<const bf16_t*>(cos),
+                       static_cast<const bf16_t*>(sin), static_cast<bf16_t*>(q), static_cast<bf16_t*>(k),
+                       static_cast<bf16_t*>(v), static_cast<bf16_t*>(k_cache), static_cast<bf16_t*>(v_cache), slots,
+                       n_heads, n_kv_heads, head_dim);
+  else
+    hipLaunchKernelGGL(rope_qkv_kernel<float>, dim3(unsigned(n_tok)), dim3(256), 0, s,
+                       static_cast<const float*>(qkv), static_cast<const float*>(cos), static_cast<const float*>(sin),
+                       static_cast<float*>(q), static_cast<float*>(k), static_cast<float*>(v),
+                       static_cast<float*>(k_cache), static_cast<float*>(v_cache), slots, n_heads, n_kv_heads,
+                       head_dim);
+  return check_launch("rope_qkv");
+}

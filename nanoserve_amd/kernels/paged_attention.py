@@ -1,0 +1,70 @@
+"""Paged-attention DECODE on the GPU through the HIP kernel (csrc/paged_attention.hip).
+
+Same entry point and argument meaning as nanoserve/kernels/paged_attention.py:85-105:
+
+    paged_attention_decode(q, k_pool, v_pool, block_tables, context_lens, scale) -> out
+
+q: [B, n_heads, head_dim] (last dim contiguous); k_pool / v_pool: ONE layer's pool
+[num_blocks, block_size, n_kv_heads, head_dim] with identical strides; block_tables: int32 [B, max_blocks]
+(padding entries never read); context_lens: int32 [B], including the new token whose K/V must already be
+written. Returns out = torch.empty_like(q) filled with the attention output.
+
+The bf16 kernel splits long contexts across workgroups and merges the partial softmax states in-kernel.
+That merge needs a small device workspace; one per (device, B, n_kv_heads, head_dim, max_blocks) is
+allocated on first use (outside any graph capture: the graph runners warm up eagerly first) and reused by
+every later call and graph replay. Calls on one stream never overlap, so sharing it is safe.
+"""
+from __future__ import annotations
+
+import torch
+
+from nanoserve_amd import _lib
+
+_WORKSPACES: dict[tuple, torch.Tensor] = {}
+
+
+def decode_workspace(device: torch.device, B: int, n_kv_heads: int, head_dim: int, max_blocks: int,
+                     dtype: torch.dtype) -> torch.Tensor | None:
+    """The (zero-initialised, self-resetting) split-K workspace for this launch shape, or None if the
+    launch needs none."""
+    nbytes = _lib.lib().ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, _lib.dtype_code_of(dtype))
+    if nbytes == 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(), B, n_kv_heads, head_dim,
+           max_blocks, dtype)
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("paged_attention_decode: first call for this shape happened inside a graph capture; "
+                               "run one eager call (warm-up) before capturing")
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                           block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float) -> torch.Tensor:
+    B, n_heads, head_dim = q.shape
+    num_blocks, block_size, n_kv_heads, hd2 = k_pool.shape
+    assert hd2 == head_dim and q.dtype == k_pool.dtype == v_pool.dtype
+    assert q.stride(-1) == 1 and k_pool.stride(-1) == 1 and v_pool.stride() == k_pool.stride()
+    assert v_pool.shape == k_pool.shape
+    assert block_tables.dtype == torch.int32 and block_tables.dim() == 2 and block_tables.shape[0] == B
+    assert block_tables.stride(1) == 1 or block_tables.shape[1] == 1
+    assert context_lens.dtype == torch.int32 and context_lens.shape == (B,) and context_lens.is_contiguous()
+    _lib.require_gpu(q, k_pool, v_pool, block_tables, context_lens)
+    out = torch.empty_like(q)
+    if B == 0:
+        return out
+    max_blocks = block_tables.shape[1]
+    ws = decode_workspace(q.device, B, n_kv_heads, head_dim, max_blocks, q.dtype)
+    L = _lib.lib()
+    _lib.check(L.ns_paged_attn_decode(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, n_heads, n_kv_heads, head_dim, block_size, max_blocks, num_blocks, float(scale), _lib.dtype_code(q),
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _lib.stream_of(q)),
+        "paged_attention_decode")
+    return out

@@ -1,0 +1,97 @@
+"""HIP fused token-wise kernels vs the CPU oracle's unfused ops (oracle/ops.py).
+
+Gates follow the reference's tests/test_fused_ops.py:29-96: fp32 within 1e-5; bf16 at least 99% bitwise
+identical and the rest within 1 bf16 ulp; the residual add is exact; RoPE writes rotated K and plain V at
+exactly the given slots and nothing else. Inputs are drawn on the CPU (seeded) and copied to the GPU, so the
+oracle (torch on the CPU) and the kernels see identical values.
+"""
+import pytest
+import torch
+
+from oracle import ops
+from tests.conftest import cpu_gen
+
+pytestmark = pytest.mark.gpu
+
+DT = [torch.float32, torch.bfloat16]
+
+
+def check(out, ref, dtype):
+    out = out.cpu()
+    assert out.shape == ref.shape and out.dtype == ref.dtype
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-5)
+        return
+    same = (out == ref).float().mean().item()
+    assert same >= 0.99, f"only {same:.4f} bitwise identical"
+    torch.testing.assert_close(out.float(), ref.float(), rtol=2 ** -7, atol=1e-6)   # <= 1 bf16 ulp
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("n", [896, 1536, 2048])
+def test_rms_norm(hiplib, dtype, n):
+    from nanoserve_amd.kernels.fused import rms_norm
+    g = cpu_gen(0)
+    x = (torch.randn(37, n, generator=g) * 3).to(dtype)
+    w = (1 + 0.1 * torch.randn(n, generator=g)).to(dtype)
+    check(rms_norm(x.cuda(), w.cuda(), 1e-6), ops.rms_norm(x, w, 1e-6), dtype)
+
+
+@pytest.mark.parametrize("dtype", DT)
+def test_rms_norm_with_residual_add(hiplib, dtype):
+    from nanoserve_amd.kernels.fused import rms_norm
+    g = cpu_gen(1)
+    x, a = (torch.randn(1, 37, 896, generator=g).to(dtype) for _ in range(2))
+    w = (1 + 0.1 * torch.randn(896, generator=g)).to(dtype)
+    out, res = rms_norm(a.cuda(), w.cuda(), 1e-6, residual=x.cuda())
+    ref_out, ref_res = ops.rms_norm_residual(a, w, 1e-6, x)
+    assert torch.equal(res.cpu(), ref_res)                     # the add is exact: same rounding as PyTorch
+    check(out, ref_out, dtype)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("n", [4864, 8960, 11008, 100])
+def test_silu_mul(hiplib, dtype, n):
+    from nanoserve_amd.kernels.fused import silu_mul
+    g = cpu_gen(2)
+    x = (torch.randn(1, 37, 2 * n, generator=g) * 2).to(dtype)
+    check(silu_mul(x.cuda()), ops.silu_mul(x), dtype)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (12, 2, 128), (16, 2, 128)])
+def test_rope_qkv_and_cache_write(hiplib, dtype, nh, nkv, hd):
+    from nanoserve_amd.kernels.fused import rope_qkv
+    g = cpu_gen(3)
+    N = 37
+    qkv = torch.randn(N, (nh + 2 * nkv) * hd, generator=g).to(dtype)
+    positions = torch.randint(0, 2000, (N,), generator=g)
+    cos, sin = ops.rope_tables(positions, hd, 1_000_000.0, dtype)
+    slots = torch.randperm(8 * 16, generator=g)[:N]
+    k_cache = torch.zeros(8, 16, nkv, hd, dtype=dtype, device="cuda")
+    v_cache = torch.zeros_like(k_cache)
+    q, k, v = rope_qkv(qkv.cuda(), cos.cuda(), sin.cuda(), nh, nkv, hd, k_cache, v_cache, slots.cuda())
+
+    rk, rv = torch.zeros(8, 16, nkv, hd, dtype=dtype), torch.zeros(8, 16, nkv, hd, dtype=dtype)
+    q0, k0, v0 = ops.rope_qkv(qkv, cos, sin, nh, nkv, hd, rk, rv, slots)
+    check(q, q0, dtype)
+    check(k, k0, dtype)
+    assert torch.equal(v.cpu(), v0)
+    k, v = k.cpu(), v.cpu()
+    flat_k, flat_v = k_cache.cpu().view(-1, nkv, hd), v_cache.cpu().view(-1, nkv, hd)
+    assert torch.equal(flat_k[slots], k) and torch.equal(flat_v[slots], v)
+    untouched = torch.ones(8 * 16, dtype=torch.bool)
+    untouched[slots] = False
+    assert not flat_k[untouched].any() and not flat_v[untouched].any()
+
+
+def test_rope_without_cache(hiplib):
+    from nanoserve_amd.kernels.fused import rope_qkv
+    g = cpu_gen(4)
+    qkv = torch.randn(5, (12 + 4) * 128, generator=g).to(torch.bfloat16)
+    cos, sin = ops.rope_tables(torch.arange(5), 128, 1e6, torch.bfloat16)
+    q, k, v = rope_qkv(qkv.cuda(), cos.cuda(), sin.cuda(), 12, 2, 128)
+    q0, k0, v0 = ops.rope_qkv(qkv, cos, sin, 12, 2, 128)
+    check(q, q0, torch.bfloat16)
+    check(k, k0, torch.bfloat16)
+    assert torch.equal(v.cpu(), v0)
