@@ -49,14 +49,13 @@ const char* ns_version(void);
  *
  * Limits: head_dim in {64, 128}; block_size == 16; n_heads / n_kv_heads <= 16; ctx_b >= 1
  * (a row with ctx_b <= 0 gets zeros). Guards that keep every access inside the caller's buffers:
- * a row's page count is clamped to max_blocks (the table width), and a table entry outside
- * [0, num_blocks) is read as an all-zero page.
- * Long contexts are split into partitions that run in parallel (split-K); their partial results
- * are merged in-kernel by the last partition to finish. That needs `workspace` of at least
- * ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype) bytes whose counter
- * region (the first ns_decode_counter_bytes(B, n_kv_heads) bytes) is ZERO before the first call;
- * each call leaves the counters at zero again, so one workspace serves every later call and every
- * replay of a captured graph. Calls that share a workspace must not overlap in time.
+ * a row's page count is clamped to max_blocks (the table width), and the tokens of a table entry
+ * outside [0, num_blocks) are masked out (no memory outside the pool is read).
+ * Long contexts are split into partitions that run in parallel (split-K); a second small kernel on
+ * the same stream merges their partial softmax states. That needs `workspace` of at least
+ * ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype) bytes (256-byte aligned; no
+ * initialisation needed; 0 bytes means none is needed). Calls sharing a workspace must be ordered
+ * (same stream), which every caller in the decode loop is.
  */
 int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                          const void* k_pool, const void* v_pool,
@@ -68,7 +67,6 @@ int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype);
-size_t ns_decode_counter_bytes(int B, int n_kv_heads);
 
 /*
  * RMSNorm over rows of length n (row-major, contiguous):

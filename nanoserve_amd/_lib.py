@@ -36,7 +36,6 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         _c_int, _c_int, _c_f32, _c_int,         # max_blocks, num_blocks, scale, dtype
         _c_vp, _c_sz, _c_vp]),                  # workspace, workspace_bytes, stream
     "ns_decode_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
-    "ns_decode_counter_bytes": (_c_sz, [_c_int, _c_int]),
     "ns_rms_norm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_f32, _c_int, _c_vp]),
     "ns_silu_mul": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "ns_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,

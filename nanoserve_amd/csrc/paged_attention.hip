@@ -9,17 +9,21 @@
 //   * Split-K over the context: grid = (partitions, n_kv, B). A partition is NW waves x PPW pages;
 //     page p0 + w + NW*i goes to wave w. Rows shorter than the grid's reach exit early, so the
 //     grid depends on (B, table width) only and the launch can be captured in a hipGraph.
-//   * Each wave issues every K and V load of its pages up front (16-byte, coalesced per token row),
-//     then works page by page with matrix cores. The GQA group makes both products dense:
+//   * Each wave first reads the block ids of its pages, then issues every K and V load of those
+//     pages with no wait in between, then works page by page on the matrix cores. The GQA group
+//     makes both products dense (rows >= G of Q are zero):
 //       S^T[16 tok x 16 heads] = K_page[16 x hd] . Q^T[hd x 16]            (mfma 16x16x32 bf16)
 //       O^T[hd x 16 heads]    += V_page^T[hd x 16 tok] . P^T[16 tok x 16]  (mfma 16x16x16 bf16)
-//     Rows >= G of Q are zero. The S^T output layout (lane = head, 4 consecutive tokens) is exactly
-//     the B-operand layout P^T needs, so P never leaves registers; only V is transposed, through a
-//     wave-private LDS tile of one page.
+//     The S^T output layout (lane = head, 4 consecutive tokens) is exactly the B-operand layout
+//     P^T needs, so P never leaves registers. For V^T the contraction index (token) and the output
+//     row (dim) may be relabelled freely: lane (c16, r4) takes dims NT*c16 .. NT*c16+NT-1 of tokens
+//     4*r4 .. 4*r4+3, which are four coalesced row-slice loads, and a 4x4 register transpose
+//     (v_perm) turns them into the NT operand fragments. No LDS on the per-page path.
 //   * Softmax statistics per head: a lane's 4 tokens, then 2 butterfly shuffles (xor 16, xor 32).
 //   * Waves merge through LDS; a row with one partition writes its output directly, otherwise each
-//     partition writes (m, l, acc) to the workspace and the last one to arrive (device-scope
-//     counter) merges them and resets the counter to zero for the next call.
+//     partition writes (m, l, acc) to the workspace and a second small kernel merges them. (A
+//     last-block-done counter would need device-scope fences, which on gfx950 write back and
+//     invalidate the L2 of the XCD in every workgroup.)
 // fp32 design: one wave per (row, KV head), VALU dot products with wave reductions; kept simple,
 // it serves the fp32 correctness paths.
 #include "ns_common.h"
@@ -45,7 +49,31 @@ struct DecodeCfg<128> {
   static constexpr int NW = 4, PPW = 2;
 };
 
-__device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+// NT/2 dwords holding NT consecutive bf16 of one token row (the V slice a lane owns).
+template <int NW32>
+struct Words {
+  uint32_t w[NW32];
+};
+template <int NW32>
+__device__ __forceinline__ Words<NW32> load_words(const bf16_t* p) {
+  Words<NW32> r;
+  if constexpr (NW32 == 2) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = u.x;
+    r.w[1] = u.y;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    r.w[0] = u.x;
+    r.w[1] = u.y;
+    r.w[2] = u.z;
+    r.w[3] = u.w;
+  }
+  return r;
+}
+
+// (low halves of x, y) and (high halves of x, y) packed into one dword: v_perm_b32 byte selects.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
 template <int HD>
 __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kernel(
@@ -53,21 +81,48 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
     const bf16_t* __restrict__ vp, int64_t s_blk, int64_t s_pos, int64_t s_h, const int32_t* __restrict__ bt,
     int64_t bt_sb, const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G,
     int max_blocks, int num_blocks, float scale_log2, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    uint32_t* __restrict__ counters) {
+    int B_, int nkv_, int n_parts) {
   constexpr int NW = DecodeCfg<HD>::NW, PPW = DecodeCfg<HD>::PPW, PART = NW * PPW;
   constexpr int KS = HD / 32;  // 32-dim k-steps of the QK^T product (8 bf16 per lane per step)
-  constexpr int NT = HD / 16;  // 16-dim output tiles of the PV product
-  constexpr int VROW = HD + 8; // LDS row pitch of the V tile (bf16), padded against bank conflicts
-  const int part = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int nkv = gridDim.y, n_parts = gridDim.x;
+  constexpr int NT = HD / 16;  // 16-row output tiles of the PV product
+  constexpr int VW = NT / 2;   // dwords of a lane's V slice per token
+  // XCD-aware work map. Workgroup L runs on XCD L % 8, and low partitions are live in every row
+  // while high ones only in long rows. With rows = B * n_kv, L = part * rows + k and
+  // row = (k + part) % rows: every partition index is spread over all XCDs, a row's partitions
+  // rotate across XCDs, and live (low) partitions are dispatched first.
+  const int rows = nkv_ * B_;
+  const int L = blockIdx.x;
+  const int part = L / rows;
+  const int row = (L - part * rows + part) % rows;
+  const int b = row / nkv_, g = row - (row / nkv_) * nkv_;
+  const int nkv = nkv_;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int c16 = lane & 15;   // MFMA column: head (QK^T B / output) or token row (A operands)
-  const int r4 = lane >> 4;    // MFMA row group: owns rows / k-values 4*r4 .. 4*r4+3 (8*r4.. for x32)
+  const int c16 = lane & 15;   // MFMA column (head) for B / D; MFMA row for A operands
+  const int r4 = lane >> 4;    // k-group: tokens 4*r4 .. 4*r4+3 (PV), dims 8*r4 .. 8*r4+7 (QK^T)
+  const int p0 = part * PART;
 
+  // ctx, the partition's block ids and Q are independent: issue them together (one latency).
+  // Table entries p < max_blocks are inside the caller's table whatever ctx is.
   const int ctx = ctxl[b];
+  int blk[PPW];
+#pragma unroll
+  for (int i = 0; i < PPW; ++i) {
+    const int p = p0 + w + NW * i;
+    blk[i] = p < max_blocks ? bt[int64_t(b) * bt_sb + p] : -1;
+  }
+  bf16x8_t qf[KS];  // B operand of S^T, k = dims 32s + 8*r4 + e; rows >= G zero
+  {
+    const bool hv = c16 < G;
+    const bf16_t* qrow = q + int64_t(b) * q_sb + int64_t(g * G + (hv ? c16 : 0)) * q_sh;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * r4);
+      if (!hv) u = make_uint4(0u, 0u, 0u, 0u);
+      qf[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
   int n_pages = ctx > 0 ? (ctx + PAGE - 1) / PAGE : 0;
   if (n_pages > max_blocks) n_pages = max_blocks;
-  const int p0 = part * PART;
   if (ctx <= 0) {  // no keys: zeros (the row is invalid; nothing to attend to)
     if (part == 0)
       for (int i = tid; i < G * HD; i += NW * 64)
@@ -76,37 +131,25 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
   }
   if (p0 >= n_pages) return;  // whole workgroup: this partition is past the row's context
   const int n_active = (n_pages + PART - 1) / PART;
-
-  // ---- issue loads: Q (B operand, zero rows >= G), then every K and V fragment of this wave's pages
-  bf16x8_t qf[KS];
-  {
-    const bool hv = c16 < G;
-    const bf16_t* qrow = q + int64_t(b) * q_sb + int64_t(g * G + (hv ? c16 : 0)) * q_sh;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      uint4 u = hv ? *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * r4) : zero4();
-      qf[s] = __builtin_bit_cast(bf16x8_t, u);
-    }
-  }
-  uint4 kf[PPW][KS], vf[PPW][KS];
-  int my_pages = 0;
+  for (int i = 0; i < PPW; ++i)
+    if (p0 + w + NW * i >= n_pages) blk[i] = -1;   // dead page slot: masked below
+
+  uint4 kf[PPW][KS];
+  Words<VW> vr[PPW][4];
+  bool okp[PPW];
 #pragma unroll
   for (int i = 0; i < PPW; ++i) {
-    const int p = p0 + w + NW * i;
-    const bool live = p < n_pages;
-    my_pages += live ? 1 : 0;
-    int blk = live ? bt[int64_t(b) * bt_sb + p] : -1;
-    const bool ok = live && blk >= 0 && blk < num_blocks;
-    const int64_t off = int64_t(ok ? blk : 0) * s_blk + int64_t(c16) * s_pos + int64_t(g) * s_h + 8 * r4;
+    okp[i] = blk[i] >= 0 && blk[i] < num_blocks;
+    const int64_t base = int64_t(okp[i] ? blk[i] : 0) * s_blk + int64_t(g) * s_h;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      kf[i][s] = ok ? *reinterpret_cast<const uint4*>(kp + off + 32 * s) : zero4();
-      vf[i][s] = ok ? *reinterpret_cast<const uint4*>(vp + off + 32 * s) : zero4();
-    }
+    for (int s = 0; s < KS; ++s)
+      kf[i][s] = *reinterpret_cast<const uint4*>(kp + base + int64_t(c16) * s_pos + 32 * s + 8 * r4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vr[i][j] = load_words<VW>(vp + base + int64_t(4 * r4 + j) * s_pos + NT * c16);
   }
-
-  __shared__ __align__(16) bf16_t vtile[NW][PAGE * VROW];
-  bf16_t* vt = vtile[w];
+  // Keep the scheduler from sinking these loads toward their uses (that would serialise the pages).
+  __builtin_amdgcn_sched_barrier(0);
 
   float m_run = -INFINITY, l_run = 0.f;
   float4_t acc[NT];
@@ -115,69 +158,68 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
 
 #pragma unroll
   for (int i = 0; i < PPW; ++i) {
-    if (i < my_pages) {
-      const int p = p0 + w + NW * i;
-      // S^T = K . Q^T : lane holds tokens 4*r4 + j (j = 0..3) of head c16
-      float4_t st = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int p = p0 + w + NW * i;
+    // S^T = K . Q^T : lane holds tokens 4*r4 + j (j = 0..3) of head c16
+    float4_t st = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[i][s]), qf[s], st, 0, 0, 0);
-      float sv[4];
-      float mx = -INFINITY;
+    for (int s = 0; s < KS; ++s)
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[i][s]), qf[s], st, 0, 0, 0);
+    bool valid[4];
+    float sv[4];
+    float mx = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tok = p * PAGE + 4 * r4 + j;
-        sv[j] = tok < ctx ? st[j] * scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sv[j]);
+    for (int j = 0; j < 4; ++j) {
+      valid[j] = okp[i] && (p * PAGE + 4 * r4 + j) < ctx;   // dead pages: p >= n_pages => token >= ctx
+      sv[j] = valid[j] ? st[j] * scale_log2 : -INFINITY;
+      mx = fmaxf(mx, sv[j]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    // -inf - -inf would be NaN: while nothing is unmasked, subtract 0 instead (all weights stay 0)
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    float pv[4], psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pv[j] = exp2f(sv[j] - m_use);
+      psum += pv[j];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    // P^T as the B operand (k = token 4*r4 + j, n = head c16), rounded to bf16
+    short4_t pb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pb[j] = short(f32_to_bf16(pv[j]));
+    // V^T fragments: tile t, row c16 = dim NT*c16 + t, k = token 4*r4 + j. Masked tokens read as 0
+    // (unwritten slots past ctx may hold anything, and 0 * NaN is NaN).
+    const uint32_t m01 = (valid[0] ? 0x0000ffffu : 0u) | (valid[1] ? 0xffff0000u : 0u);
+    const uint32_t m23 = (valid[2] ? 0x0000ffffu : 0u) | (valid[3] ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int wd = t >> 1;
+      uint32_t lo, hi;
+      if ((t & 1) == 0) {
+        lo = pack_lo(vr[i][0].w[wd], vr[i][1].w[wd]);
+        hi = pack_lo(vr[i][2].w[wd], vr[i][3].w[wd]);
+      } else {
+        lo = pack_hi(vr[i][0].w[wd], vr[i][1].w[wd]);
+        hi = pack_hi(vr[i][2].w[wd], vr[i][3].w[wd]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = exp2f(m_run - m_new);
-      float pv[4], psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pv[j] = exp2f(sv[j] - m_new);
-        psum += pv[j];
-      }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t] *= alpha;
-      // P^T as the B operand (k = token 4*r4 + j, n = head c16), rounded to bf16
-      short4_t pb;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pb[j] = short(f32_to_bf16(pv[j]));
-
-      // V page -> LDS (natural [token][dim] layout), then read V^T fragments.
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int s = 0; s < KS; ++s) *reinterpret_cast<uint4*>(vt + c16 * VROW + 32 * s + 8 * r4) = vf[i][s];
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        short4_t va;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tok = p * PAGE + 4 * r4 + j;
-          const bf16_t x = vt[(4 * r4 + j) * VROW + 16 * t + c16];
-          va[j] = short(tok < ctx ? x : bf16_t(0));  // keys past ctx contribute exactly nothing
-        }
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
-      }
+      const short4_t va = __builtin_bit_cast(short4_t, make_uint2(lo & m01, hi & m23));
+      acc[t] *= alpha;
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
     }
   }
   // per-head sum over the 4 lane groups (same running max in all of them)
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 
-  // ---- merge the NW waves through LDS: acc layout [wave][head][dim]
+  // ---- merge the NW waves through LDS: acc layout [wave][head][dim]; lane holds, for tile t and
+  // r = 0..3, head c16 at dim NT*(4*r4 + r) + t.
   constexpr int AROW = HD + 4;
   __shared__ float sm_acc[NW][16 * AROW];
   __shared__ float sm_m[NW][16], sm_l[NW][16];
-  __shared__ int sm_last;
   if (r4 == 0) {
     sm_m[w][c16] = m_run;
     sm_l[w][c16] = l_run;
@@ -185,7 +227,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sm_acc[w][c16 * AROW + 16 * t + 4 * r4 + j] = acc[t][j];
+    for (int r = 0; r < 4; ++r) sm_acc[w][c16 * AROW + NT * (4 * r4 + r) + t] = acc[t][r];
   __syncthreads();
 
   const int64_t bg = int64_t(b) * nkv + g;
@@ -194,10 +236,11 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
     float M = -INFINITY;
 #pragma unroll
     for (int x = 0; x < NW; ++x) M = fmaxf(M, sm_m[x][h]);
+    const float Mu = M == -INFINITY ? 0.f : M;
     float L = 0.f, A = 0.f;
 #pragma unroll
     for (int x = 0; x < NW; ++x) {
-      const float wgt = exp2f(sm_m[x][h] - M);  // waves without pages: m = -inf -> weight 0
+      const float wgt = exp2f(sm_m[x][h] - Mu);  // waves without live pages: m = -inf -> weight 0
       L += wgt * sm_l[x][h];
       A += wgt * sm_acc[x][h * AROW + d];
     }
@@ -211,31 +254,73 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
       }
     }
   }
-  if (n_active == 1) return;
+}
 
-  // ---- cross-partition merge by the last partition to finish
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&counters[bg], 1u);
-    sm_last = (prev == uint32_t(n_active - 1)) ? 1 : 0;
+// Second pass of the split-K decode: for each (row, KV head) whose context spans more than one
+// partition, combine the partitions' (m, l, acc) with weights 2^(m_p - max m) / L. Rows that fit
+// one partition were finished by the first pass and are skipped.
+constexpr int MERGE_MAX_PARTS = 256;  // partitions per row the merge kernel handles
+constexpr int MERGE_BATCH = 8;        // partitions whose loads each thread keeps in flight
+
+template <int HD>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out,
+                                                                 int64_t o_sb, int64_t o_sh, int G, int max_blocks, int n_parts,
+                                                                 const float* __restrict__ ws_acc,
+                                                                 const float* __restrict__ ws_ml) {
+  constexpr int PART = DecodeCfg<HD>::NW * DecodeCfg<HD>::PPW;
+  const int g = blockIdx.x, b = blockIdx.y, nkv = gridDim.x;
+  const int ctx = ctxl[b];
+  int n_pages = ctx > 0 ? (ctx + PAGE - 1) / PAGE : 0;
+  if (n_pages > max_blocks) n_pages = max_blocks;
+  const int n_active = (n_pages + PART - 1) / PART;
+  if (n_active <= 1) return;
+  const int64_t bg = int64_t(b) * nkv + g;
+  const float* ml = ws_ml + bg * n_parts * 32;           // [part][16 heads][m, l]
+  const float* accp = ws_acc + bg * n_parts * (16 * HD);  // [part][16 heads][HD]
+  __shared__ float sm[MERGE_MAX_PARTS][16];               // m, then the merge weight
+  __shared__ float sl[MERGE_MAX_PARTS][16];
+  for (int i = threadIdx.x; i < n_active * 16; i += blockDim.x) {
+    sm[i >> 4][i & 15] = ml[(i >> 4) * 32 + (i & 15) * 2];
+    sl[i >> 4][i & 15] = ml[(i >> 4) * 32 + (i & 15) * 2 + 1];
   }
   __syncthreads();
-  if (!sm_last) return;
-  __threadfence();
-  for (int idx = tid; idx < G * HD; idx += NW * 64) {
-    const int h = idx / HD, d = idx - (idx / HD) * HD;
+  if (threadIdx.x < G) {
+    const int h = threadIdx.x;
     float M = -INFINITY;
-    for (int x = 0; x < n_active; ++x) M = fmaxf(M, ws_ml[((bg * n_parts + x) * 16 + h) * 2]);
-    float L = 0.f, A = 0.f;
-    for (int x = 0; x < n_active; ++x) {
-      const float wgt = exp2f(ws_ml[((bg * n_parts + x) * 16 + h) * 2] - M);
-      L += wgt * ws_ml[((bg * n_parts + x) * 16 + h) * 2 + 1];
-      A += wgt * ws_acc[(bg * n_parts + x) * (16 * HD) + h * HD + d];
-    }
-    out[int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + d] = f32_to_bf16(A / L);
+    for (int x = 0; x < n_active; ++x) M = fmaxf(M, sm[x][h]);
+    float L = 0.f;
+    for (int x = 0; x < n_active; ++x) L += exp2f(sm[x][h] - M) * sl[x][h];
+    const float inv = 1.0f / L;
+    for (int x = 0; x < n_active; ++x) sm[x][h] = exp2f(sm[x][h] - M) * inv;
   }
-  if (tid == 0) counters[bg] = 0u;  // ready for the next call / graph replay
+  __syncthreads();
+  // each thread: 4 consecutive dims of one head; MERGE_BATCH partitions' 16-byte loads in flight
+  for (int idx = threadIdx.x; idx < G * (HD / 4); idx += blockDim.x) {
+    const int h = idx / (HD / 4), d4 = idx - h * (HD / 4);
+    const float* src = accp + h * HD + 4 * d4;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int x0 = 0; x0 < n_active; x0 += MERGE_BATCH) {
+      float4 u[MERGE_BATCH];
+#pragma unroll
+      for (int e = 0; e < MERGE_BATCH; ++e) {
+        const int x = min(x0 + e, n_active - 1);
+        u[e] = *reinterpret_cast<const float4*>(src + int64_t(x) * (16 * HD));
+      }
+#pragma unroll
+      for (int e = 0; e < MERGE_BATCH; ++e) {
+        const float wgt = (x0 + e < n_active) ? sm[min(x0 + e, n_active - 1)][h] : 0.f;
+        a.x += wgt * u[e].x;
+        a.y += wgt * u[e].y;
+        a.z += wgt * u[e].z;
+        a.w += wgt * u[e].w;
+      }
+    }
+    bf16_t* o = out + int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + 4 * d4;
+    o[0] = f32_to_bf16(a.x);
+    o[1] = f32_to_bf16(a.y);
+    o[2] = f32_to_bf16(a.z);
+    o[3] = f32_to_bf16(a.w);
+  }
 }
 
 // fp32: one wave per (row, KV head). Lane owns dims lane and lane + 64 (hd 128).
@@ -307,18 +392,13 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 using namespace ns;
 
-extern "C" size_t ns_decode_counter_bytes(int B, int n_kv_heads) {
-  if (B <= 0 || n_kv_heads <= 0) return 0;
-  return align256(size_t(B) * n_kv_heads * sizeof(uint32_t));
-}
-
 extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype) {
   if (dtype != NS_DTYPE_BF16 || B <= 0 || n_kv_heads <= 0 || max_blocks <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
   const size_t parts = size_t(decode_parts(head_dim, max_blocks));
   if (parts <= 1) return 0;
   const size_t slots = size_t(B) * n_kv_heads * parts;
-  return ns_decode_counter_bytes(B, n_kv_heads) + align256(slots * 16 * 2 * sizeof(float)) +
+  return align256(slots * 16 * 2 * sizeof(float)) +
          align256(slots * 16 * size_t(head_dim) * sizeof(float));
 }
 
@@ -364,10 +444,10 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                  0,
              "paged_attention_decode: q / k_pool / v_pool must be 16-byte aligned");
   const int parts = decode_parts(head_dim, max_blocks);
-  NS_REQUIRE(parts <= 65535, "paged_attention_decode: %d partitions exceed the grid limit", parts);
+  NS_REQUIRE(parts <= MERGE_MAX_PARTS, "paged_attention_decode: %d partitions (table width %d) exceed %d", parts,
+             max_blocks, MERGE_MAX_PARTS);
   float* ws_acc = nullptr;
   float* ws_ml = nullptr;
-  uint32_t* counters = nullptr;
   if (parts > 1) {
     const size_t need = ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype);
     if (workspace == nullptr || workspace_bytes < need) {
@@ -376,24 +456,29 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
       return NS_E_WORKSPACE;
     }
     NS_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "paged_attention_decode: workspace not 256-byte aligned");
-    char* base = static_cast<char*>(workspace);
     const size_t slots = size_t(B) * n_kv_heads * parts;
-    counters = reinterpret_cast<uint32_t*>(base);
-    ws_ml = reinterpret_cast<float*>(base + ns_decode_counter_bytes(B, n_kv_heads));
-    ws_acc = reinterpret_cast<float*>(base + ns_decode_counter_bytes(B, n_kv_heads) +
-                                      align256(slots * 16 * 2 * sizeof(float)));
+    ws_ml = static_cast<float*>(workspace);
+    ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(slots * 16 * 2 * sizeof(float)));
   }
   const float sl2 = scale * LOG2E;
-  const dim3 grid(parts, n_kv_heads, B);
+  const dim3 grid(unsigned(parts) * unsigned(n_kv_heads) * unsigned(B));
   if (head_dim == 64)
     hipLaunchKernelGGL(paged_decode_bf16_kernel<64>, grid, dim3(DecodeCfg<64>::NW * 64), 0, s,
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
-                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, counters);
+                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, B, n_kv_heads, parts);
   else
     hipLaunchKernelGGL(paged_decode_bf16_kernel<128>, grid, dim3(DecodeCfg<128>::NW * 64), 0, s,
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
-                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, counters);
-  return check_launch("paged_attention_decode(bf16)");
+                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, B, n_kv_heads, parts);
+  int st = check_launch("paged_attention_decode(bf16)");
+  if (st != NS_OK || parts <= 1) return st;
+  if (head_dim == 64)
+    hipLaunchKernelGGL(paged_decode_merge_kernel<64>, dim3(n_kv_heads, B), dim3(256), 0, s, context_lens,
+                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, parts, ws_acc, ws_ml);
+  else
+    hipLaunchKernelGGL(paged_decode_merge_kernel<128>, dim3(n_kv_heads, B), dim3(256), 0, s, context_lens,
+                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, parts, ws_acc, ws_ml);
+  return check_launch("paged_attention_decode(bf16 merge)");
 }

@@ -9,8 +9,8 @@ q: [B, n_heads, head_dim] (last dim contiguous); k_pool / v_pool: ONE layer's po
 (padding entries never read); context_lens: int32 [B], including the new token whose K/V must already be
 written. Returns out = torch.empty_like(q) filled with the attention output.
 
-The bf16 kernel splits long contexts across workgroups and merges the partial softmax states in-kernel.
-That merge needs a small device workspace; one per (device, B, n_kv_heads, head_dim, max_blocks) is
+The bf16 kernel splits long contexts across workgroups; a second small kernel merges the partial softmax
+states. That merge needs a small device workspace; one per (device, B, n_kv_heads, head_dim, max_blocks) is
 allocated on first use (outside any graph capture: the graph runners warm up eagerly first) and reused by
 every later call and graph replay. Calls on one stream never overlap, so sharing it is safe.
 """
@@ -25,8 +25,7 @@ _WORKSPACES: dict[tuple, torch.Tensor] = {}
 
 def decode_workspace(device: torch.device, B: int, n_kv_heads: int, head_dim: int, max_blocks: int,
                      dtype: torch.dtype) -> torch.Tensor | None:
-    """The (zero-initialised, self-resetting) split-K workspace for this launch shape, or None if the
-    launch needs none."""
+    """The split-K workspace for this launch shape, or None if the launch needs none."""
     nbytes = _lib.lib().ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, _lib.dtype_code_of(dtype))
     if nbytes == 0:
         return None
@@ -37,7 +36,7 @@ def decode_workspace(device: torch.device, B: int, n_kv_heads: int, head_dim: in
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("paged_attention_decode: first call for this shape happened inside a graph capture; "
                                "run one eager call (warm-up) before capturing")
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

@@ -19,7 +19,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol():
     lib = _lib.load_library()
     names = declared_functions()
-    assert len(names) >= 8
+    assert len(names) >= 7
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
@@ -39,8 +39,7 @@ def test_workspace_sizing():
     assert lib.ns_decode_workspace_bytes(32, 2, 64, 256, 0) == 0          # fp32 path never splits
     n = lib.ns_decode_workspace_bytes(32, 2, 64, 256, 1)
     slots = 32 * 2 * 16
-    assert n >= slots * 16 * (64 + 2) * 4 + 32 * 2 * 4
-    assert lib.ns_decode_counter_bytes(32, 2) == 256
+    assert n >= slots * 16 * (64 + 2) * 4
 
 
 def test_invalid_arguments_are_rejected_on_the_host():
