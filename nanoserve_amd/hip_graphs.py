@@ -1,0 +1,266 @@
+"""hipGraph runners for the decode loop (torch.cuda.CUDAGraph records hipGraphs on ROCm).
+
+DecodeGraphRunner — one graph per batch bucket for pure-decode steps; contract of
+nanoserve/cuda_graphs.py:42-126:
+  * buckets (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128); a batch of n replays the smallest bucket >= n;
+  * inputs live in static device buffers overwritten before each replay (tokens, positions, slots int64;
+    block tables int32 [Bmax, W]; context lengths int32), W = ceil(max_seq_len / block_size);
+  * padding rows use token 0, slot garbage_block * block_size, table row [garbage_block, 0, ...] and
+    ctx 1: they write and read only the reserved garbage block;
+  * capture is lazy (first use of a bucket) after two eager warm-ups on a shared side stream, and every
+    graph shares one memory pool; run() returns a view of the graph's logits, valid until the next replay.
+Every capture and replay runs under torch.inference_mode (as forward_batch does): the graph-safe RNG
+state torch registers at capture must be created and updated in one mode. All HIP kernels take the
+capture stream from torch and allocate nothing, so the whole step — embedding,
+28 layers of GEMMs / fused ops / split-K attention, final norm and LM head — is one graph launch.
+
+PiecewiseGraphRunner — mixed prefill + decode steps (nanoserve/cuda_graphs.py:151-259): per token
+bucket, L+1 graph pieces (embed + layer 0 _pre; layer j-1 _post + layer j _pre; last _post + final
+norm) with attention run eagerly between them through the same HIP kernels.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from nanoserve_amd.kv_cache import PagedKVCache
+from nanoserve_amd.model import DecodeMeta, Qwen2Model, SeqInput
+
+BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128)
+
+_SIDE_STREAM = None
+
+
+def _capture_stream() -> torch.cuda.Stream:
+    """One warm-up stream for every capture in the process (default priority)."""
+    global _SIDE_STREAM
+    if _SIDE_STREAM is None:
+        _SIDE_STREAM = torch.cuda.Stream()
+    return _SIDE_STREAM
+
+
+class DecodeGraphRunner:
+    def __init__(self, model: Qwen2Model, pool: PagedKVCache, max_seq_len: int, max_batch: int = BUCKETS[-1]):
+        self.model, self.pool = model, pool
+        self.buckets = [b for b in BUCKETS if b <= max_batch]
+        self.max_bucket = self.buckets[-1]
+        self.max_blocks = math.ceil(max_seq_len / pool.block_size)
+        self.garbage_block = pool.allocator.allocate()
+        dev, mb = model.device, self.max_bucket
+        self.tokens = torch.zeros(mb, dtype=torch.long, device=dev)
+        self.positions = torch.zeros(mb, dtype=torch.long, device=dev)
+        self.slots = torch.zeros(mb, dtype=torch.long, device=dev)
+        self.block_tables = torch.zeros(mb, self.max_blocks, dtype=torch.int32, device=dev)
+        self.context_lens = torch.ones(mb, dtype=torch.int32, device=dev)
+        self.token_idx = torch.arange(mb, device=dev)
+        # pinned host staging: one H2D copy per buffer per step
+        self._h_tokens = torch.zeros(mb, dtype=torch.long, pin_memory=True)
+        self._h_positions = torch.zeros(mb, dtype=torch.long, pin_memory=True)
+        self._h_slots = torch.zeros(mb, dtype=torch.long, pin_memory=True)
+        self._h_tables = torch.zeros(mb, self.max_blocks, dtype=torch.int32, pin_memory=True)
+        self._h_lens = torch.ones(mb, dtype=torch.int32, pin_memory=True)
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.outputs: dict[int, torch.Tensor] = {}
+        self.mempool = None
+        self._reset_to_padding()
+
+    @property
+    def captured_buckets(self) -> list[int]:
+        return sorted(self.graphs)
+
+    def bucket_for(self, n: int) -> int | None:
+        return next((b for b in self.buckets if b >= n), None)
+
+    def _reset_to_padding(self) -> None:
+        self.tokens.zero_()
+        self.positions.zero_()
+        self.slots.fill_(self.garbage_block * self.pool.block_size)
+        self.block_tables.zero_()
+        self.block_tables[:, 0] = self.garbage_block
+        self.context_lens.fill_(1)
+
+    def _forward(self, B: int) -> torch.Tensor:
+        meta = DecodeMeta(self.token_idx[:B], self.block_tables[:B], self.context_lens[:B], all_rows=True)
+        seqs = [SeqInput(1, ctx_len=1, use_kernel=True)] * B
+        return self.model.forward_batch(self.tokens[:B], self.positions[:B], seqs, logits="all", paged=self.pool,
+                                        slot_mapping=self.slots[:B], decode_meta=meta)
+
+    def _capture(self, B: int) -> None:
+        # warm-up and capture run on padding inputs only, so they cannot overwrite real K/V
+        self._reset_to_padding()
+        side = _capture_stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._forward(B)
+        torch.cuda.current_stream().wait_stream(side)
+        if self.mempool is None:
+            self.mempool = torch.cuda.graph_pool_handle()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self.mempool):
+            out = self._forward(B)
+        self.graphs[B], self.outputs[B] = graph, out
+
+    def stage(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
+              context_lens: list[int]) -> int:
+        """Write one step's inputs into the static buffers (padding rows point at the garbage block);
+        returns the bucket."""
+        n = len(tokens)
+        B = self.bucket_for(n)
+        if B is None:
+            raise ValueError(f"batch of {n} exceeds the largest graph bucket ({self.max_bucket})")
+        W = self.max_blocks
+        g = self.garbage_block
+        pad = B - n
+        for t in block_tables:
+            if len(t) > W:
+                raise ValueError(f"block table of {len(t)} blocks exceeds the graph width {W} (max_seq_len)")
+        ht, hp, hs, hb, hl = self._h_tokens, self._h_positions, self._h_slots, self._h_tables, self._h_lens
+        ht[:B] = torch.tensor(tokens + [0] * pad, dtype=torch.long)
+        hp[:B] = torch.tensor(positions + [0] * pad, dtype=torch.long)
+        hs[:B] = torch.tensor(slots + [g * self.pool.block_size] * pad, dtype=torch.long)
+        hl[:B] = torch.tensor(context_lens + [1] * pad, dtype=torch.int32)
+        pad_row = [g] + [0] * (W - 1)
+        hb[:B] = torch.tensor([t + [0] * (W - len(t)) for t in block_tables] + [pad_row] * pad, dtype=torch.int32)
+        self.tokens[:B].copy_(ht[:B], non_blocking=True)
+        self.positions[:B].copy_(hp[:B], non_blocking=True)
+        self.slots[:B].copy_(hs[:B], non_blocking=True)
+        self.block_tables[:B].copy_(hb[:B], non_blocking=True)
+        self.context_lens[:B].copy_(hl[:B], non_blocking=True)
+        return B
+
+    @torch.inference_mode()
+    def run(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
+            context_lens: list[int]) -> torch.Tensor:
+        """One decode step for n requests via the bucket's graph; logits [n, vocab] (a view of the graph's
+        output buffer, valid until the next replay of that bucket)."""
+        n = len(tokens)
+        B = self.bucket_for(n)
+        if B is None:
+            raise ValueError(f"batch of {n} exceeds the largest graph bucket ({self.max_bucket})")
+        if B not in self.graphs:
+            self._capture(B)
+        torch.cuda.current_stream().synchronize()   # the pinned staging buffers are reused every step
+        self.stage(tokens, positions, slots, block_tables, context_lens)
+        self.graphs[B].replay()
+        return self.outputs[B][:n]
+
+    @torch.inference_mode()
+    def capture_all(self, max_batch: int) -> None:
+        """Capture every bucket a batch of up to max_batch requests can use."""
+        top = self.bucket_for(min(max_batch, self.max_bucket))
+        for B in self.buckets:
+            if B <= top and B not in self.graphs:
+                self._capture(B)
+
+
+PIECEWISE_CAP = 512
+
+
+def piecewise_buckets(max_tokens: int, cap: int = PIECEWISE_CAP) -> list[int]:
+    """Token-count buckets for mixed steps: every 16 up to 256, then every 32, up to min(max_tokens, cap)."""
+    top = min(max_tokens, cap)
+    grid = list(range(16, 256, 16)) + list(range(256, cap + 1, 32))
+    return [b for b in grid if b < top] + [top]
+
+
+class PiecewiseGraphRunner:
+    def __init__(self, model: Qwen2Model, pool: PagedKVCache, garbage_block: int, max_tokens: int = PIECEWISE_CAP,
+                 buckets: list[int] | None = None):
+        self.model, self.pool, self.garbage_block = model, pool, garbage_block
+        self.buckets = sorted(buckets) if buckets else piecewise_buckets(max_tokens)
+        self.max_tokens = self.buckets[-1]
+        cfg, dev, dt, Tm = model.cfg, model.device, model.dtype, self.max_tokens
+        self.gslot = garbage_block * pool.block_size
+        self.tokens = torch.zeros(Tm, dtype=torch.long, device=dev)
+        self.positions = torch.zeros(Tm, dtype=torch.long, device=dev)
+        self.slots = torch.full((Tm,), self.gslot, dtype=torch.long, device=dev)
+
+        def z(*shape):
+            return torch.zeros(1, Tm, *shape, dtype=dt, device=dev)
+
+        self.x = z(cfg.hidden_size)
+        self.q, self.k, self.v = z(cfg.n_heads, cfg.head_dim), z(cfg.n_kv_heads, cfg.head_dim), z(cfg.n_kv_heads, cfg.head_dim)
+        self.o = z(cfg.n_heads * cfg.head_dim)
+        self.cos, self.sin = z(cfg.head_dim), z(cfg.head_dim)
+        self.graphs: dict[int, list[torch.cuda.CUDAGraph]] = {}
+        self.mempool = None
+
+    @property
+    def captured_buckets(self) -> list[int]:
+        return sorted(self.graphs)
+
+    def bucket_for(self, n: int) -> int | None:
+        return next((b for b in self.buckets if b >= n), None)
+
+    def _piece(self, j: int, B: int) -> None:
+        m, L = self.model, self.model.cfg.n_layers
+        if j == 0:
+            x = torch.nn.functional.embedding(self.tokens[:B], m.embed)[None]
+            cos, sin = m.rope(self.positions[:B])
+            self.cos[:, :B].copy_(cos)
+            self.sin[:, :B].copy_(sin)
+        else:
+            x = m._post(j - 1, self.x[:, :B], self.o[:, :B])
+        if j < L:
+            q, k, v = m._pre(j, x, self.cos[:, :B], self.sin[:, :B], self.pool, self.slots[:B])
+            self.q[:, :B].copy_(q)
+            self.k[:, :B].copy_(k)
+            self.v[:, :B].copy_(v)
+            self.x[:, :B].copy_(x)
+        else:
+            self.x[:, :B].copy_(m.final_norm(x))
+
+    def _capture(self, B: int) -> None:
+        self.tokens.zero_()
+        self.positions.zero_()
+        self.slots.fill_(self.gslot)
+        L = self.model.cfg.n_layers
+        side = _capture_stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                for j in range(L + 1):
+                    self._piece(j, B)
+        torch.cuda.current_stream().wait_stream(side)
+        if self.mempool is None:
+            self.mempool = torch.cuda.graph_pool_handle()
+        graphs = []
+        for j in range(L + 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self.mempool):
+                self._piece(j, B)
+            graphs.append(g)
+        self.graphs[B] = graphs
+
+    @torch.inference_mode()
+    def capture_all(self) -> None:
+        for B in reversed(self.buckets):   # largest first: its temporaries carve the shared pool once
+            if B not in self.graphs:
+                self._capture(B)
+
+    @torch.inference_mode()
+    def run(self, tokens: list[int], positions: list[int], slots: list[int], seqs: list[SeqInput],
+            decode_meta: DecodeMeta | None, rows: torch.Tensor | None = None) -> torch.Tensor:
+        """One mixed step of T tokens: logits of each sequence's last token, or of `rows` if given."""
+        T = len(tokens)
+        B = self.bucket_for(T)
+        if B is None:
+            raise ValueError(f"step of {T} tokens exceeds the largest piecewise bucket ({self.max_tokens})")
+        if B not in self.graphs:
+            self._capture(B)
+        pad = B - T
+        self.tokens[:B].copy_(torch.tensor(tokens + [0] * pad))
+        self.positions[:B].copy_(torch.tensor(positions + [0] * pad))
+        self.slots[:B].copy_(torch.tensor(slots + [self.gslot] * pad))
+        m, graphs = self.model, self.graphs[B]
+        q, k, v, o = self.q[:, :T], self.k[:, :T], self.v[:, :T], self.o[:, :T]
+        m._rows_cache = None
+        slot_view = self.slots[:T]
+        for i in range(m.cfg.n_layers):
+            graphs[i].replay()
+            m._attend(i, q, k, v, seqs, self.pool, decode_meta, out=o, slot_mapping=slot_view)
+        graphs[-1].replay()
+        m._rows_cache = None
+        return m.lm_head_rows(self.x[:, :T], seqs, "last" if rows is None else rows)

@@ -1,0 +1,360 @@
+"""Qwen2 decoder forward on the MI355X: HIP kernels for every token-wise op and for attention.
+
+Interface follows nanoserve/model.py (ModelConfig :26-56, LayerWeights :67-114, SeqInput :117-129,
+DecodeMeta :132-137, Qwen2Model :154-367) so the engine, scheduler, KV manager and graph runners call it
+the same way. The math of one layer on N flattened tokens (nanoserve/model.py:223-260, fused path):
+
+    h      = rms_norm(x, ln1)                                  HIP  (kernels/fused.py)
+    qkv    = h @ [Wq;Wk;Wv]^T + [bq;bk;bv]                     GEMM (kernels/linear.py)
+    q,k,v  = rope_qkv(qkv, cos, sin) + K/V stored at slots     HIP
+    o      = paged attention over each row's pages             HIP  (kernels/paged_attention.py)
+    h, x   = rms_norm(o @ Wo^T, ln2, residual=x)               GEMM + HIP
+    x      = x + silu_mul(h @ [Wg;Wu]^T) @ Wd^T                GEMM + HIP + GEMM
+
+Attention: one-token decode rows (DecodeMeta) and the tokens of prefill / chunked-prefill rows all go
+through the paged kernel. Prefill token j of a sequence with ctx_len cached tokens is a row whose context
+is ctx_len + j + 1 tokens of that sequence's table: exactly the causal offset mask of
+nanoserve/model.py:292-309, with K/V read in place from the pages rope_qkv has just written.
+
+Only the HIP path exists here: a CPU tensor, the contiguous cache or a missing kernel library raise. The
+unfused PyTorch restatement (the CPU oracle used by the tests) lives outside this package.
+"""
+from __future__ import annotations
+
+import copy
+import json
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    vocab_size: int
+    hidden_size: int
+    n_layers: int
+    n_heads: int            # query heads
+    n_kv_heads: int         # key/value heads (GQA)
+    head_dim: int
+    intermediate_size: int  # MLP width
+    rope_theta: float
+    rms_norm_eps: float
+    tie_word_embeddings: bool
+
+    @classmethod
+    def from_hf_config(cls, d: dict) -> "ModelConfig":
+        rope_theta = d.get("rope_theta") or (d.get("rope_parameters") or {}).get("rope_theta")
+        return cls(vocab_size=d["vocab_size"], hidden_size=d["hidden_size"], n_layers=d["num_hidden_layers"],
+                   n_heads=d["num_attention_heads"], n_kv_heads=d["num_key_value_heads"],
+                   head_dim=d.get("head_dim") or d["hidden_size"] // d["num_attention_heads"],
+                   intermediate_size=d["intermediate_size"], rope_theta=float(rope_theta),
+                   rms_norm_eps=d["rms_norm_eps"], tie_word_embeddings=d.get("tie_word_embeddings", False))
+
+    @classmethod
+    def from_pretrained(cls, folder: str) -> "ModelConfig":
+        return cls.from_hf_config(json.loads((_local_folder(folder) / "config.json").read_text()))
+
+    def kv_bytes_per_token(self, dtype: torch.dtype) -> int:
+        """KV memory of one token: every layer stores one K and one V vector per KV head."""
+        return self.n_layers * 2 * self.n_kv_heads * self.head_dim * torch.finfo(dtype).bits // 8
+
+
+# Architectures of the benchmark configurations (Qwen2.5 shapes; weights are random-init).
+QWEN25_0_5B = ModelConfig(vocab_size=151936, hidden_size=896, n_layers=24, n_heads=14, n_kv_heads=2, head_dim=64,
+                          intermediate_size=4864, rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True)
+QWEN25_1_5B = ModelConfig(vocab_size=151936, hidden_size=1536, n_layers=28, n_heads=12, n_kv_heads=2, head_dim=128,
+                          intermediate_size=8960, rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True)
+QWEN25_3B = ModelConfig(vocab_size=151936, hidden_size=2048, n_layers=36, n_heads=16, n_kv_heads=2, head_dim=128,
+                        intermediate_size=11008, rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True)
+
+
+def _local_folder(name: str) -> Path:
+    p = Path(name)
+    if not p.is_dir():
+        raise FileNotFoundError(f"{name}: a local model folder (config.json + *.safetensors) is required; "
+                                "this build never downloads")
+    return p
+
+
+@dataclass
+class LayerWeights:
+    ln1: torch.Tensor
+    q_w: torch.Tensor
+    q_b: torch.Tensor
+    k_w: torch.Tensor
+    k_b: torch.Tensor
+    v_w: torch.Tensor
+    v_b: torch.Tensor
+    o_w: torch.Tensor
+    ln2: torch.Tensor
+    gate_w: torch.Tensor
+    up_w: torch.Tensor
+    down_w: torch.Tensor
+    qkv_w: torch.Tensor | None = None     # merged [q; k; v] rows (per-matrix fields become views)
+    qkv_b: torch.Tensor | None = None
+    gate_up_w: torch.Tensor | None = None  # merged [gate; up] rows
+
+    HF_NAMES = {
+        "ln1": "input_layernorm.weight",
+        "q_w": "self_attn.q_proj.weight", "q_b": "self_attn.q_proj.bias",
+        "k_w": "self_attn.k_proj.weight", "k_b": "self_attn.k_proj.bias",
+        "v_w": "self_attn.v_proj.weight", "v_b": "self_attn.v_proj.bias",
+        "o_w": "self_attn.o_proj.weight",
+        "ln2": "post_attention_layernorm.weight",
+        "gate_w": "mlp.gate_proj.weight", "up_w": "mlp.up_proj.weight", "down_w": "mlp.down_proj.weight",
+    }
+
+    @classmethod
+    def from_state_dict(cls, sd: dict, i: int) -> "LayerWeights":
+        return cls(**{f: sd[f"model.layers.{i}.{hf}"] for f, hf in cls.HF_NAMES.items()})
+
+    def merge(self) -> None:
+        """Merged QKV and gate/up matrices (one GEMM each); the per-matrix fields become row views of them,
+        so nothing is stored twice (nanoserve/model.py:101-114)."""
+        if self.qkv_w is not None:
+            return
+        nq, nk, ng = self.q_w.shape[0], self.k_w.shape[0], self.gate_w.shape[0]
+        self.qkv_w = torch.cat([self.q_w, self.k_w, self.v_w])
+        self.q_w, self.k_w, self.v_w = self.qkv_w[:nq], self.qkv_w[nq:nq + nk], self.qkv_w[nq + nk:]
+        self.qkv_b = torch.cat([self.q_b, self.k_b, self.v_b])
+        self.q_b, self.k_b, self.v_b = self.qkv_b[:nq], self.qkv_b[nq:nq + nk], self.qkv_b[nq + nk:]
+        self.gate_up_w = torch.cat([self.gate_w, self.up_w])
+        self.gate_w, self.up_w = self.gate_up_w[:ng], self.gate_up_w[ng:]
+
+
+@dataclass
+class SeqInput:
+    """One sequence's slice of a batched step (nanoserve/model.py:117-129). Paged only: `block_table` =
+    this request's block ids (int tensor on the device; may be None for a fresh prefill, whose pages are
+    then read off the slot mapping), `ctx_len` = tokens already stored before this step."""
+    n_tokens: int
+    cache: object | None = None
+    block_table: torch.Tensor | None = None
+    ctx_len: int = 0
+    use_kernel: bool = False      # a one-token decode handled through DecodeMeta
+
+
+@dataclass
+class DecodeMeta:
+    """Built once per step for all one-token decode rows (nanoserve/model.py:132-137)."""
+    token_idx: torch.Tensor       # [Bd] positions of their tokens in the flattened batch
+    block_tables: torch.Tensor    # [Bd, max_blocks] int32
+    context_lens: torch.Tensor    # [Bd] int32, including this step's token
+    all_rows: bool = False        # token_idx is arange(N): rows map 1:1 to the step's tokens (no gather)
+
+
+def random_state_dict(cfg: ModelConfig, seed: int = 0, dtype: torch.dtype = torch.bfloat16,
+                      device: str | torch.device = "cpu") -> dict[str, torch.Tensor]:
+    """Random-init Qwen2 weights under HF names, drawn on the CPU in fp32 with one seeded generator in HF
+    order (embed_tokens first, then each layer's tensors in LayerWeights.HF_NAMES order, then the final
+    norm): matrices and biases ~ N(0, 0.02), norm weights = 1, LM head tied to the embedding. Identical
+    values for the CPU oracle and the GPU, whatever the dtype."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+
+    def normal(*shape):
+        t = torch.empty(*shape, dtype=torch.float32)
+        t.normal_(0.0, 0.02, generator=g)
+        return t.to(dtype).to(device)
+
+    H, I, hd = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    sd = {"model.embed_tokens.weight": normal(cfg.vocab_size, H)}
+    shapes = {"q_w": (cfg.n_heads * hd, H), "q_b": (cfg.n_heads * hd,), "k_w": (cfg.n_kv_heads * hd, H),
+              "k_b": (cfg.n_kv_heads * hd,), "v_w": (cfg.n_kv_heads * hd, H), "v_b": (cfg.n_kv_heads * hd,),
+              "o_w": (H, cfg.n_heads * hd), "gate_w": (I, H), "up_w": (I, H), "down_w": (H, I)}
+    for i in range(cfg.n_layers):
+        for field, hf in LayerWeights.HF_NAMES.items():
+            name = f"model.layers.{i}.{hf}"
+            if field in ("ln1", "ln2"):
+                sd[name] = torch.ones(H, dtype=dtype, device=device)
+            else:
+                sd[name] = normal(*shapes[field])
+    sd["model.norm.weight"] = torch.ones(H, dtype=dtype, device=device)
+    if not cfg.tie_word_embeddings:
+        sd["lm_head.weight"] = normal(cfg.vocab_size, H)
+    return sd
+
+
+class Qwen2Model:
+    """Weights + forward; no nn.Module (nothing is trained)."""
+
+    fused = True
+
+    def __init__(self, cfg: ModelConfig, state_dict: dict[str, torch.Tensor]):
+        self.cfg = cfg
+        self.embed = state_dict["model.embed_tokens.weight"]
+        self.norm = state_dict["model.norm.weight"]
+        self.lm_head = self.embed if cfg.tie_word_embeddings else state_dict["lm_head.weight"]
+        self.layers = [LayerWeights.from_state_dict(state_dict, i) for i in range(cfg.n_layers)]
+        for layer in self.layers:
+            layer.merge()
+        self.device = self.embed.device
+        self.dtype = self.embed.dtype
+        # RoPE inverse frequencies, fp32, computed on the CPU like HF, then moved
+        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float) / cfg.head_dim))
+        self.inv_freq = inv.to(self.device)
+
+    @classmethod
+    def from_pretrained(cls, folder: str, device: str | torch.device = "cuda",
+                        dtype: torch.dtype = torch.bfloat16) -> "Qwen2Model":
+        """Load a local HF folder (config.json + *.safetensors); converts one tensor at a time."""
+        from safetensors.torch import load_file
+        path = _local_folder(folder)
+        cfg = ModelConfig.from_pretrained(str(path))
+        raw: dict[str, torch.Tensor] = {}
+        for f in sorted(path.glob("*.safetensors")):
+            raw.update(load_file(str(f), device="cpu"))
+        sd = {k: raw.pop(k).to(dtype).to(device) for k in list(raw)}
+        return cls(cfg, sd)
+
+    def with_fused_ops(self) -> "Qwen2Model":
+        """The HIP path is always fused; returns a shallow copy sharing the weights (reference API)."""
+        m = copy.copy(self)
+        m.fused = True
+        return m
+
+    def named_weights(self) -> dict[str, torch.Tensor]:
+        out = {"model.embed_tokens.weight": self.embed, "model.norm.weight": self.norm}
+        if not self.cfg.tie_word_embeddings:
+            out["lm_head.weight"] = self.lm_head
+        for i, layer in enumerate(self.layers):
+            for field, hf in LayerWeights.HF_NAMES.items():
+                out[f"model.layers.{i}.{hf}"] = getattr(layer, field)
+        return out
+
+    # ---------------------------------------------------------------------------------------- pieces
+    def _require_gpu(self) -> None:
+        if self.device.type != "cuda":
+            raise ValueError("Qwen2Model runs the HIP kernels: put the weights on the GPU")
+
+    def final_norm(self, x: torch.Tensor) -> torch.Tensor:
+        from nanoserve_amd.kernels.fused import rms_norm
+        return rms_norm(x, self.norm, self.cfg.rms_norm_eps)
+
+    def rope(self, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """cos/sin [1, T, head_dim] in the model dtype (nanoserve/model.py:212-217)."""
+        freqs = positions[None, :, None].float() * self.inv_freq.to(device=positions.device, dtype=torch.float)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        return emb.cos().to(self.dtype), emb.sin().to(self.dtype)
+
+    def _pre(self, i: int, x: torch.Tensor, cos, sin, paged=None, slot_mapping=None):
+        """RMSNorm, merged QKV GEMM, RoPE + paged K/V write. x [1, N, H] -> q [1,N,nh,hd], k/v [1,N,nkv,hd]."""
+        from nanoserve_amd.kernels.fused import rms_norm, rope_qkv
+        from nanoserve_amd.kernels.linear import linear
+        layer, cfg = self.layers[i], self.cfg
+        qkv = linear(rms_norm(x, layer.ln1, cfg.rms_norm_eps)[0], layer.qkv_w, layer.qkv_b)
+        q, k, v = rope_qkv(qkv, cos[0], sin[0], cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                           paged.k[i] if paged is not None else None,
+                           paged.v[i] if paged is not None else None, slot_mapping)
+        return q[None], k[None], v[None]
+
+    def _post(self, i: int, x: torch.Tensor, o: torch.Tensor) -> torch.Tensor:
+        """o_proj + residual (fused into the norm), RMSNorm, SwiGLU MLP + residual."""
+        from nanoserve_amd.kernels.fused import rms_norm, silu_mul
+        from nanoserve_amd.kernels.linear import linear
+        layer = self.layers[i]
+        h, x = rms_norm(linear(o[0], layer.o_w)[None], layer.ln2, self.cfg.rms_norm_eps, residual=x)
+        return x + linear(silu_mul(linear(h[0], layer.gate_up_w)), layer.down_w)[None]
+
+    def _attend(self, i: int, q, k, v, seqs: list[SeqInput], paged=None, decode_meta=None,
+                out: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
+        """Attention of layer i for the step's flattened tokens; q [1, N, nh, hd]. Returns [1, N, nh*hd]
+        (written into `out` if given). Decode rows come from decode_meta; every other sequence's tokens are
+        rows with causal-offset contexts (see the module docstring)."""
+        from nanoserve_amd.kernels.paged_attention import paged_attention_decode
+        if paged is None:
+            raise ValueError("the HIP attention path reads the paged KV cache: pass `paged`")
+        N, nh, hd = q.shape[1], q.shape[2], q.shape[3]
+        scale = hd ** -0.5
+        if decode_meta is not None and decode_meta.all_rows:
+            o = paged_attention_decode(q[0], paged.k[i], paged.v[i], decode_meta.block_tables,
+                                       decode_meta.context_lens, scale)
+            if out is None:
+                return o.view(1, N, nh * hd)
+            out[0].copy_(o.view(N, nh * hd))
+            return out
+        o_all = out if out is not None else torch.empty(1, N, nh * hd, device=q.device, dtype=q.dtype)
+        if decode_meta is not None:
+            o_dec = paged_attention_decode(q[0][decode_meta.token_idx], paged.k[i], paged.v[i],
+                                           decode_meta.block_tables, decode_meta.context_lens, scale)
+            o_all[0].index_copy_(0, decode_meta.token_idx, o_dec.reshape(o_dec.shape[0], -1))
+        rows = self._prefill_rows(seqs, paged, slot_mapping)
+        if rows is not None:
+            idx, tables, lens = rows
+            o_pf = paged_attention_decode(q[0][idx], paged.k[i], paged.v[i], tables, lens, scale)
+            o_all[0].index_copy_(0, idx, o_pf.reshape(o_pf.shape[0], -1))
+        return o_all
+
+    def _prefill_rows(self, seqs: list[SeqInput], paged, slot_mapping):
+        """(token index, block tables, context lengths) of every non-decode token of the step, one row per
+        token: token j of a sequence with ctx_len cached tokens sees ctx_len + j + 1 tokens. Cached per step
+        (all layers share it) on the SeqInput list object."""
+        cache = getattr(self, "_rows_cache", None)
+        if cache is not None and cache[0] is seqs and cache[1] is slot_mapping:
+            return cache[2]
+        dev, bs = self.device, paged.block_size
+        idx_parts, lens_parts, tabs = [], [], []
+        start = 0
+        for s in seqs:
+            T = s.n_tokens
+            if not s.use_kernel and T > 0:
+                n_pages = -(-(s.ctx_len + T) // bs)
+                if s.block_table is not None:
+                    bt = s.block_table.to(device=dev, dtype=torch.int32)[:n_pages]
+                elif s.ctx_len == 0:
+                    if slot_mapping is None:
+                        raise ValueError("a fresh prefill without block_table needs slot_mapping")
+                    bt = (slot_mapping[start:start + T:bs] // bs).to(torch.int32)
+                else:
+                    raise ValueError("a continuation chunk (ctx_len > 0) needs its block_table")
+                idx_parts.append(torch.arange(start, start + T, device=dev))
+                lens_parts.append(torch.arange(s.ctx_len + 1, s.ctx_len + T + 1, device=dev, dtype=torch.int32))
+                tabs.append((bt, T))
+            start += T
+        if not idx_parts:
+            rows = None
+        else:
+            width = max(bt.shape[0] for bt, _ in tabs)
+            tables = torch.cat([F.pad(bt, (0, width - bt.shape[0]))[None].expand(T, width) for bt, T in tabs])
+            rows = (torch.cat(idx_parts), tables.contiguous(), torch.cat(lens_parts))
+        self._rows_cache = (seqs, slot_mapping, rows)
+        return rows
+
+    @torch.inference_mode()
+    def forward_batch(self, token_ids: torch.Tensor, positions: torch.Tensor, seqs: list[SeqInput],
+                      logits="last", paged=None, slot_mapping: torch.Tensor | None = None,
+                      decode_meta: DecodeMeta | None = None) -> torch.Tensor:
+        """One forward pass over several sequences (prefilling, continuing a chunked prefill on a cached
+        context, or decoding one token). token_ids/positions: [N] in `seqs` order. Returns logits
+        [len(seqs), vocab] for each sequence's last token ("last"), [N, vocab] ("all"), or the rows of an
+        index tensor."""
+        self._require_gpu()
+        if paged is None:
+            raise ValueError("the HIP path needs the paged KV cache (`paged` + `slot_mapping`)")
+        assert sum(s.n_tokens for s in seqs) == token_ids.shape[0], "seqs must cover token_ids exactly"
+        self._rows_cache = None
+        x = F.embedding(token_ids, self.embed)[None]
+        cos, sin = self.rope(positions)
+        for i in range(self.cfg.n_layers):
+            q, k, v = self._pre(i, x, cos, sin, paged, slot_mapping)
+            x = self._post(i, x, self._attend(i, q, k, v, seqs, paged, decode_meta, slot_mapping=slot_mapping))
+        self._rows_cache = None
+        return self.lm_head_rows(self.final_norm(x), seqs, logits)
+
+    def lm_head_rows(self, x: torch.Tensor, seqs: list[SeqInput], logits="last") -> torch.Tensor:
+        """Final-normed hidden states [1, N, H] -> logits of the requested rows."""
+        from nanoserve_amd.kernels.linear import linear
+        if isinstance(logits, torch.Tensor):
+            x = x[:, logits, :]
+        elif logits == "last":
+            if len(seqs) == 1:
+                x = x[:, -1:, :]
+            else:
+                ends = torch.tensor([s.n_tokens for s in seqs], device=x.device).cumsum(0) - 1
+                x = x[:, ends, :]
+        return linear(x[0].contiguous(), self.lm_head)
+
+    def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, cache=None, logits: str = "last"):
+        raise NotImplementedError("the single-sequence contiguous-cache API (M1) is not part of the HIP path; "
+                                  "use forward_batch with a PagedKVCache")
