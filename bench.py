@@ -1,0 +1,215 @@
+"""Headline benchmark: decode tokens/s of the HIP decode loop on one MI355X, plus the paged-attention
+roofline and the CPU oracle timed beside it.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Workload: Qwen2.5-1.5B-architecture decoder, random-init bf16 weights (N(0, 0.02),
+norms 1, tied embeddings), 32 sequences whose 1024-token random prompts are prefilled into the paged KV
+cache through the engine (not timed), then W untimed and K timed greedy decode steps at batch 32. A step
+is one LLMEngine.step(): schedule, stage inputs, replay the bucket-32 hipGraph (embedding, 28 layers,
+final norm, LM head), argmax + the step's single device->host sync, KV commit. value = 32 * K / (time of
+the K steps); inputs and weights are resident in HBM before timing starts.
+
+roofline: the paged-attention decode op alone at BASELINE config 2 (B=32, 14 q / 2 kv heads, hd 64,
+ctx U[512, 4096], 16-token pages scattered over a 64k-block pool, 8 disjoint draws used round-robin so the
+256 MB Infinity Cache cannot serve them). Algorithmic bytes per call = sum_b ctx_b*n_kv*hd*2(K,V)*2B +
+Q and O (2*B*n_heads*hd*2B) + block-table entries read (4B per page) + context lengths (4B per row);
+duration from HIP events bracketing each call (split-K pass + merge pass) on the launch stream.
+step_roofline: the decode step's algorithmic HBM bytes (every weight once, the KV cache of every row, the
+new K/V and the logits) over the measured step time.
+
+cpu_baseline: the CPU oracle (oracle/model.py, the reference algorithm restated in PyTorch) on this
+host's cores: one fp32 decode step of the same 1.5B shape at batch 32 with 1024-token contexts
+(random-valued caches), median of 3 timed steps after 1 warm-up.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gated_event_times(fn, n: int) -> list[float]:
+    """Duration (ms) of each of n calls of fn, from events recorded right before and after it. A sleep
+    kernel first keeps the GPU behind the host, so no call waits on Python to be enqueued."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2e8))
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return [e0.elapsed_time(e1) for e0, e1 in evs]
+
+
+def paged_attention_roofline() -> dict:
+    from nanoserve_amd.kernels.paged_attention import paged_attention_decode
+    B, NH, NKV, HD, NB, W, R = 32, 14, 2, 64, 65536, 256, 8
+    g = torch.Generator().manual_seed(2)
+    dev = "cuda"
+    k = torch.randn(NB, 16, NKV, HD, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(NB, 16, NKV, HD, device=dev, dtype=torch.bfloat16)
+    perm = torch.randperm(NB, generator=g)
+    draws, used = [], 0
+    for _ in range(R):
+        ctx = torch.randint(512, 4097, (B,), generator=g).tolist()
+        t = torch.zeros(B, W, dtype=torch.int32)
+        for i, c in enumerate(ctx):
+            n = -(-c // 16)
+            t[i, :n] = perm[used:used + n].int()
+            used += n
+        q = torch.randn(B, NH, HD, generator=g).to(torch.bfloat16)
+        nbytes = (sum(ctx) * NKV * HD * 2 * 2 + 2 * B * NH * HD * 2 + 4 * sum(-(-c // 16) for c in ctx) + 4 * B)
+        draws.append((q.to(dev), t.to(dev), torch.tensor(ctx, dtype=torch.int32, device=dev), nbytes))
+    scale = HD ** -0.5
+    for q, t, c, _ in draws:
+        paged_attention_decode(q, k, v, t, c, scale)
+    it = iter(range(10 ** 9))
+
+    def call():
+        q, t, c, _ = draws[next(it) % R]
+        paged_attention_decode(q, k, v, t, c, scale)
+
+    times = gated_event_times(call, 400)[40:]        # drop the first pass over the draws
+    ms = statistics.mean(times)
+    avg_bytes = sum(d[3] for d in draws) / R
+    achieved = avg_bytes / (ms * 1e-3) / 1e9
+    del k, v
+    return {"bound": "hbm", "kernel": "paged_attention_decode (split-K + merge), BASELINE config 2",
+            "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+            "bytes_per_launch": int(avg_bytes), "us_per_launch": round(ms * 1e3, 2)}
+
+
+def cpu_baseline(sd_cpu: dict, cfg, B: int, ctx: int) -> dict:
+    """The CPU oracle's decode step at the benchmark shape (fp32), bounded sample."""
+    from oracle.model import OracleModel
+    threads = torch.get_num_threads()
+    orc = OracleModel(cfg, sd_cpu, dtype=torch.float32)
+    g = torch.Generator().manual_seed(11)
+    caches = []
+    for _ in range(B):
+        c = orc.new_cache(ctx + 8)
+        c.k[:, :, :ctx].normal_(generator=g)
+        c.v[:, :, :ctx].normal_(generator=g)
+        c.length = ctx
+        caches.append(c)
+    toks = torch.randint(0, cfg.vocab_size, (B,), generator=g).tolist()
+    times = []
+    for r in range(4):
+        t0 = time.perf_counter()
+        lg = orc.step([(c, [t]) for c, t in zip(caches, toks)])
+        toks = lg.argmax(-1).tolist()
+        times.append(time.perf_counter() - t0)
+    step_s = statistics.median(times[1:])
+    return {"value": round(B / step_s, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle fp32 decode step, 1.5B shape, batch {B}, {ctx}-token contexts "
+                      f"(random-valued caches), median of 3 steps after 1 warm-up: {step_s * 1e3:.0f} ms/step"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--prompt-len", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (data-parallel replicas would "
+              "scale the per-GPU number with no exchange); run it with --gpus 1", file=sys.stderr)
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from nanoserve_amd.engine import LLMEngine
+    from nanoserve_amd.model import QWEN25_1_5B, Qwen2Model, random_state_dict
+
+    cfg, B, P, K, W = QWEN25_1_5B, args.batch, args.prompt_len, args.steps, args.warmup
+    torch.manual_seed(0)
+    log("generating random-init 1.5B weights (CPU, fp32, seeded)")
+    sd_cpu = random_state_dict(cfg, seed=0, dtype=torch.float32)
+    model = Qwen2Model(cfg, {n: t.to("cuda", torch.bfloat16) for n, t in sd_cpu.items()})
+    max_seq = P + W + K + 8
+    eng = LLMEngine(model, eos_token_ids=[], max_seq_len=max_seq, max_num_seqs=B, max_num_batched_tokens=2048,
+                    batch_wait_s=0.0, kv_cache_tokens=B * (max_seq + 16), piecewise_graphs=False)
+    g = torch.Generator().manual_seed(1)
+    for _ in range(B):
+        eng.add_request(torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist(), W + K + 1, ignore_eos=True)
+    log(f"prefilling {B} x {P} tokens (not timed)")
+    t0 = time.perf_counter()
+    while any(s.is_prefill for s in eng.scheduler.running) or eng.scheduler.waiting:
+        eng.step()
+    torch.cuda.synchronize()
+    log(f"prefill done in {time.perf_counter() - t0:.1f} s; {W} warm-up decode steps (captures bucket {B})")
+    for _ in range(W):
+        eng.step()
+    assert eng.last_step.n_decode == B and eng.last_step.n_prefill == 0
+    g0 = eng.stats["graph_steps"]
+    ctx_sum = sum(s.num_tokens for s in eng.scheduler.running)   # context of the first timed step (incl. new)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        eng.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert eng.stats["graph_steps"] - g0 == K, "every timed step must be a graph replay"
+    ms_step = elapsed / K * 1e3
+    tok_s = B * K / elapsed
+
+    # algorithmic HBM bytes of one decode step
+    wbytes = sum(t.numel() * t.element_size() for name, t in model.named_weights().items()
+                 if name != "model.embed_tokens.weight")
+    wbytes += model.lm_head.numel() * model.lm_head.element_size()           # LM head reads the whole table
+    kv_tok = cfg.kv_bytes_per_token(torch.bfloat16)
+    mean_ctx_total = ctx_sum + B * (K - 1) / 2                                 # sum_b ctx_b averaged over steps
+    step_bytes = wbytes + mean_ctx_total * kv_tok + B * cfg.vocab_size * 2
+    step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"decode: {tok_s:.0f} tok/s, {ms_step:.3f} ms/step, {step_gbs:.0f} GB/s algorithmic")
+
+    del eng
+    torch.cuda.empty_cache()
+    log("paged-attention roofline (config 2 shape)")
+    roof = paged_attention_roofline()
+    log(f"paged attention: {roof['us_per_launch']} us/call, {roof['achieved']} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle, fp32)")
+        del model
+        torch.cuda.empty_cache()
+        cpu = cpu_baseline(sd_cpu, cfg, B, P)
+        log(f"cpu: {cpu['value']} tok/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": "decode tok/s, Qwen2.5-1.5B-shape b=32; paged-attn HBM GB/s as % of peak",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: random-init weights N(0,0.02), random 1024-token prompts",
+        "config": {"workload": "BASELINE config 3: Qwen2.5-1.5B-shape bf16 greedy decode, batch 32, "
+                               "1024-token prompts in the paged KV cache, hipGraph bucket 32",
+                   "batch": B, "prompt_len": P, "block_size": 16},
+        "roofline": roof,
+        "step_roofline": {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(step_gbs / PEAK_HBM_GBS, 4), "bytes_per_step": int(step_bytes),
+                          "roofline_tok_s": round(B / (step_bytes / (PEAK_HBM_GBS * 1e9)), 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
