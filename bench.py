@@ -142,12 +142,15 @@ def main() -> int:
     log("generating random-init 1.5B weights (CPU, fp32, seeded)")
     sd_cpu = random_state_dict(cfg, seed=0, dtype=torch.float32)
     model = Qwen2Model(cfg, {n: t.to("cuda", torch.bfloat16) for n, t in sd_cpu.items()})
-    max_seq = P + W + K + 8
+    # Sequences are admitted two per prefill step, so the first ones start decoding up to B/2 steps early:
+    # max_new_tokens leaves room for that, and no sequence finishes inside the timed window.
+    max_new = W + K + B + 8
+    max_seq = P + max_new
     eng = LLMEngine(model, eos_token_ids=[], max_seq_len=max_seq, max_num_seqs=B, max_num_batched_tokens=2048,
                     batch_wait_s=0.0, kv_cache_tokens=B * (max_seq + 16), piecewise_graphs=False)
     g = torch.Generator().manual_seed(1)
     for _ in range(B):
-        eng.add_request(torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist(), W + K + 1, ignore_eos=True)
+        eng.add_request(torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist(), max_new, ignore_eos=True)
     log(f"prefilling {B} x {P} tokens (not timed)")
     t0 = time.perf_counter()
     while any(s.is_prefill for s in eng.scheduler.running) or eng.scheduler.waiting:
@@ -159,15 +162,17 @@ def main() -> int:
     assert eng.last_step.n_decode == B and eng.last_step.n_prefill == 0
     g0 = eng.stats["graph_steps"]
     ctx_sum = sum(s.num_tokens for s in eng.scheduler.running)   # context of the first timed step (incl. new)
+    produced = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(K):
-        eng.step()
+        produced += len(eng.step())
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     assert eng.stats["graph_steps"] - g0 == K, "every timed step must be a graph replay"
+    assert produced == B * K and len(eng.scheduler.running) == B, "every timed step must decode the full batch"
     ms_step = elapsed / K * 1e3
-    tok_s = B * K / elapsed
+    tok_s = produced / elapsed
 
     # algorithmic HBM bytes of one decode step
     wbytes = sum(t.numel() * t.element_size() for name, t in model.named_weights().items()

@@ -99,6 +99,48 @@ int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, void* q, void
                 void* k_cache, void* v_cache, const int64_t* slots,
                 int64_t n_tok, int n_heads, int n_kv_heads, int head_dim, int dtype, void* stream);
 
+/*
+ * Skinny GEMMs of the decode step (bf16, 1 <= M <= 64, K a multiple of 32; W row-major [N, K], x [M, K],
+ * outputs row-major). They replace the F.linear calls of nanoserve/model.py:231,256-257,362 for
+ * decode-sized batches: y = x W^T (+ bias) with fp32 accumulation and one rounding to bf16, like
+ * F.linear. Small N is split over K across workgroups; the fp32 partials go to `workspace` (at least
+ * ns_gemm_workspace_bytes(M, N, K) bytes; 0 = none needed) and are summed in a fixed order, so results
+ * are deterministic. Each fused variant rounds where the unfused ops it replaces round.
+ */
+size_t ns_gemm_workspace_bytes(int M, int N, int K);
+
+/* y = round(x W^T + bias); bias may be NULL. */
+int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, int dtype,
+            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Merged gate/up projection + SwiGLU: w_gate_up = [gate; up] ([N2, K], N2 = 2 * intermediate);
+ * out[M, N2/2] = round(round(silu(round(x Wg^T))) * round(x Wu^T)).
+ * Replaces silu_mul(F.linear(h, gate_up_w)) (nanoserve/model.py:257, fused.py:75).
+ */
+int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int N2, int K, int dtype,
+                     void* stream);
+
+/*
+ * Projection + residual add (+ RMSNorm): o = round(x W^T); res_out = round(residual + o); if norm_w is
+ * not NULL, h = round(norm_w * round(res_out * rsqrt(mean(res_out^2) + eps))).
+ * Replaces rms_norm(F.linear(o, o_w), ln2, eps, residual=x) (nanoserve/model.py:256) and
+ * x + F.linear(a, down_w) followed by the next layer's rms_norm (model.py:257, :227-231).
+ */
+int ns_gemm_residual_rms_norm(const void* x, const void* w, const void* residual, void* res_out,
+                              const void* norm_w, void* h, float eps, int M, int N, int K, int dtype,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Merged QKV projection + bias + RoPE + paged KV write: qkv = round(x W^T + bias), then the
+ * ns_rope_qkv contract on it (q, k, v outputs; k/v stored at slots when k_cache is given).
+ * Replaces rope_qkv(F.linear(h, qkv_w, qkv_b), ...) (nanoserve/model.py:231-234).
+ */
+int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void* cos, const void* sin,
+                     void* q, void* k, void* v, void* k_cache, void* v_cache, const int64_t* slots, int M,
+                     int K, int n_heads, int n_kv_heads, int head_dim, int dtype, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

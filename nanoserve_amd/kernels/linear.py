@@ -1,14 +1,120 @@
 """Projection GEMMs of the decode loop: y = x @ W^T (+ b), x [M, K], W [N, K] row-major.
 
-One indirection point for every projection of the model (QKV, O, gate/up, down, LM head;
-nanoserve/model.py:231,256-257,362). Large-M (prefill) products go to the vendor GEMM through torch
-(hipBLASLt on ROCm).
+The one indirection point for every projection of the model (QKV, O, gate/up, down, LM head;
+nanoserve/model.py:231,256-257,362). Decode-sized bf16 products (M <= 64) run the skinny HIP GEMMs
+(csrc/gemm.hip), which stream each weight once and fold the neighbouring token-wise ops into their
+epilogues; larger products (prefill chunks) and fp32 go to the vendor GEMM through torch (hipBLASLt on
+ROCm) followed by the standalone HIP token-wise kernels. Both routes round where the unfused PyTorch ops
+round, so they differ only in the fp32 summation order of the products.
+
+Fused entry points (each with the unfused composition it equals):
+  linear(x, w, b)                                   F.linear(x, w, b)
+  linear_silu_mul(x, w_gate_up)                     silu_mul(F.linear(x, w_gate_up))
+  linear_residual_rms_norm(x, w, residual, nw, eps) rms_norm(F.linear(x, w), nw, eps, residual=residual)
+                                                    -> (h, residual + F.linear(x, w)); nw=None -> (None, sum)
+  linear_rope_qkv(x, w, b, cos, sin, ...)           rope_qkv(F.linear(x, w, b), cos, sin, ...)
 """
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
 
+from nanoserve_amd import _lib
+from nanoserve_amd.kernels.fused import rms_norm, rope_qkv, silu_mul
+
+SKINNY_MAX_M = 64
+
+_WS: dict[int, torch.Tensor] = {}
+_WS_RETIRED: list[torch.Tensor] = []   # superseded buffers stay alive: captured graphs may point at them
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WS.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("skinny GEMM workspace must be sized by an eager call before graph capture")
+        if ws is not None:
+            _WS_RETIRED.append(ws)
+        ws = torch.empty(max(nbytes, 1 << 22), dtype=torch.uint8, device=device)
+        _WS[idx] = ws
+    return ws
+
+
+def skinny_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    M, K = x.shape
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.device.type == "cuda" and 1 <= M <= SKINNY_MAX_M
+            and K % 32 == 0 and x.is_contiguous() and w.is_contiguous() and x.data_ptr() % 16 == 0
+            and w.data_ptr() % 16 == 0)
+
+
+def _ws_args(x: torch.Tensor, N: int):
+    M, K = x.shape
+    ws = _workspace(x.device, _lib.lib().ns_gemm_workspace_bytes(M, N, K))
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
+
 
 def linear(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
-    return F.linear(x, w, b)
+    if not skinny_ok(x, w):
+        return F.linear(x, w, b)
+    M, K = x.shape
+    N = w.shape[0]
+    y = torch.empty(M, N, device=x.device, dtype=x.dtype)
+    wsp, wsn = _ws_args(x, N)
+    _lib.check(_lib.lib().ns_gemm(x.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), M, N, K, 1, wsp, wsn,
+                                  _lib.stream_of(x)), "linear")
+    return y
+
+
+def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+    if not skinny_ok(x, w_gate_up):
+        return silu_mul(F.linear(x, w_gate_up))
+    M, K = x.shape
+    N2 = w_gate_up.shape[0]
+    out = torch.empty(M, N2 // 2, device=x.device, dtype=x.dtype)
+    _lib.check(_lib.lib().ns_gemm_silu_mul(x.data_ptr(), w_gate_up.data_ptr(), out.data_ptr(), M, N2, K, 1,
+                                           _lib.stream_of(x)), "linear_silu_mul")
+    return out
+
+
+def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor | None,
+                             eps: float):
+    """(rms_norm(residual + x W^T), residual + x W^T) with the sum rounded to the dtype; norm_w None -> (None, sum).
+    x [M, K], residual [M, N]."""
+    if not skinny_ok(x, w) or not residual.is_contiguous():
+        y = F.linear(x, w)
+        if norm_w is None:
+            return None, residual + y
+        return rms_norm(y, norm_w, eps, residual=residual)
+    M, K = x.shape
+    N = w.shape[0]
+    res_out = torch.empty(M, N, device=x.device, dtype=x.dtype)
+    h = torch.empty(M, N, device=x.device, dtype=x.dtype) if norm_w is not None else None
+    wsp, wsn = _ws_args(x, N)
+    _lib.check(_lib.lib().ns_gemm_residual_rms_norm(
+        x.data_ptr(), w.data_ptr(), residual.data_ptr(), res_out.data_ptr(), _lib.ptr(norm_w), _lib.ptr(h),
+        float(eps), M, N, K, 1, wsp, wsn, _lib.stream_of(x)), "linear_residual_rms_norm")
+    return h, res_out
+
+
+def linear_rope_qkv(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
+                    n_heads: int, n_kv_heads: int, head_dim: int, k_cache=None, v_cache=None, slots=None):
+    if not skinny_ok(x, w) or not (cos.is_contiguous() and sin.is_contiguous()):
+        return rope_qkv(F.linear(x, w, b), cos, sin, n_heads, n_kv_heads, head_dim, k_cache, v_cache, slots)
+    M, K = x.shape
+    N = w.shape[0]
+    assert N == (n_heads + 2 * n_kv_heads) * head_dim and cos.shape == (M, head_dim) and sin.shape == (M, head_dim)
+    if k_cache is not None:
+        assert k_cache.is_contiguous() and v_cache.is_contiguous() and slots.dtype == torch.int64
+        assert slots.shape == (M,) and slots.is_contiguous()
+    q = torch.empty(M, n_heads, head_dim, device=x.device, dtype=x.dtype)
+    k = torch.empty(M, n_kv_heads, head_dim, device=x.device, dtype=x.dtype)
+    v = torch.empty_like(k)
+    wsp, wsn = _ws_args(x, N)
+    _lib.check(_lib.lib().ns_gemm_rope_qkv(
+        x.data_ptr(), w.data_ptr(), _lib.ptr(b), cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr(),
+        v.data_ptr(), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(slots) if k_cache is not None else None,
+        M, K, n_heads, n_kv_heads, head_dim, 1, wsp, wsn, _lib.stream_of(x)), "linear_rope_qkv")
+    return q, k, v

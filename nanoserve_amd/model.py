@@ -4,12 +4,17 @@ Interface follows nanoserve/model.py (ModelConfig :26-56, LayerWeights :67-114, 
 DecodeMeta :132-137, Qwen2Model :154-367) so the engine, scheduler, KV manager and graph runners call it
 the same way. The math of one layer on N flattened tokens (nanoserve/model.py:223-260, fused path):
 
-    h      = rms_norm(x, ln1)                                  HIP  (kernels/fused.py)
-    qkv    = h @ [Wq;Wk;Wv]^T + [bq;bk;bv]                     GEMM (kernels/linear.py)
-    q,k,v  = rope_qkv(qkv, cos, sin) + K/V stored at slots     HIP
-    o      = paged attention over each row's pages             HIP  (kernels/paged_attention.py)
-    h, x   = rms_norm(o @ Wo^T, ln2, residual=x)               GEMM + HIP
-    x      = x + silu_mul(h @ [Wg;Wu]^T) @ Wd^T                GEMM + HIP + GEMM
+    h      = rms_norm(x, ln1)
+    q,k,v  = rope_qkv(h @ [Wq;Wk;Wv]^T + [bq;bk;bv], cos, sin) + K/V stored at slots
+    o      = paged attention over each row's pages                       (kernels/paged_attention.py)
+    h, x   = rms_norm(o @ Wo^T, ln2, residual=x)
+    x      = x + silu_mul(h @ [Wg;Wu]^T) @ Wd^T
+
+For decode-sized bf16 batches (M <= 64) each projection is one skinny HIP GEMM with the neighbouring op in
+its epilogue (kernels/linear.py): QKV + bias + RoPE + KV write; O + residual + RMSNorm; gate/up + SiLU*mul;
+down + residual + the NEXT RMSNorm (the next layer's ln1, or the final norm after the last layer), so a
+layer is 4 GEMM launches (+ split-K epilogues) and 2 attention launches. Larger batches use the vendor GEMM
+and the standalone HIP kernels; both round where PyTorch's unfused ops round.
 
 Attention: one-token decode rows (DecodeMeta) and the tokens of prefill / chunked-prefill rows all go
 through the paged kernel. Prefill token j of a sequence with ctx_len cached tokens is a row whose context
@@ -240,22 +245,31 @@ class Qwen2Model:
 
     def _pre(self, i: int, x: torch.Tensor, cos, sin, paged=None, slot_mapping=None):
         """RMSNorm, merged QKV GEMM, RoPE + paged K/V write. x [1, N, H] -> q [1,N,nh,hd], k/v [1,N,nkv,hd]."""
-        from nanoserve_amd.kernels.fused import rms_norm, rope_qkv
-        from nanoserve_amd.kernels.linear import linear
+        from nanoserve_amd.kernels.fused import rms_norm
+        h = rms_norm(x, self.layers[i].ln1, self.cfg.rms_norm_eps)[0]
+        return self._qkv(i, h, cos, sin, paged, slot_mapping)
+
+    def _qkv(self, i: int, h: torch.Tensor, cos, sin, paged=None, slot_mapping=None):
+        """QKV projection (+ bias) of the normed activations h [N, H], RoPE, K/V stored at the slots."""
+        from nanoserve_amd.kernels.linear import linear_rope_qkv
         layer, cfg = self.layers[i], self.cfg
-        qkv = linear(rms_norm(x, layer.ln1, cfg.rms_norm_eps)[0], layer.qkv_w, layer.qkv_b)
-        q, k, v = rope_qkv(qkv, cos[0], sin[0], cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
-                           paged.k[i] if paged is not None else None,
-                           paged.v[i] if paged is not None else None, slot_mapping)
+        q, k, v = linear_rope_qkv(h, layer.qkv_w, layer.qkv_b, cos[0], sin[0], cfg.n_heads, cfg.n_kv_heads,
+                                  cfg.head_dim, paged.k[i] if paged is not None else None,
+                                  paged.v[i] if paged is not None else None, slot_mapping)
         return q[None], k[None], v[None]
 
+    def _mlp(self, i: int, x: torch.Tensor, o: torch.Tensor, next_norm: torch.Tensor | None):
+        """o_proj + residual + RMSNorm, SwiGLU MLP + residual; with next_norm, the following RMSNorm (the
+        next layer's ln1 or the final norm) is applied in the same epilogue. x, o 2-D -> (h_next, x)."""
+        from nanoserve_amd.kernels.linear import linear_residual_rms_norm, linear_silu_mul
+        layer, eps = self.layers[i], self.cfg.rms_norm_eps
+        h, x = linear_residual_rms_norm(o, layer.o_w, x, layer.ln2, eps)
+        a = linear_silu_mul(h, layer.gate_up_w)
+        return linear_residual_rms_norm(a, layer.down_w, x, next_norm, eps)
+
     def _post(self, i: int, x: torch.Tensor, o: torch.Tensor) -> torch.Tensor:
-        """o_proj + residual (fused into the norm), RMSNorm, SwiGLU MLP + residual."""
-        from nanoserve_amd.kernels.fused import rms_norm, silu_mul
-        from nanoserve_amd.kernels.linear import linear
-        layer = self.layers[i]
-        h, x = rms_norm(linear(o[0], layer.o_w)[None], layer.ln2, self.cfg.rms_norm_eps, residual=x)
-        return x + linear(silu_mul(linear(h[0], layer.gate_up_w)), layer.down_w)[None]
+        """o_proj + residual (fused into the norm), RMSNorm, SwiGLU MLP + residual. x [1,N,H], o [1,N,nh*hd]."""
+        return self._mlp(i, x[0], o[0], None)[1][None]
 
     def _attend(self, i: int, q, k, v, seqs: list[SeqInput], paged=None, decode_meta=None,
                 out: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
@@ -334,13 +348,18 @@ class Qwen2Model:
             raise ValueError("the HIP path needs the paged KV cache (`paged` + `slot_mapping`)")
         assert sum(s.n_tokens for s in seqs) == token_ids.shape[0], "seqs must cover token_ids exactly"
         self._rows_cache = None
-        x = F.embedding(token_ids, self.embed)[None]
+        from nanoserve_amd.kernels.fused import rms_norm
+        L, eps = self.cfg.n_layers, self.cfg.rms_norm_eps
+        x = F.embedding(token_ids, self.embed)
         cos, sin = self.rope(positions)
-        for i in range(self.cfg.n_layers):
-            q, k, v = self._pre(i, x, cos, sin, paged, slot_mapping)
-            x = self._post(i, x, self._attend(i, q, k, v, seqs, paged, decode_meta, slot_mapping=slot_mapping))
+        h = rms_norm(x, self.layers[0].ln1, eps)
+        for i in range(L):
+            q, k, v = self._qkv(i, h, cos, sin, paged, slot_mapping)
+            o = self._attend(i, q, k, v, seqs, paged, decode_meta, slot_mapping=slot_mapping)[0]
+            next_norm = self.layers[i + 1].ln1 if i + 1 < L else self.norm
+            h, x = self._mlp(i, x, o, next_norm)       # h: the next layer's normed input / the final norm
         self._rows_cache = None
-        return self.lm_head_rows(self.final_norm(x), seqs, logits)
+        return self.lm_head_rows(h[None], seqs, logits)
 
     def lm_head_rows(self, x: torch.Tensor, seqs: list[SeqInput], logits="last") -> torch.Tensor:
         """Final-normed hidden states [1, N, H] -> logits of the requested rows."""
