@@ -141,6 +141,13 @@ int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void*
                      int K, int n_heads, int n_kv_heads, int head_dim, int dtype, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/*
+ * Greedy selection: out[r] = index of the first maximal element of row r of x (rows x n, row stride
+ * ld elements); NaN ranks above every number (torch.argmax semantics). int64 output.
+ * Replaces logits.argmax(-1) of nanoserve/engine.py:239 / sampling.py:59-60.
+ */
+int ns_argmax_rows(const void* x, int64_t ld, int64_t rows, int n, int dtype, int64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

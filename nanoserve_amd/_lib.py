@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "ns_silu_mul": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "ns_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                              _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "ns_argmax_rows": (_c_int, [_c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
     "ns_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
     "ns_gemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
     "ns_gemm_silu_mul": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),

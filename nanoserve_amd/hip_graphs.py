@@ -62,6 +62,7 @@ class DecodeGraphRunner:
         self._h_lens = torch.ones(mb, dtype=torch.int32, pin_memory=True)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.outputs: dict[int, torch.Tensor] = {}
+        self.greedy: dict[int, torch.Tensor] = {}    # in-graph argmax of each row's logits (int64)
         self.mempool = None
         self._reset_to_padding()
 
@@ -80,11 +81,13 @@ class DecodeGraphRunner:
         self.block_tables[:, 0] = self.garbage_block
         self.context_lens.fill_(1)
 
-    def _forward(self, B: int) -> torch.Tensor:
+    def _forward(self, B: int) -> tuple[torch.Tensor, torch.Tensor]:
+        from nanoserve_amd.kernels.sampling import argmax_rows
         meta = DecodeMeta(self.token_idx[:B], self.block_tables[:B], self.context_lens[:B], all_rows=True)
         seqs = [SeqInput(1, ctx_len=1, use_kernel=True)] * B
-        return self.model.forward_batch(self.tokens[:B], self.positions[:B], seqs, logits="all", paged=self.pool,
-                                        slot_mapping=self.slots[:B], decode_meta=meta)
+        logits = self.model.forward_batch(self.tokens[:B], self.positions[:B], seqs, logits="all", paged=self.pool,
+                                          slot_mapping=self.slots[:B], decode_meta=meta)
+        return logits, argmax_rows(logits)
 
     def _capture(self, B: int) -> None:
         # warm-up and capture run on padding inputs only, so they cannot overwrite real K/V
@@ -99,8 +102,8 @@ class DecodeGraphRunner:
             self.mempool = torch.cuda.graph_pool_handle()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self.mempool):
-            out = self._forward(B)
-        self.graphs[B], self.outputs[B] = graph, out
+            out, greedy = self._forward(B)
+        self.graphs[B], self.outputs[B], self.greedy[B] = graph, out, greedy
 
     def stage(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
               context_lens: list[int]) -> int:
@@ -144,7 +147,12 @@ class DecodeGraphRunner:
         torch.cuda.current_stream().synchronize()   # the pinned staging buffers are reused every step
         self.stage(tokens, positions, slots, block_tables, context_lens)
         self.graphs[B].replay()
+        self.last_bucket = B
         return self.outputs[B][:n]
+
+    def greedy_tokens(self, n: int) -> list[int]:
+        """Argmax of the first n rows of the last replay (computed inside the graph): one 8n-byte copy."""
+        return self.greedy[self.last_bucket][:n].tolist()
 
     @torch.inference_mode()
     def capture_all(self, max_batch: int) -> None:

@@ -1,7 +1,8 @@
 """Token selection: greedy argmax, or temperature / top-k / top-p sampling by the Gumbel-max trick with a
 per-request splitmix64 stream (semantics of nanoserve/sampling.py:26-90; draw n of request r uses a
-generator seeded with mix_seed(seed_r, n), so results do not depend on batch composition). Greedy is the
-decode-loop path; sampling runs as plain torch ops on the logits' device.
+generator seeded with mix_seed(seed_r, n), so results do not depend on batch composition). Greedy rows use
+the HIP argmax kernel; the non-greedy rows' masking and Gumbel draw run as torch ops on the GPU (sampling
+kernels are not part of the decode-loop hot path).
 """
 from __future__ import annotations
 
@@ -42,8 +43,9 @@ def mix_seed(seed: int, step: int) -> int:
 
 def sample(logits: torch.Tensor, params: list, seeds: list[int], steps: list[int]) -> list[int]:
     """logits [B, V] -> one token per row; row i uses params[i] (None = greedy) and stream (seeds[i], steps[i])."""
+    from nanoserve_amd.kernels.sampling import argmax_rows
     greedy = [p is None or p.greedy for p in params]
-    out = logits.argmax(-1)
+    out = argmax_rows(logits)
     if all(greedy):
         return out.tolist()
     rows = [i for i, g in enumerate(greedy) if not g]
