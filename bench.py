@@ -14,7 +14,8 @@ roofline: the paged-attention decode op alone at BASELINE config 2 (B=32, 14 q /
 ctx U[512, 4096], 16-token pages scattered over a 64k-block pool, 8 disjoint draws used round-robin so the
 256 MB Infinity Cache cannot serve them). Algorithmic bytes per call = sum_b ctx_b*n_kv*hd*2(K,V)*2B +
 Q and O (2*B*n_heads*hd*2B) + block-table entries read (4B per page) + context lengths (4B per row);
-duration from HIP events bracketing each call (split-K pass + merge pass) on the launch stream.
+duration = (time between two HIP events bracketing 400 back-to-back calls on the launch stream) / 400,
+each call being the split-K pass + the merge pass.
 step_roofline: the decode step's algorithmic HBM bytes (every weight once, the KV cache of every row, the
 new K/V and the logits) over the measured step time.
 
@@ -55,6 +56,20 @@ def gated_event_times(fn, n: int) -> list[float]:
     return [e0.elapsed_time(e1) for e0, e1 in evs]
 
 
+def gated_region_time(fn, n: int) -> float:
+    """Time (ms) of n back-to-back calls of fn between one pair of events on the launch stream, behind a
+    sleep kernel so the GPU never waits on Python to enqueue the next call."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2e8))
+    e0.record()
+    for _ in range(n):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
 def paged_attention_roofline() -> dict:
     from nanoserve_amd.kernels.paged_attention import paged_attention_decode
     B, NH, NKV, HD, NB, W, R = 32, 14, 2, 64, 65536, 256, 8
@@ -83,15 +98,42 @@ def paged_attention_roofline() -> dict:
         q, t, c, _ = draws[next(it) % R]
         paged_attention_decode(q, k, v, t, c, scale)
 
-    times = gated_event_times(call, 400)[40:]        # drop the first pass over the draws
-    ms = statistics.mean(times)
+    for _ in range(2 * R):                          # one warm pass over the draws
+        call()
+    ms = gated_region_time(call, 400) / 400
     avg_bytes = sum(d[3] for d in draws) / R
     achieved = avg_bytes / (ms * 1e-3) / 1e9
     del k, v
     return {"bound": "hbm", "kernel": "paged_attention_decode (split-K + merge), BASELINE config 2",
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
             "bytes_per_launch": int(avg_bytes), "us_per_launch": round(ms * 1e3, 2)}
+
+
+def copy_calibration(nbytes: int = 512 << 20, reps: int = 4) -> float:
+    """A plain device copy of known size (nbytes read + nbytes written per launch): under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE per dispatch give the scale from counter units to bytes. Returns GB/s."""
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    times = gated_event_times(lambda: dst.copy_(src), reps)
+    del src, dst
+    return 2 * nbytes / (min(times) * 1e-3) / 1e9
+
+
+def pmc_traffic() -> int | None:
+    """HBM bytes per paged-attention call (split-K pass + merge pass) measured by rocprofv3 --pmc FETCH_SIZE
+    and WRITE_SIZE runs of `bench.py --attention-only`, scaled by the copy calibration, as committed in
+    profiles/paged_attention_decode_config2_pmc.md (None when that summary is absent)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "paged_attention_decode_config2_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(sd_cpu: dict, cfg, B: int, ctx: int) -> dict:
@@ -128,12 +170,20 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--prompt-len", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the paged-attention roofline and the copy calibration (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (data-parallel replicas would "
               "scale the per-GPU number with no exchange); run it with --gpus 1", file=sys.stderr)
         return 2
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    if args.attention_only:
+        roof = paged_attention_roofline()
+        log(f"paged attention: {roof['us_per_launch']} us/call, {roof['achieved']} GB/s")
+        log(f"copy calibration: {copy_calibration():.0f} GB/s")
+        print(json.dumps({"roofline": roof}), flush=True)
+        return 0
     from nanoserve_amd.engine import LLMEngine
     from nanoserve_amd.model import QWEN25_1_5B, Qwen2Model, random_state_dict
 
