@@ -101,45 +101,73 @@ int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, void* q, void
 
 /*
  * Skinny GEMMs of the decode step (bf16, 1 <= M <= 64, K a multiple of 32; W row-major [N, K], x [M, K],
- * outputs row-major). They replace the F.linear calls of nanoserve/model.py:231,256-257,362 for
- * decode-sized batches: y = x W^T (+ bias) with fp32 accumulation and one rounding to bf16, like
- * F.linear. Small N is split over K across workgroups; the fp32 partials go to `workspace` (at least
- * ns_gemm_workspace_bytes(M, N, K) bytes; 0 = none needed) and are summed in a fixed order, so results
- * are deterministic. Each fused variant rounds where the unfused ops it replaces round.
+ * outputs row-major, every pointer 16-byte aligned). They replace the F.linear calls of
+ * nanoserve/model.py:231,256-257,362 for decode-sized batches: y = x W^T (+ bias) with fp32 accumulation
+ * and one rounding to bf16, like F.linear; each fused variant rounds where the unfused ops it replaces
+ * round. One launch per call: the weight tiles are shared out evenly over the GPU, and a tile that two
+ * workgroups share is summed by the later of them in a fixed order, so results are deterministic.
+ * Every entry point needs `workspace`: at least ns_gemm_workspace_bytes(M, N, K) bytes, 256-byte
+ * aligned, ZERO-FILLED once before its first use. Each call leaves its counters at zero again, so the
+ * buffer can be reused by any later call on the same stream without clearing (calls that share a
+ * workspace must not overlap in time).
  */
 size_t ns_gemm_workspace_bytes(int M, int N, int K);
 
+/*
+ * Normalised inputs. The projections that follow an RMSNorm in the model (QKV after ln1, gate/up after
+ * ln2, the LM head after the final norm) take the un-normalised r = residual + ... and normalise each
+ * activation fragment as they load it: h = round(w * round(r * inv)), inv = rsqrt(sum / K + eps), where
+ * sum adds the per-64-column row sums of r^2 that ns_gemm_residual_norm_stats wrote (x_sumsq, fp32
+ * [ceil(K/64)][64], row m at column m) in one fixed order. So the RMSNorm never runs as a separate pass,
+ * and every consumer sees bitwise the same h; ns_rms_norm_apply materialises h where a tensor is needed.
+ * x_sumsq == NULL: x is used as is (x_norm_w, x_eps ignored).
+ */
+
 /* y = round(x W^T + bias); bias may be NULL. */
 int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, int dtype,
+            const float* x_sumsq, const void* x_norm_w, float x_eps,
             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Merged gate/up projection + SwiGLU: w_gate_up = [gate; up] ([N2, K], N2 = 2 * intermediate);
  * out[M, N2/2] = round(round(silu(round(x Wg^T))) * round(x Wu^T)).
  * Replaces silu_mul(F.linear(h, gate_up_w)) (nanoserve/model.py:257, fused.py:75).
+ * Workspace: ns_gemm_workspace_bytes(M, N2, K).
  */
 int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int N2, int K, int dtype,
-                     void* stream);
+                     const float* x_sumsq, const void* x_norm_w, float x_eps,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Projection + residual add (+ RMSNorm): o = round(x W^T); res_out = round(residual + o); if norm_w is
- * not NULL, h = round(norm_w * round(res_out * rsqrt(mean(res_out^2) + eps))).
- * Replaces rms_norm(F.linear(o, o_w), ln2, eps, residual=x) (nanoserve/model.py:256) and
- * x + F.linear(a, down_w) followed by the next layer's rms_norm (model.py:257, :227-231).
+ * Projection + residual add + the statistics of the RMSNorm that follows: o = round(x W^T);
+ * res_out = round(residual + o); row_sumsq[t][m] = sum over columns 64t .. 64t+63 of res_out[m]^2 (fp32,
+ * [ceil(N/64)][64], may be NULL). N a multiple of 8.
+ * With a normalised consumer (or ns_rms_norm_apply) this replaces rms_norm(F.linear(o, o_w), ln2, eps,
+ * residual=x) (nanoserve/model.py:256, fused.py:45) and x + F.linear(a, down_w) followed by the next
+ * layer's rms_norm (model.py:257, :227-231).
  */
-int ns_gemm_residual_rms_norm(const void* x, const void* w, const void* residual, void* res_out,
-                              const void* norm_w, void* h, float eps, int M, int N, int K, int dtype,
-                              void* workspace, size_t workspace_bytes, void* stream);
+int ns_gemm_residual_norm_stats(const void* x, const void* w, const void* residual, void* res_out,
+                                float* row_sumsq, int M, int N, int K, int dtype,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * h = round(norm_w * round(r * rsqrt(sum / n + eps))) with sum from row_sumsq exactly as the GEMMs
+ * compute it on load (rows <= 64, n a multiple of 8). Completes nanoserve/kernels/fused.py:45 rms_norm
+ * for rows whose statistics came from ns_gemm_residual_norm_stats.
+ */
+int ns_rms_norm_apply(const void* r, const float* row_sumsq, const void* norm_w, float eps, void* h,
+                      int64_t rows, int n, int dtype, void* stream);
 
 /*
  * Merged QKV projection + bias + RoPE + paged KV write: qkv = round(x W^T + bias), then the
  * ns_rope_qkv contract on it (q, k, v outputs; k/v stored at slots when k_cache is given).
- * Replaces rope_qkv(F.linear(h, qkv_w, qkv_b), ...) (nanoserve/model.py:231-234).
+ * head_dim 64 or 128. Replaces rope_qkv(F.linear(h, qkv_w, qkv_b), ...) (nanoserve/model.py:231-234).
  */
 int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void* cos, const void* sin,
                      void* q, void* k, void* v, void* k_cache, void* v_cache, const int64_t* slots, int M,
-                     int K, int n_heads, int n_kv_heads, int head_dim, int dtype, void* workspace,
-                     size_t workspace_bytes, void* stream);
+                     int K, int n_heads, int n_kv_heads, int head_dim, int dtype,
+                     const float* x_sumsq, const void* x_norm_w, float x_eps,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Greedy selection: out[r] = index of the first maximal element of row r of x (rows x n, row stride

@@ -42,12 +42,17 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                              _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "ns_argmax_rows": (_c_int, [_c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
     "ns_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
-    "ns_gemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
-    "ns_gemm_silu_mul": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
-    "ns_gemm_residual_rms_norm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_f32, _c_int, _c_int,
-                                           _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
+    "ns_gemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,   # x w bias y M N K dtype
+                         _c_vp, _c_vp, _c_f32,                                      # x_sumsq x_norm_w x_eps
+                         _c_vp, _c_sz, _c_vp]),                                     # ws ws_bytes stream
+    "ns_gemm_silu_mul": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
+                                  _c_vp, _c_vp, _c_f32, _c_vp, _c_sz, _c_vp]),
+    "ns_gemm_residual_norm_stats": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp,      # x w residual res_out sumsq
+                                             _c_int, _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
+    "ns_rms_norm_apply": (_c_int, [_c_vp, _c_vp, _c_vp, _c_f32, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "ns_gemm_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
+                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                  _c_vp, _c_vp, _c_f32, _c_vp, _c_sz, _c_vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -1,28 +1,43 @@
 // Skinny GEMMs of the decode step on gfx950: Y[M, N] = X[M, K] . W[N, K]^T with M <= 64 (the decode
-// batch), bf16 in, fp32 accumulate. At M = 32 each weight byte feeds 32 multiply-adds, so the product is
-// bound by streaming W once from HBM; the kernels are built to keep that stream full and to fold the
-// token-wise ops around each projection into its epilogue.
+// batch), bf16 in, fp32 accumulate, one launch per projection with the token-wise op that follows it
+// fused into the epilogue. At M = 32 each weight byte feeds 32 multiply-adds, so a projection is bound
+// by streaming W once from HBM; everything here serves keeping that stream full.
 //
-// Main kernel (one workgroup = 4 waves = one 64-column tile x one K slice):
-//   * MFMA 16x16x32 bf16: B operand = 16 weight rows x 8 consecutive k per lane (a 16-byte load straight
-//     from W), A operand = 16 activation rows x 8 k (16-byte load from X, which stays in L2). A wave owns
-//     all 64 columns of the tile (4 n-tiles), so every 16-byte X load feeds 4 MFMAs and weight bytes are
-//     2x the activation bytes per k-step at M = 32.
-//   * each wave takes a contiguous quarter of the tile's k-steps and issues a batch of U k-steps of loads
-//     before its MFMAs; the waves' partial tiles are summed through LDS in a fixed order (deterministic).
-//   * small N: the K range is split over KSPLIT workgroups (deterministic: partials go to a workspace and
-//     an epilogue kernel sums them in order). The host picks KSPLIT so that ~256 workgroups run.
-// Modes:
-//   PLAIN    y = round(acc + bias)                                   (LM head, generic)
-//   PARTIAL  ws[s] = acc (fp32)                                      (split-K, fused epilogues below)
-//   SILU     paired gate/up tiles: 32 output columns = gate rows t*32.., up rows N/2 + t*32..;
-//            out = round(round(silu(round(g))) * round(u))            (merged gate/up + SiLU*mul)
-// Epilogue kernels (sum partials in order, then):
-//   bias                 y = round(sum + bias)
-//   residual + RMSNorm   o = round(sum); r = round(res + o) -> res_out; h = round(w * round(r * rsqrt(mean r^2 + eps)))
-//   bias + RoPE + KV     qkv = round(sum + bias), then the rope_qkv contract (fused.hip) incl. the cache write
-// Rounding points are PyTorch's for F.linear (+bias), x + y, rms_norm and silu(g) * u in bf16, so the
-// fused step equals the unfused ops up to the fp32 summation order of the products.
+// Work split: the weight matrix is cut into 64-row tiles and K into 256-k chunks. Each workgroup owns one
+// segment -- a whole tile, or one of ks K-slices of a tile -- so it flushes exactly once, at its end.
+// With many tiles every workgroup takes a whole tile (two resident per CU, so one's epilogue overlaps
+// the other's streaming). With fewer tiles than twice the CU count, the first CU-count tiles go whole
+// and the remainder are sliced, so the last round is spread over the GPU instead of running on a few
+// CUs; with fewer tiles than CUs every tile is sliced. A sliced tile's workgroups publish their fp32
+// partial tiles; the last slice to arrive (a per-tile counter) sums them in slice order -- a fixed
+// order, so results are deterministic -- and runs the epilogue. One launch, no epilogue kernel.
+//
+// Inside a workgroup (4 waves, one 64-row tile at a time):
+//   * weights stream HBM -> registers -> LDS -> MFMA B fragments. Wave j loads n-tile j (16 rows) of the
+//     chunk: instruction p (0..7) reads 512 contiguous bytes of row p (lanes 0-31) and of row p+8 (lanes
+//     32-63). The LDS pitch of 1040 bytes per row pair keeps the stores and the 16-lane fragment reads free
+//     of bank conflicts. Row-contiguous loads stream markedly faster than MFMA-layout loads (16 rows x
+//     64 bytes per instruction).
+//   * a rolling pipeline keeps D chunks of loads in flight per wave (register slots refilled as soon as
+//     their chunk is staged); the LDS stage is double-buffered, one barrier per chunk.
+//   * the 4 waves split each chunk's 8 k-steps (2 each) for all 4 n-tiles (mfma_f32_16x16x32_bf16,
+//     A = X fragments straight from L2, B = weight fragments from LDS); at the end of a tile the waves'
+//     partial tiles are summed through LDS in wave order.
+// Epilogues (rounding points are PyTorch's for the unfused ops each one replaces):
+//   STORE    y = round(acc + bias)                                        (F.linear; LM head)
+//   SILU     tile = 32 gate rows + the matching 32 up rows;
+//            out = round(round(silu(round(g))) * round(u))                 (silu_mul(F.linear(x, Wgu)))
+//   RESNORM  o = round(acc); r = round(residual + o) -> res_out, and each 64-column tile's row sums of
+//            r^2 -> row_sumsq[tile][row] (fp32): the statistics of the RMSNorm that follows
+// Normalised activations ("norm on load"): a projection whose input is rms_norm(r) takes r itself plus
+// the producer's row_sumsq and the norm weight, and normalises each X fragment as it loads it:
+//   h = round(w * round(r * inv)), inv = rsqrt(sum(row_sumsq) / K + eps)
+// with the row sums added in one fixed order (rms_norm_row_inv), so every consumer -- and
+// ns_rms_norm_apply, which materialises h where a tensor is needed -- sees bitwise the same h.
+//   ROPE     tile = 32 dims of a head and the 32 dims half a head further (the rotate-half partners);
+//            qkv = round(acc + bias), then out_lo = r(r(xl cl) - r(xh sl)), out_hi = r(r(xh ch) + r(xl sh))
+//            for q and k heads, v copied; k and v also stored at the token's cache slot
+// Cross-workgroup data moves through agent-scope atomic stores/loads (ns_common.h: publish_*).
 #include <cstdlib>
 #include <type_traits>
 
@@ -34,58 +49,332 @@ typedef __attribute__((ext_vector_type(8))) __bf16 g_bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float g_float4_t;
 typedef __attribute__((ext_vector_type(4))) unsigned int g_u32x4_t;   // native vector: stays in registers
 
-enum GemmMode { GEMM_PLAIN = 0, GEMM_PARTIAL = 1, GEMM_SILU = 2 };
+enum GemmEpi { EPI_STORE = 0, EPI_SILU = 1, EPI_RESNORM = 2, EPI_ROPE = 3 };
 
 constexpr int G_WAVES = 4;
-constexpr int G_TN = 4;          // 16-row n-tiles per workgroup tile: 64 weight rows
-constexpr int G_KC = 256;        // k per chunk: 512 bytes of each weight row
-constexpr int G_SC = 3;          // chunks whose weight loads are in flight together (a super chunk)
-constexpr int G_PAIR = 1040;     // LDS bytes of one row pair (rows p and p+8 of an n-tile) + 16 B pad
+constexpr int G_TN = 4;            // 16-row n-tiles per tile: 64 weight rows
+constexpr int G_KC = 256;          // k per chunk: 512 bytes of each weight row
+constexpr int G_PAIR = 1040;       // LDS bytes of one row pair (rows p and p+8 of an n-tile) + 16 B pad
 constexpr int G_NTB = 8 * G_PAIR;  // LDS bytes of one n-tile (16 rows) of a chunk
 constexpr int G_STAGE = G_TN * G_NTB;
+constexpr int G_RED = 65;          // floats per tile row in the cross-wave reduction (64 + 1 pad)
+constexpr int G_MAX_M = 64;
+// The arrival counters sit at the start of every workspace, in a region no other data ever uses, so the
+// "all counters are zero between calls" invariant holds whatever shapes share the buffer.
+constexpr int G_MAX_TILES = 8191;
+constexpr size_t G_CNT_BYTES = sizeof(unsigned) * (G_MAX_TILES + 1);
 
-// Weight row of n-tile j, row r (0..15) of the tile (clamped; rows past the matrix are dropped later).
-template <int MODE>
-__device__ __forceinline__ int tile_row(int tile, int j, int r, int N) {
-  if constexpr (MODE == GEMM_SILU) {
-    const int half = N >> 1;
-    const int row = (j < 2 ? 0 : half) + tile * 32 + 16 * (j & 1) + r;
-    return min(row, (j < 2 ? half : N) - 1);
+struct GemmArgs {
+  const bf16_t* x;
+  const bf16_t* w;
+  int M, N, K;              // N: rows of w
+  int tiles, chunks;        // tiles, 256-k chunks per tile
+  int whole, ks;            // tiles [0, whole) get one workgroup each; every later tile is cut into ks
+                            // K slices, one workgroup each, summed by the last slice to finish
+  // epilogue operands
+  const bf16_t* bias;
+  bf16_t* y;
+  const bf16_t* residual;
+  bf16_t* res_out;
+  float* sumsq_out;         // RESNORM: [tiles][64] row sums of r^2
+  // normalised input: x holds r; xsq [ceil(K/64)][64] its row sums of r^2, xnw the norm weight [K]
+  const float* xsq;
+  const bf16_t* xnw;
+  float xeps;
+  const bf16_t* cosb;
+  const bf16_t* sinb;
+  bf16_t* q;
+  bf16_t* k;
+  bf16_t* v;
+  bf16_t* kc;
+  bf16_t* vc;
+  const int64_t* slots;
+  int nh, nkv, hd;
+  // workspace (zeroed once by the owner; every launch leaves the counters at zero)
+  unsigned* cnt;    // [tiles] arrival counters + [1] finished-tile counter (start of the workspace)
+  float* part;      // [(tiles - whole) * ks][64 rows][64] published partial tiles of the sliced tiles
+};
+
+// Weight row of n-tile j, row r (0..15) of tile t (clamped inside the matrix / its half).
+template <int EPI>
+__device__ __forceinline__ int tile_row(const GemmArgs& a, int t, int j, int r) {
+  if constexpr (EPI == EPI_SILU) {
+    const int half = a.N >> 1;
+    const int row = (j < 2 ? 0 : half) + t * 32 + 16 * (j & 1) + r;
+    return min(row, (j < 2 ? half : a.N) - 1);
+  } else if constexpr (EPI == EPI_ROPE) {
+    const int tph = a.hd >> 6;   // tiles per head
+    const int head = t / tph, hf = t - head * tph;
+    return head * a.hd + hf * (a.hd >> 2) + 16 * (j & 1) + (j >> 1) * (a.hd >> 1) + r;
   } else {
-    return min(tile * 64 + 16 * j + r, N - 1);
+    return min(t * 64 + 16 * j + r, a.N - 1);
   }
 }
 
-// Main kernel. Workgroup = 4 waves = one 64-row weight tile x one K slice (chunks [c0, c1) of 256 k).
-// Weight path: HBM -> registers -> LDS -> MFMA B fragments. Wave j loads n-tile j: instruction p (0..7)
-// reads 512 contiguous bytes of row p (lanes 0-31) and of row p+8 (lanes 32-63) of the chunk, so every
-// load instruction covers two long row segments; the LDS pitch of 1040 bytes per row pair makes both the
-// stores and the 16-lane fragment reads bank-conflict free. Activation path: X fragments straight from L2.
-// The 4 waves split each chunk's 8 k-steps (2 each) and reduce their partial tiles through LDS.
-template <int TM, int MODE>
-__global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
-                                                                   const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
-                                                                   float* __restrict__ ws, int M, int N, int K, int ksplit) {
-  constexpr int RED_BYTES = G_WAVES * TM * G_TN * 4 * 64 * 4;
-  constexpr int LDS_BYTES = RED_BYTES > G_STAGE ? RED_BYTES : G_STAGE;
-  __shared__ __align__(16) unsigned char lds[LDS_BYTES];
-  const int tile = blockIdx.x, s = blockIdx.y;
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+__device__ __forceinline__ void store_bf16x8(bf16_t* p, const float (&v)[8]) {
+  g_u32x4_t u;
+  u[0] = pack_bf16x2(v[0], v[1]);
+  u[1] = pack_bf16x2(v[2], v[3]);
+  u[2] = pack_bf16x2(v[4], v[5]);
+  u[3] = pack_bf16x2(v[6], v[7]);
+  *reinterpret_cast<g_u32x4_t*>(p) = u;
+}
+__device__ __forceinline__ void load_bf16x8(const bf16_t* p, float (&v)[8]) {
+  const g_u32x4_t u = *reinterpret_cast<const g_u32x4_t*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[2 * e] = __uint_as_float(u[e] << 16);
+    v[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+  }
+}
+
+// Values of 8 consecutive tile columns [col, col + 8) of tile row m: from the LDS reduction buffer
+// (sum of the 4 waves in order) or from the published partials of the tile's ks slices (in order).
+struct TileSource {
+  const float* red;      // LDS [wave][R][G_RED]
+  int R;
+  bool from_parts;
+  int ks;
+  const float* part;     // slice 0 of this tile; slice s at + s * G_MAX_M * 64
+};
+constexpr int G_MAXC = 8;   // slices whose partials are in flight together
+
+__device__ __forceinline__ void tile_values(const TileSource& s, int m, int col, float (&v)[8]) {
+  if (!s.from_parts) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < G_WAVES; ++w) acc += s.red[(w * s.R + m) * G_RED + col + e];
+      v[e] = acc;
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  for (int s0 = 0; s0 < s.ks; s0 += G_MAXC) {
+    float x[G_MAXC][8];
+#pragma unroll
+    for (int k = 0; k < G_MAXC; ++k) {
+      // partial slice layout [e][row * 8 + column group]: lanes hit consecutive words
+      const float* p = s.part + int64_t(min(s0 + k, s.ks - 1)) * G_MAX_M * 64 + m * 8 + (col >> 3);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[k][e] = publish_load(p + e * G_MAX_M * 8);
+    }
+#pragma unroll
+    for (int k = 0; k < G_MAXC; ++k)
+      if (s0 + k < s.ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += x[k][e];
+  }
+}
+
+// Per-thread work items of an epilogue, unrolled to their compile-time maximum so that no loop with a
+// data-dependent trip count (and memory operations) sits inside the streaming loop: the compiler's
+// wait counts for the in-flight weight loads then stay exact across a tile flush.
+template <int TM>
+constexpr int g_items8() { return (16 * TM * 8 + G_WAVES * 64 - 1) / (G_WAVES * 64); }   // (row, 8 columns)
+template <int TM>
+constexpr int g_items4() { return (16 * TM * 4 + G_WAVES * 64 - 1) / (G_WAVES * 64); }   // (row, 8 lo + 8 hi)
+
+// Drain this wave's memory operations after a loop whose trip count depends on data: with nothing left
+// in flight, the compiler's wait counts for the prefetched slots are exact again.
+__device__ __forceinline__ void drain_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <int TM, int EPI>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSource& src, int t) {
+  const int tid = threadIdx.x, M = a.M;
+  if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+    for (int it = 0; it < g_items8<TM>(); ++it) {
+      const int idx = tid + it * G_WAVES * 64;
+      const int m = idx >> 3, cq = idx & 7, n0 = t * 64 + 8 * cq;
+      if (m < M && n0 < a.N) {
+        float v[8];
+        tile_values(src, m, 8 * cq, v);
+        if (a.bias != nullptr)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] += n0 + e < a.N ? bf16_to_f32(a.bias[n0 + e]) : 0.f;
+        bf16_t* dst = a.y + int64_t(m) * a.N + n0;
+        if ((a.N & 7) == 0) {
+          store_bf16x8(dst, v);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n0 + e < a.N) dst[e] = f32_to_bf16(v[e]);
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_SILU) {
+    const int half = a.N >> 1;
+#pragma unroll
+    for (int it = 0; it < g_items4<TM>(); ++it) {
+      const int idx = tid + it * G_WAVES * 64;
+      const int m = idx >> 2, cq = idx & 3, n0 = t * 32 + 8 * cq;
+      if (m < M && n0 < half) {
+        float gv[8], uv[8], o[8];
+        tile_values(src, m, 8 * cq, gv);
+        tile_values(src, m, 32 + 8 * cq, uv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float gb = round_bf16(gv[e]), ub = round_bf16(uv[e]);
+          o[e] = round_bf16(gb / (1.0f + expf(-gb))) * ub;
+        }
+        bf16_t* dst = a.y + int64_t(m) * half + n0;
+        if ((half & 7) == 0) {
+          store_bf16x8(dst, o);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n0 + e < half) dst[e] = f32_to_bf16(o[e]);
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_ROPE) {
+    const int tph = a.hd >> 6, head = t / tph, hf = t - head * tph, hh = a.hd >> 1;
+#pragma unroll
+    for (int it = 0; it < g_items4<TM>(); ++it) {
+      const int idx = tid + it * G_WAVES * 64;
+      const int m = idx >> 2, cq = idx & 3;
+      if (m < M) {
+        const int d0 = hf * (a.hd >> 2) + 8 * cq;             // dims d0..d0+7 and d0+hd/2..
+        float xl[8], xh[8], lo[8], hi[8];
+        tile_values(src, m, 8 * cq, xl);
+        tile_values(src, m, 32 + 8 * cq, xh);
+        const int rl = head * a.hd + d0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xl[e] = round_bf16(xl[e] + (a.bias != nullptr ? bf16_to_f32(a.bias[rl + e]) : 0.f));
+          xh[e] = round_bf16(xh[e] + (a.bias != nullptr ? bf16_to_f32(a.bias[rl + hh + e]) : 0.f));
+        }
+        if (head < a.nh + a.nkv) {
+          float cl[8], ch[8], sl[8], sh[8];
+          load_bf16x8(a.cosb + int64_t(m) * a.hd + d0, cl);
+          load_bf16x8(a.cosb + int64_t(m) * a.hd + d0 + hh, ch);
+          load_bf16x8(a.sinb + int64_t(m) * a.hd + d0, sl);
+          load_bf16x8(a.sinb + int64_t(m) * a.hd + d0 + hh, sh);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            lo[e] = round_bf16(xl[e] * cl[e]) - round_bf16(xh[e] * sl[e]);
+            hi[e] = round_bf16(xh[e] * ch[e]) + round_bf16(xl[e] * sh[e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            lo[e] = xl[e];
+            hi[e] = xh[e];
+          }
+        }
+        bf16_t* dst;
+        bf16_t* cdst = nullptr;
+        if (head < a.nh) {
+          dst = a.q + (int64_t(m) * a.nh + head) * a.hd;
+        } else if (head < a.nh + a.nkv) {
+          const int kh = head - a.nh;
+          dst = a.k + (int64_t(m) * a.nkv + kh) * a.hd;
+          if (a.kc != nullptr) cdst = a.kc + (a.slots[m] * a.nkv + kh) * a.hd;
+        } else {
+          const int vh = head - a.nh - a.nkv;
+          dst = a.v + (int64_t(m) * a.nkv + vh) * a.hd;
+          if (a.vc != nullptr) cdst = a.vc + (a.slots[m] * a.nkv + vh) * a.hd;
+        }
+        store_bf16x8(dst + d0, lo);
+        store_bf16x8(dst + d0 + hh, hi);
+        if (cdst != nullptr) {
+          store_bf16x8(cdst + d0, lo);
+          store_bf16x8(cdst + d0 + hh, hi);
+        }
+      }
+    }
+  } else {  // EPI_RESNORM
+    const int N = a.N;
+    // res_out and this tile's row sums of r^2 (8 threads per row: lanes 8k .. 8k+7)
+#pragma unroll
+    for (int it = 0; it < g_items8<TM>(); ++it) {
+      const int idx = tid + it * G_WAVES * 64;
+      const int m = idx >> 3, cq = idx & 7, n0 = t * 64 + 8 * cq;
+      const bool live = m < M;
+      float ss = 0.f;
+      if (live && n0 < N) {
+        float o[8], rs[8], r[8];
+        tile_values(src, m, 8 * cq, o);
+        load_bf16x8(a.residual + int64_t(m) * N + n0, rs);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          r[e] = round_bf16(rs[e] + round_bf16(o[e]));
+          ss += r[e] * r[e];
+        }
+        store_bf16x8(a.res_out + int64_t(m) * N + n0, r);
+      }
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      ss += __shfl_xor(ss, 4, 64);
+      if (live && cq == 0 && a.sumsq_out != nullptr) a.sumsq_out[int64_t(t) * G_MAX_M + m] = ss;
+    }
+  }
+}
+
+// inv of row m for normalised inputs: lane group r4 (the 4 lanes of one row) adds the row sums of
+// producer tiles r4, r4+4, ... in order, then the groups combine as (g0 + g1) + (g2 + g3) through two
+// butterfly steps, which gives every lane of the 4 the same bits. Called by all 64 lanes of a wave.
+__device__ __forceinline__ float rms_norm_row_inv(const float* sumsq, int ptiles, int m, int r4, int K, float eps) {
+  float part = 0.f;
+  for (int p = r4; p < ptiles; p += 4) part += sumsq[int64_t(p) * G_MAX_M + m];
+  part += __shfl_xor(part, 16, 64);
+  part += __shfl_xor(part, 32, 64);
+  return rsqrtf(part / float(K) + eps);
+}
+
+// 8 bf16 of r (one X fragment) -> 8 bf16 of h = round(w * round(r * inv))
+__device__ __forceinline__ g_u32x4_t norm_fragment(g_u32x4_t r, g_u32x4_t w, float inv) {
+  g_u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float r0 = __uint_as_float(r[e] << 16), r1 = __uint_as_float(r[e] & 0xffff0000u);
+    const float w0 = __uint_as_float(w[e] << 16), w1 = __uint_as_float(w[e] & 0xffff0000u);
+    o[e] = pack_bf16x2(w0 * round_bf16(r0 * inv), w1 * round_bf16(r1 * inv));
+  }
+  return o;
+}
+
+template <int TM, int EPI, bool NX>
+__global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
+  __shared__ __align__(16) unsigned char lds[2 * G_STAGE];
+  __shared__ unsigned s_flag;
+  constexpr int R = 16 * TM;
+  // this workgroup's segment: chunks [c0, c1) of tile t (slice s of ks)
+  const int b = blockIdx.x, C = a.chunks, K = a.K;
+  int t, s, ks;
+  if (b < a.whole) {
+    t = b;
+    s = 0;
+    ks = 1;
+  } else {
+    ks = a.ks;
+    t = a.whole + (b - a.whole) / ks;
+    s = (b - a.whole) - (t - a.whole) * ks;
+  }
+  const int c0 = s * C / ks, c1 = (s + 1) * C / ks;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
-  const int nchunks = (K + G_KC - 1) / G_KC;
-  const int c0 = int((int64_t(nchunks) * s) / ksplit), c1 = int((int64_t(nchunks) * (s + 1)) / ksplit);
-
-  // this lane's weight rows: n-tile wv, rows p (lanes 0-31) / p + 8 (lanes 32-63), p = 0..7
   const int half_sel = lane >> 5, col16 = lane & 31;
+  const int st_off = wv * G_NTB + half_sel * 512 + col16 * 16;        // + p * G_PAIR
+  const int fr_off = (c16 & 7) * G_PAIR + (c16 >> 3) * 512 + r4 * 16;   // + j * G_NTB + kstep * 64
   const bf16_t* wbase[8];
 #pragma unroll
-  for (int p = 0; p < 8; ++p)
-    wbase[p] = w + int64_t(tile_row<MODE>(tile, wv, p + 8 * half_sel, N)) * K + 8 * col16;
-  const int st_off = wv * G_NTB + half_sel * 512 + col16 * 16;       // + p * G_PAIR
-  const int fr_off = (c16 & 7) * G_PAIR + (c16 >> 3) * 512 + r4 * 16;  // + j * G_NTB + kstep * 64
+  for (int p = 0; p < 8; ++p) wbase[p] = a.w + int64_t(tile_row<EPI>(a, t, wv, p + 8 * half_sel)) * K + 8 * col16;
   const bf16_t* xrow[TM];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) xrow[i] = x + int64_t(min(16 * i + c16, M - 1)) * K + 8 * r4;
+  for (int i = 0; i < TM; ++i) xrow[i] = a.x + int64_t(min(16 * i + c16, a.M - 1)) * K + 8 * r4;
+  float xinv[TM];   // normalised input: inv of this lane's X rows
+  if constexpr (NX) {
+    const int ptiles = (K + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xinv[i] = rms_norm_row_inv(a.xsq, ptiles, min(16 * i + c16, a.M - 1), r4, K, a.xeps);
+  }
 
   g_float4_t acc[TM][G_TN];
 #pragma unroll
@@ -93,373 +382,361 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(const bf16_t*
 #pragma unroll
     for (int j = 0; j < G_TN; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int sc = c0; sc < c1; sc += G_SC) {
-    // issue every weight load of up to G_SC chunks, and this wave's activation fragments (k-steps 2wv,
-    // 2wv+1 of each chunk); k beyond K reads a clamped in-bounds address and is masked below
-    g_u32x4_t wr[G_SC][8], xf[G_SC][2][TM];
+  // Rolling pipeline: register slot q holds the weight rows (and this wave's X fragments) of chunk
+  // c0 + q (mod D); while one chunk is staged through LDS and multiplied, the loads of the next D-1 are
+  // in flight, and a slot is refilled with chunk c + D as soon as its chunk has been staged. Refills past
+  // the segment re-load its last chunk (an L2 hit), so every path issues the same load sequence and the
+  // compiler's wait counts stay exact (vmcnt leaves the other slots' loads in flight).
+  constexpr int D = (TM <= 2 && !NX) ? 3 : 2;
+  g_u32x4_t wr[D][8], xf[D][2][TM];
+  g_u32x4_t xw[D][2];   // normalised input: norm-weight fragments of the lane's k range
+  const int clast = c1 - 1;
+  auto load_w = [&](auto qc, int c) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    const int kc = min(c * G_KC, K - 8 * col16 - 8);   // k beyond K: a clamped in-bounds address, masked below
 #pragma unroll
-    for (int q = 0; q < G_SC; ++q) {
-      const int kc = min(sc + q, c1 - 1) * G_KC;
+    for (int p = 0; p < 8; ++p) wr[q][p] = *reinterpret_cast<const g_u32x4_t*>(wbase[p] + kc);
+  };
+  auto load_x = [&](auto qc, int c) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    const int kc = c * G_KC;
 #pragma unroll
-      for (int p = 0; p < 8; ++p) wr[q][p] = *reinterpret_cast<const g_u32x4_t*>(wbase[p] + min(kc, K - 8 * col16 - 8));
+    for (int h = 0; h < 2; ++h) {
+      const int k = min(kc + 32 * (2 * wv + h), K - 32);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) xf[q][h][i] = *reinterpret_cast<const g_u32x4_t*>(xrow[i] + k);
+      if constexpr (NX) xw[q][h] = *reinterpret_cast<const g_u32x4_t*>(a.xnw + k + 8 * r4);
     }
+  };
+  int buf = 0;
+  auto step = [&](auto qc, int c, int next) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    unsigned char* stage = lds + buf * G_STAGE;
 #pragma unroll
-    for (int q = 0; q < G_SC; ++q) {
-      const int kc = min(sc + q, c1 - 1) * G_KC;
+    for (int p = 0; p < 8; ++p) *reinterpret_cast<g_u32x4_t*>(stage + st_off + p * G_PAIR) = wr[q][p];
+    load_w(qc, next);
+    __syncthreads();   // the chunk's 64 rows are in this buffer; every wave is done with the other one
+    const int kc = c * G_KC;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int h = 0; h < 2; ++h) {
+      const int kstep = 2 * wv + h;
+      if (kc + 32 * kstep < K) {   // uniform
+        g_bf16x8_t bfr[G_TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          xf[q][t][i] = *reinterpret_cast<const g_u32x4_t*>(xrow[i] + min(kc + 32 * (2 * wv + t), K - 32));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // one chunk at a time through the LDS stage; q is a compile-time constant so wr/xf stay in registers
-    auto chunk = [&](auto qc) {
-      constexpr int q = decltype(qc)::value;
-      if (sc + q >= c1) return;   // uniform
-      const int kc = (sc + q) * G_KC;
-      __syncthreads();   // the stage is free (previous chunk consumed)
+        for (int j = 0; j < G_TN; ++j)
+          bfr[j] = __builtin_bit_cast(g_bf16x8_t, *reinterpret_cast<const g_u32x4_t*>(stage + j * G_NTB + kstep * 64 + fr_off));
 #pragma unroll
-      for (int p = 0; p < 8; ++p) *reinterpret_cast<g_u32x4_t*>(lds + st_off + p * G_PAIR) = wr[q][p];
-      __syncthreads();
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int ks = 2 * wv + t;
-        if (kc + 32 * ks < K) {   // uniform
-          g_bf16x8_t bfr[G_TN];
+        for (int i = 0; i < TM; ++i) {
+          g_u32x4_t xa = xf[q][h][i];
+          if constexpr (NX) xa = norm_fragment(xa, xw[q][h], xinv[i]);
 #pragma unroll
           for (int j = 0; j < G_TN; ++j)
-            bfr[j] = __builtin_bit_cast(g_bf16x8_t, *reinterpret_cast<const g_u32x4_t*>(lds + j * G_NTB + ks * 64 + fr_off));
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < G_TN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, xf[q][t][i]), bfr[j],
-                                                                  acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, xa), bfr[j], acc[i][j], 0,
+                                                                0, 0);
         }
       }
-    };
-    static_assert(G_SC == 3, "chunk() is expanded for three chunks");
-    chunk(std::integral_constant<int, 0>{});
-    chunk(std::integral_constant<int, 1>{});
-    chunk(std::integral_constant<int, 2>{});
+    }
+    load_x(qc, next);
+    buf ^= 1;
+  };
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
+  using Q2 = std::integral_constant<int, 2>;
+  load_w(Q0{}, c0);
+  load_x(Q0{}, c0);
+  load_w(Q1{}, min(c0 + 1, clast));
+  load_x(Q1{}, min(c0 + 1, clast));
+  if constexpr (D > 2) {
+    load_w(Q2{}, min(c0 + 2, clast));
+    load_x(Q2{}, min(c0 + 2, clast));
   }
+  int c = c0;
+  for (; c + D <= c1; c += D) {   // whole rounds only: no path into the loop header skips a step
+    step(Q0{}, c, min(c + D, clast));
+    step(Q1{}, c + 1, min(c + 1 + D, clast));
+    if constexpr (D > 2) step(Q2{}, c + 2, min(c + 2 + D, clast));
+  }
+  if (c < c1) step(Q0{}, c, clast);
+  if constexpr (D > 2)
+    if (c + 1 < c1) step(Q1{}, c + 1, clast);
 
-  // sum the 4 waves' partial tiles through LDS (fixed order); element e = ((i*4 + j)*4 + r)*64 + lane
-  __syncthreads();
-  float* sm = reinterpret_cast<float*>(lds);
-  constexpr int PER_WAVE = TM * G_TN * 4 * 64;
+  // ---- the segment is done: sum the waves' partial tiles through LDS (wave order)
+  float* red = reinterpret_cast<float*>(lds);
+  __syncthreads();   // every wave is done with both stage buffers
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < G_TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sm[wv * PER_WAVE + ((i * G_TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+      for (int r = 0; r < 4; ++r) red[(wv * R + 16 * i + 4 * r4 + r) * G_RED + 16 * j + c16] = acc[i][j][r];
   __syncthreads();
-
-  if constexpr (MODE == GEMM_SILU) {
-    const int half = N >> 1;
-    for (int e = tid; e < TM * 2 * 4 * 64; e += G_WAVES * 64) {
-      const int l = e & 63, r = (e >> 6) & 3, j = (e >> 8) & 1, i = e >> 9;
-      const int eg = ((i * G_TN + j) * 4 + r) * 64 + l, eu = ((i * G_TN + j + 2) * 4 + r) * 64 + l;
-      float g = 0.f, u = 0.f;
+  TileSource src{red, R, false, ks, nullptr};
+  if (ks == 1) {
+    tile_epilogue<TM, EPI>(a, src, t);
+    return;
+  }
+  // sliced tile: publish this slice's partial; the last slice to arrive sums all of them in slice order
+  float* tile_part = a.part + int64_t(t - a.whole) * ks * G_MAX_M * 64;
+  float* my = tile_part + int64_t(s) * G_MAX_M * 64;
 #pragma unroll
-      for (int qw = 0; qw < G_WAVES; ++qw) {
-        g += sm[qw * PER_WAVE + eg];
-        u += sm[qw * PER_WAVE + eu];
-      }
-      const int m = 16 * i + 4 * (l >> 4) + r, n = tile * 32 + 16 * j + (l & 15);
-      if (m < M && n < half) {
-        const float gb = round_bf16(g), ub = round_bf16(u);
-        const float sv = round_bf16(gb / (1.0f + expf(-gb)));
-        y[int64_t(m) * half + n] = f32_to_bf16(sv * ub);
-      }
-    }
-  } else {
-    for (int e = tid; e < PER_WAVE; e += G_WAVES * 64) {
-      const int l = e & 63, r = (e >> 6) & 3, j = (e >> 8) & 3, i = e >> 10;
-      float v = 0.f;
+  for (int it = 0; it < g_items8<TM>(); ++it) {
+    const int idx = tid + it * G_WAVES * 64;
+    const int m = idx >> 3, cq = idx & 7;
+    if (m < a.M) {
+      float v[8];
+      tile_values(src, m, 8 * cq, v);
 #pragma unroll
-      for (int qw = 0; qw < G_WAVES; ++qw) v += sm[qw * PER_WAVE + e];
-      const int m = 16 * i + 4 * (l >> 4) + r, n = tile * 64 + 16 * j + (l & 15);
-      if (m < M && n < N) {
-        if constexpr (MODE == GEMM_PARTIAL) {
-          ws[(int64_t(s) * M + m) * N + n] = v;
-        } else {
-          if (bias != nullptr) v += bf16_to_f32(bias[n]);
-          y[int64_t(m) * N + n] = f32_to_bf16(v);
-        }
-      }
+      for (int e = 0; e < 8; ++e) publish_store(my + e * G_MAX_M * 8 + m * 8 + cq, v[e]);
     }
   }
-}
-
-// ---------------------------------------------------------------------------------- split-K epilogues
-// Partials ws[s][m][n] (fp32) are summed in order s = 0, 1, ... Every thread owns one group of 4 columns of
-// a row and loads its KMAX partial float4s at once (steps past ksplit read a valid slice and are weighted
-// 0), so an epilogue costs one memory latency.
-constexpr int KMAX = 16;   // largest K split the host picks
-
-__device__ __forceinline__ float4 sum_partials(const float* __restrict__ ws, int64_t total, int64_t off, int ksplit) {
-  float4 p[KMAX];
-#pragma unroll
-  for (int s = 0; s < KMAX; ++s) p[s] = *reinterpret_cast<const float4*>(ws + min(s, ksplit - 1) * total + off);
-  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int s = 0; s < KMAX; ++s) {
-    if (s < ksplit) {
-      a.x += p[s].x;
-      a.y += p[s].y;
-      a.z += p[s].z;
-      a.w += p[s].w;
-    }
-  }
-  return a;
-}
-
-// grid (ceil(N/4 / 256), M): y = round(sum + bias)
-__global__ __launch_bounds__(256) void splitk_bias_kernel(const float* __restrict__ ws, const bf16_t* __restrict__ bias,
-                                                          bf16_t* __restrict__ y, int M, int N, int ksplit) {
-  const int m = blockIdx.y, c4 = blockIdx.x * 256 + threadIdx.x;
-  if (4 * c4 >= N) return;
-  const int64_t total = int64_t(M) * N, off = int64_t(m) * N + 4 * c4;
-  const float4 a = sum_partials(ws, total, off, ksplit);
-  const float v[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float b = bias != nullptr ? bf16_to_f32(bias[4 * c4 + e]) : 0.f;
-    y[off + e] = f32_to_bf16(v[e] + b);
-  }
-}
-
-constexpr int EPI_THREADS = 1024;   // one workgroup per row, one thread per 4 columns: rows up to 4096
-
-// One workgroup of ceil(N/4) threads (rounded up to a wave) per row: o = round(sum); r = round(res + o)
-// -> res_out; with a norm weight, h = rms_norm(r) (fp32 statistics, the rms_norm kernel's rounding).
-__global__ __launch_bounds__(EPI_THREADS) void splitk_residual_rmsnorm_kernel(
-    const float* __restrict__ ws, const bf16_t* __restrict__ res, bf16_t* __restrict__ res_out,
-    const bf16_t* __restrict__ nw, bf16_t* __restrict__ h, int M, int N, int ksplit, float eps) {
-  const int m = blockIdx.x, c4 = threadIdx.x;
-  const bool live = 4 * c4 < N;
-  const int64_t total = int64_t(M) * N, off = int64_t(m) * N + 4 * (live ? c4 : 0);
-  const float4 a = sum_partials(ws, total, off, ksplit);
-  const float o[4] = {a.x, a.y, a.z, a.w};
-  float r[4];
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    r[e] = live ? round_bf16(bf16_to_f32(res[off + e]) + round_bf16(o[e])) : 0.f;
-    if (live) res_out[off + e] = f32_to_bf16(r[e]);
-    ss += r[e] * r[e];
-  }
-  if (nw == nullptr) return;
-  __shared__ float part[EPI_THREADS / 64];
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  publish_complete();
   __syncthreads();
-  float tot = 0.f;
-  for (int i = 0; i < int(blockDim.x) / 64; ++i) tot += part[i];
-  const float inv = rsqrtf(tot / float(N) + eps);
-  if (live)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) h[off + e] = f32_to_bf16(bf16_to_f32(nw[4 * c4 + e]) * round_bf16(r[e] * inv));
-}
-
-// One workgroup per token: qkv row = round(sum + bias) staged in LDS, then RoPE + KV write exactly as
-// the rope_qkv kernel (out_lo = r(r(xl cl) - r(xh sl)), out_hi = r(r(xh ch) + r(xl sh)), v copied).
-constexpr int ROPE_MAX_WIDTH = 4096;
-__global__ __launch_bounds__(ROPE_MAX_WIDTH / 4) void splitk_bias_rope_kernel(
-    const float* __restrict__ ws, const bf16_t* __restrict__ bias, const bf16_t* __restrict__ cosb,
-    const bf16_t* __restrict__ sinb, bf16_t* __restrict__ q, bf16_t* __restrict__ k, bf16_t* __restrict__ v,
-    bf16_t* __restrict__ kc, bf16_t* __restrict__ vc, const int64_t* __restrict__ slots, int M, int nh, int nkv,
-    int hd, int ksplit) {
-  const int t = blockIdx.x;
-  const int width = (nh + 2 * nkv) * hd, half = hd >> 1;
-  const int64_t total = int64_t(M) * width;
-  __shared__ float row[ROPE_MAX_WIDTH];
-  {
-    const int c4 = threadIdx.x;
-    if (4 * c4 < width) {
-      const float4 a = sum_partials(ws, total, int64_t(t) * width + 4 * c4, ksplit);
-      const float vv[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        row[4 * c4 + e] = round_bf16(vv[e] + (bias != nullptr ? bf16_to_f32(bias[4 * c4 + e]) : 0.f));
-    }
+  if (tid == 0) {
+    const unsigned prev = publish_count(a.cnt + t);
+    const unsigned last = prev == unsigned(ks - 1);
+    if (last) publish_reset(a.cnt + t);
+    s_flag = last;
   }
   __syncthreads();
-  const bf16_t* cr = cosb + int64_t(t) * hd;
-  const bf16_t* sr = sinb + int64_t(t) * hd;
-  const int64_t slot = kc != nullptr ? slots[t] : 0;
-  const int n_rot = (nh + nkv) * half;
-  for (int i = threadIdx.x; i < n_rot; i += blockDim.x) {
-    const int head = i / half, d = i - head * half;
-    const float xl = row[head * hd + d], xh = row[head * hd + half + d];
-    const float cl = bf16_to_f32(cr[d]), ch = bf16_to_f32(cr[half + d]);
-    const float sl = bf16_to_f32(sr[d]), sh = bf16_to_f32(sr[half + d]);
-    const bf16_t lo = f32_to_bf16(round_bf16(xl * cl) - round_bf16(xh * sl));
-    const bf16_t hi = f32_to_bf16(round_bf16(xh * ch) + round_bf16(xl * sh));
-    if (head < nh) {
-      bf16_t* dst = q + (int64_t(t) * nh + head) * hd;
-      dst[d] = lo;
-      dst[half + d] = hi;
-    } else {
-      const int kh = head - nh;
-      bf16_t* dst = k + (int64_t(t) * nkv + kh) * hd;
-      dst[d] = lo;
-      dst[half + d] = hi;
-      if (kc != nullptr) {
-        bf16_t* cd = kc + (slot * nkv + kh) * hd;
-        cd[d] = lo;
-        cd[half + d] = hi;
-      }
-    }
-  }
-  const int n_v = nkv * hd;
-  for (int i = threadIdx.x; i < n_v; i += blockDim.x) {
-    const bf16_t val = f32_to_bf16(row[(nh + nkv) * hd + i]);
-    v[int64_t(t) * n_v + i] = val;
-    if (vc != nullptr) vc[slot * n_v + i] = val;
+  if (s_flag == 0u) return;
+  acquire_published();
+  src.from_parts = true;
+  src.part = tile_part;
+  tile_epilogue<TM, EPI>(a, src, t);
+}
+
+// h = round(w * round(r * inv)) for whole rows, inv exactly as the GEMMs compute it on load: one wave per
+// row, 8 columns (16 bytes) per lane per step.
+__global__ __launch_bounds__(64) void rms_norm_apply_kernel(const bf16_t* __restrict__ r, const float* __restrict__ sumsq,
+                                                           const bf16_t* __restrict__ w, bf16_t* __restrict__ h, int N,
+                                                           float eps) {
+  const int m = blockIdx.x, lane = threadIdx.x;
+  const float inv = rms_norm_row_inv(sumsq, (N + 63) / 64, m, lane >> 4, N, eps);
+  for (int c = 8 * lane; c < N; c += 8 * 64) {
+    const g_u32x4_t rv = *reinterpret_cast<const g_u32x4_t*>(r + int64_t(m) * N + c);
+    const g_u32x4_t wv = *reinterpret_cast<const g_u32x4_t*>(w + c);
+    *reinterpret_cast<g_u32x4_t*>(h + int64_t(m) * N + c) = norm_fragment(rv, wv, inv);
   }
 }
 
 // ------------------------------------------------------------------------------------------- host side
+// Workgroups that stream at once: one per CU (NS_GEMM_WGS overrides, for experiments).
 static int target_workgroups() {
   static int target = [] {
-    const char* e = getenv("NS_GEMM_TARGET_WGS");
+    const char* e = getenv("NS_GEMM_WGS");
     const int v = e != nullptr ? atoi(e) : 0;
     return v > 0 ? v : 256;
   }();
   return target;
 }
 
-static int pick_ksplit(int tiles, int K) {
-  const int nchunks = (K + G_KC - 1) / G_KC;
-  int k = (target_workgroups() + tiles - 1) / tiles;
-  const int one_round = (nchunks + G_SC - 1) / G_SC;   // slices that fit one super chunk of loads
-  if (k > 1 && k < one_round) k = one_round;            // when K is split anyway, one load round per slice
-  if (k < 1) k = 1;
-  if (k > nchunks) k = nchunks;     // every slice holds at least one chunk
-  if (k > KMAX) k = KMAX;
-  return k;
-}
+struct Plan {
+  int tiles, chunks, whole, ks, grid;
+  size_t cnt_off, part_off, bytes;
+};
 
-template <int MODE>
-static int launch_main(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* y, float* ws, int M, int N,
-                       int K, int tiles, int ksplit, hipStream_t st) {
-  const dim3 grid(tiles, ksplit);
-  if (M <= 16)
-    hipLaunchKernelGGL((skinny_gemm_kernel<1, MODE>), grid, dim3(G_WAVES * 64), 0, st, x, w, bias, y, ws, M, N, K, ksplit);
-  else if (M <= 32)
-    hipLaunchKernelGGL((skinny_gemm_kernel<2, MODE>), grid, dim3(G_WAVES * 64), 0, st, x, w, bias, y, ws, M, N, K, ksplit);
-  else
-    hipLaunchKernelGGL((skinny_gemm_kernel<4, MODE>), grid, dim3(G_WAVES * 64), 0, st, x, w, bias, y, ws, M, N, K, ksplit);
-  return check_launch("skinny_gemm");
+static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// tiles: 64-row tiles of the weight (SILU: 32 gate + 32 up rows, i.e. 32 output columns).
+// Many tiles: one workgroup per tile. Fewer than twice the target: the target's worth of whole tiles,
+// and the rest cut into K slices so that the last round is spread over the GPU too. Fewer tiles than
+// the target: every tile cut into up to `chunks` slices.
+static Plan make_plan(int tiles, int K) {
+  Plan p;
+  const int T = target_workgroups();
+  p.tiles = tiles;
+  p.chunks = (K + G_KC - 1) / G_KC;
+  if (tiles >= 2 * T) {
+    p.whole = tiles;
+    p.ks = 1;
+  } else {
+    p.whole = tiles >= T ? T : 0;
+    const int rest = tiles - p.whole;
+    int ks = rest > 0 ? (T + rest - 1) / rest : 1;
+    if (tiles >= T) ks = rest > 0 ? T / rest : 1;
+    p.ks = ks < 1 ? 1 : (ks > p.chunks ? p.chunks : ks);
+  }
+  if (p.ks == 1) p.whole = tiles;
+  p.grid = p.whole + (tiles - p.whole) * p.ks;
+  p.cnt_off = 0;
+  p.part_off = G_CNT_BYTES;   // fixed: every plan finds the counters at the same, otherwise unused bytes
+  p.bytes = p.part_off + align256(sizeof(float) * size_t(tiles - p.whole) * p.ks * G_MAX_M * 64);
+  return p;
 }
 
 static int check_common(const void* x, const void* w, int M, int N, int K, int dtype) {
   NS_REQUIRE(dtype == NS_DTYPE_BF16, "skinny gemm: bf16 only (dtype %d)", dtype);
-  NS_REQUIRE(M >= 1 && M <= 64, "skinny gemm: M=%d outside 1..64", M);
+  NS_REQUIRE(M >= 1 && M <= G_MAX_M, "skinny gemm: M=%d outside [1, %d]", M, G_MAX_M);
   NS_REQUIRE(N >= 1 && K >= 32 && K % 32 == 0, "skinny gemm: N=%d K=%d (K must be a positive multiple of 32)", N, K);
-  NS_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16) == 0,
-             "skinny gemm: x and w must be 16-byte aligned");
+  NS_REQUIRE(x != nullptr && w != nullptr, "skinny gemm: null operand");
+  NS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
+             "skinny gemm: operands must be 16-byte aligned");
   return NS_OK;
 }
 
-static int need_ws(void* ws, size_t ws_bytes, int ksplit, int M, int N) {
-  const size_t need = size_t(ksplit) * M * N * sizeof(float);
-  if (ws == nullptr || ws_bytes < need) {
-    set_error("skinny gemm: workspace of %zu bytes needed, got %zu", need, ws == nullptr ? size_t(0) : ws_bytes);
+static int bind_workspace(GemmArgs& a, const Plan& p, void* ws, size_t ws_bytes) {
+  NS_REQUIRE(p.tiles <= G_MAX_TILES, "skinny gemm: %d tiles exceed the %d the workspace counters cover", p.tiles,
+             G_MAX_TILES);
+  if (ws == nullptr || ws_bytes < p.bytes || reinterpret_cast<uintptr_t>(ws) % 256 != 0) {
+    set_error("skinny gemm: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed, got %zu", p.bytes,
+              ws == nullptr ? size_t(0) : ws_bytes);
     return NS_E_WORKSPACE;
   }
+  unsigned char* b = static_cast<unsigned char*>(ws);
+  a.cnt = reinterpret_cast<unsigned*>(b + p.cnt_off);
+  a.part = reinterpret_cast<float*>(b + p.part_off);
+  a.tiles = p.tiles;
+  a.chunks = p.chunks;
+  a.whole = p.whole;
+  a.ks = p.ks;
   return NS_OK;
 }
+
+template <int EPI, bool NX>
+static void launch_nx(const GemmArgs& a, hipStream_t st) {
+  const dim3 grid(unsigned(a.whole + (a.tiles - a.whole) * a.ks)), block(G_WAVES * 64);
+  if (a.M <= 16)
+    hipLaunchKernelGGL((skinny_gemm_kernel<1, EPI, NX>), grid, block, 0, st, a);
+  else if (a.M <= 32)
+    hipLaunchKernelGGL((skinny_gemm_kernel<2, EPI, NX>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<4, EPI, NX>), grid, block, 0, st, a);
+}
+template <int EPI>
+static int launch(const GemmArgs& a, hipStream_t st) {
+  if constexpr (EPI == EPI_RESNORM) {
+    launch_nx<EPI, false>(a, st);
+  } else {
+    if (a.xsq != nullptr)
+      launch_nx<EPI, true>(a, st);
+    else
+      launch_nx<EPI, false>(a, st);
+  }
+  return check_launch("skinny_gemm");
+}
+
+// Optional normalised input (x holds r; see the file comment): sumsq NULL = plain x.
+static int bind_xnorm(GemmArgs& a, const float* x_sumsq, const void* x_norm_w, float x_eps) {
+  NS_REQUIRE(x_sumsq == nullptr || (x_norm_w != nullptr && reinterpret_cast<uintptr_t>(x_norm_w) % 16 == 0 &&
+                                     a.K % 8 == 0),
+             "skinny gemm: a normalised input needs a 16-byte aligned norm weight and K %% 8 == 0");
+  a.xsq = x_sumsq;
+  a.xnw = static_cast<const bf16_t*>(x_norm_w);
+  a.xeps = x_eps;
+  return NS_OK;
+}
+
+static GemmArgs base_args(const void* x, const void* w, int M, int N, int K) {
+  GemmArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.w = static_cast<const bf16_t*>(w);
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  return a;
+}
+
+static bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 }  // namespace ns
 
 using namespace ns;
 
+// Largest workspace any entry point needs for this shape (the SILU plan has at most as many tiles).
 extern "C" size_t ns_gemm_workspace_bytes(int M, int N, int K) {
   if (M < 1 || N < 1 || K < 32) return 0;
-  const int ksplit = pick_ksplit((N + 63) / 64, K);
-  return size_t(ksplit) * M * N * sizeof(float);
+  return make_plan((N + 63) / 64, K).bytes;
 }
 
 extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, int dtype,
-                       void* ws, size_t ws_bytes, void* stream) {
+                       const float* x_sumsq, const void* x_norm_w, float x_eps, void* ws, size_t ws_bytes,
+                       void* stream) {
   int st = check_common(x, w, M, N, K, dtype);
   if (st != NS_OK) return st;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int tiles = (N + 63) / 64;
-  const int ksplit = pick_ksplit(tiles, K);
-  if (ksplit == 1)
-    return launch_main<GEMM_PLAIN>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w),
-                                   static_cast<const bf16_t*>(bias), static_cast<bf16_t*>(y), nullptr, M, N, K, tiles, 1, s);
-  if ((st = need_ws(ws, ws_bytes, ksplit, M, N)) != NS_OK) return st;
-  st = launch_main<GEMM_PARTIAL>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w), nullptr, nullptr,
-                                 static_cast<float*>(ws), M, N, K, tiles, ksplit, s);
-  if (st != NS_OK) return st;
-  NS_REQUIRE(N % 4 == 0, "gemm: split-K needs N %% 4 == 0 (N=%d)", N);
-  hipLaunchKernelGGL(splitk_bias_kernel, dim3(unsigned((N / 4 + 255) / 256), unsigned(M)), dim3(256), 0, s,
-                     static_cast<const float*>(ws), static_cast<const bf16_t*>(bias), static_cast<bf16_t*>(y), M, N,
-                     ksplit);
-  return check_launch("gemm split-K epilogue");
+  NS_REQUIRE(y != nullptr && aligned16(y), "gemm: output must be 16-byte aligned");
+  GemmArgs a = base_args(x, w, M, N, K);
+  a.bias = static_cast<const bf16_t*>(bias);
+  a.y = static_cast<bf16_t*>(y);
+  if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
+  if ((st = bind_workspace(a, make_plan((N + 63) / 64, K), ws, ws_bytes)) != NS_OK) return st;
+  return launch<EPI_STORE>(a, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int N2, int K, int dtype,
+                                const float* x_sumsq, const void* x_norm_w, float x_eps, void* ws, size_t ws_bytes,
                                 void* stream) {
   int st = check_common(x, w_gate_up, M, N2, K, dtype);
   if (st != NS_OK) return st;
   NS_REQUIRE(N2 % 2 == 0, "gemm_silu_mul: merged gate/up rows %d must be even", N2);
-  const int tiles = (N2 / 2 + 31) / 32;
-  return launch_main<GEMM_SILU>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w_gate_up), nullptr,
-                                static_cast<bf16_t*>(out), nullptr, M, N2, K, tiles, 1, reinterpret_cast<hipStream_t>(stream));
+  NS_REQUIRE(out != nullptr && aligned16(out), "gemm_silu_mul: output must be 16-byte aligned");
+  GemmArgs a = base_args(x, w_gate_up, M, N2, K);
+  a.y = static_cast<bf16_t*>(out);
+  if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
+  if ((st = bind_workspace(a, make_plan((N2 / 2 + 31) / 32, K), ws, ws_bytes)) != NS_OK) return st;
+  return launch<EPI_SILU>(a, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int ns_gemm_residual_rms_norm(const void* x, const void* w, const void* residual, void* res_out,
-                                         const void* norm_w, void* h, float eps, int M, int N, int K, int dtype,
-                                         void* ws, size_t ws_bytes, void* stream) {
+extern "C" int ns_gemm_residual_norm_stats(const void* x, const void* w, const void* residual, void* res_out,
+                                           float* row_sumsq, int M, int N, int K, int dtype, void* ws,
+                                           size_t ws_bytes, void* stream) {
   int st = check_common(x, w, M, N, K, dtype);
   if (st != NS_OK) return st;
-  NS_REQUIRE(N % 4 == 0 && N <= 4 * EPI_THREADS, "gemm_residual_rms_norm: row length %d (multiple of 4, <= %d)", N,
-             4 * EPI_THREADS);
-  NS_REQUIRE(residual != nullptr && res_out != nullptr, "gemm_residual_rms_norm: residual and res_out required");
-  NS_REQUIRE(norm_w == nullptr || h != nullptr, "gemm_residual_rms_norm: norm weight given without output");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int tiles = (N + 63) / 64;
-  const int ksplit = pick_ksplit(tiles, K);
-  if ((st = need_ws(ws, ws_bytes, ksplit, M, N)) != NS_OK) return st;
-  st = launch_main<GEMM_PARTIAL>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w), nullptr, nullptr,
-                                 static_cast<float*>(ws), M, N, K, tiles, ksplit, s);
-  if (st != NS_OK) return st;
-  hipLaunchKernelGGL(splitk_residual_rmsnorm_kernel, dim3(M), dim3(unsigned((N / 4 + 63) / 64 * 64)), 0, s, static_cast<const float*>(ws),
-                     static_cast<const bf16_t*>(residual), static_cast<bf16_t*>(res_out),
-                     static_cast<const bf16_t*>(norm_w), static_cast<bf16_t*>(h), M, N, ksplit, eps);
-  return check_launch("gemm residual/rms_norm epilogue");
+  NS_REQUIRE(N % 8 == 0, "gemm_residual_norm_stats: row length %d must be a multiple of 8", N);
+  NS_REQUIRE(residual != nullptr && res_out != nullptr, "gemm_residual_norm_stats: residual and res_out required");
+  NS_REQUIRE(aligned16(residual) && aligned16(res_out), "gemm_residual_norm_stats: operands must be 16-byte aligned");
+  GemmArgs a = base_args(x, w, M, N, K);
+  a.residual = static_cast<const bf16_t*>(residual);
+  a.res_out = static_cast<bf16_t*>(res_out);
+  a.sumsq_out = row_sumsq;
+  if ((st = bind_workspace(a, make_plan((N + 63) / 64, K), ws, ws_bytes)) != NS_OK) return st;
+  return launch<EPI_RESNORM>(a, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int ns_rms_norm_apply(const void* r, const float* row_sumsq, const void* norm_w, float eps, void* h,
+                                 int64_t rows, int n, int dtype, void* stream) {
+  NS_REQUIRE(dtype == NS_DTYPE_BF16, "rms_norm_apply: bf16 only (dtype %d)", dtype);
+  NS_REQUIRE(rows >= 0 && rows <= G_MAX_M && n >= 8 && n % 8 == 0, "rms_norm_apply: rows=%lld n=%d (rows <= %d, n %% 8 == 0)",
+             (long long)rows, n, G_MAX_M);
+  NS_REQUIRE(r != nullptr && row_sumsq != nullptr && norm_w != nullptr && h != nullptr && aligned16(r) &&
+                 aligned16(norm_w) && aligned16(h),
+             "rms_norm_apply: null or misaligned operand");
+  if (rows == 0) return NS_OK;
+  hipLaunchKernelGGL(rms_norm_apply_kernel, dim3(unsigned(rows)), dim3(64), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const bf16_t*>(r), row_sumsq, static_cast<const bf16_t*>(norm_w), static_cast<bf16_t*>(h),
+                     n, eps);
+  return check_launch("rms_norm_apply");
 }
 
 extern "C" int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void* cos, const void* sin,
                                 void* q, void* k, void* v, void* k_cache, void* v_cache, const int64_t* slots, int M,
-                                int K, int n_heads, int n_kv_heads, int head_dim, int dtype, void* ws, size_t ws_bytes,
-                                void* stream) {
+                                int K, int n_heads, int n_kv_heads, int head_dim, int dtype, const float* x_sumsq,
+                                const void* x_norm_w, float x_eps, void* ws, size_t ws_bytes, void* stream) {
+  NS_REQUIRE(head_dim == 64 || head_dim == 128, "gemm_rope_qkv: head_dim %d (64 or 128)", head_dim);
+  NS_REQUIRE(n_heads >= 1 && n_kv_heads >= 1, "gemm_rope_qkv: heads %d / %d", n_heads, n_kv_heads);
   const int N = (n_heads + 2 * n_kv_heads) * head_dim;
   int st = check_common(x, w, M, N, K, dtype);
   if (st != NS_OK) return st;
-  NS_REQUIRE(head_dim % 2 == 0 && N % 4 == 0 && N <= ROPE_MAX_WIDTH, "gemm_rope_qkv: width %d / head_dim %d unsupported",
-             N, head_dim);
   NS_REQUIRE((k_cache == nullptr) == (v_cache == nullptr) && (k_cache == nullptr || slots != nullptr),
              "gemm_rope_qkv: give both caches and slots, or none");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int tiles = (N + 63) / 64;
-  const int ksplit = pick_ksplit(tiles, K);
-  if ((st = need_ws(ws, ws_bytes, ksplit, M, N)) != NS_OK) return st;
-  st = launch_main<GEMM_PARTIAL>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w), nullptr, nullptr,
-                                 static_cast<float*>(ws), M, N, K, tiles, ksplit, s);
-  if (st != NS_OK) return st;
-  hipLaunchKernelGGL(splitk_bias_rope_kernel, dim3(M), dim3(unsigned((N / 4 + 63) / 64 * 64)), 0, s, static_cast<const float*>(ws),
-                     static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(cos), static_cast<const bf16_t*>(sin),
-                     static_cast<bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
-                     static_cast<bf16_t*>(k_cache), static_cast<bf16_t*>(v_cache), slots, M, n_heads, n_kv_heads,
-                     head_dim, ksplit);
-  return check_launch("gemm rope/qkv epilogue");
+  NS_REQUIRE(cos != nullptr && sin != nullptr && q != nullptr && k != nullptr && v != nullptr,
+             "gemm_rope_qkv: null operand");
+  NS_REQUIRE(aligned16(cos) && aligned16(sin) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(k_cache) &&
+                 aligned16(v_cache),
+             "gemm_rope_qkv: operands must be 16-byte aligned");
+  GemmArgs a = base_args(x, w, M, N, K);
+  a.bias = static_cast<const bf16_t*>(bias);
+  a.cosb = static_cast<const bf16_t*>(cos);
+  a.sinb = static_cast<const bf16_t*>(sin);
+  a.q = static_cast<bf16_t*>(q);
+  a.k = static_cast<bf16_t*>(k);
+  a.v = static_cast<bf16_t*>(v);
+  a.kc = static_cast<bf16_t*>(k_cache);
+  a.vc = static_cast<bf16_t*>(v_cache);
+  a.slots = slots;
+  a.nh = n_heads;
+  a.nkv = n_kv_heads;
+  a.hd = head_dim;
+  if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
+  if ((st = bind_workspace(a, make_plan(N / 64, K), ws, ws_bytes)) != NS_OK) return st;
+  return launch<EPI_ROPE>(a, reinterpret_cast<hipStream_t>(stream));
 }

@@ -42,6 +42,64 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Hand-off of data between workgroups of one launch without device-scope fences. On gfx950 an
+// agent-scope release/acquire fence writes back / invalidates the whole L2 of the XCD, which costs
+// tens of nanoseconds per workgroup, serialised. Instead the data itself moves through agent-scope
+// atomic stores and loads, which are coherent across XCDs (they bypass the non-coherent L2), and
+// ordering comes from waiting for those stores to complete before the counter update that
+// publishes them (release side), and from the counter's returned value being consumed before the
+// data loads issue (acquire side). This is the publication scheme rocPRIM's look-back scan uses on
+// gfx942/gfx950.
+__device__ __forceinline__ void publish_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_store(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float publish_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t publish_load(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16-byte forms (a single agent-scope vector store / load: the compiler has no 128-bit atomic, so these
+// are written out; it does not count them in its own wait bookkeeping, which only makes its waits
+// stronger). A batch of publish_load16_issue calls is completed by publish_load16_wait on the same
+// registers, which waits for every load of the wave and pins the registers' uses after that wait.
+typedef __attribute__((ext_vector_type(4))) unsigned int pub_u32x4_t;
+__device__ __forceinline__ void publish_store16(void* p, pub_u32x4_t v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ pub_u32x4_t publish_load16_issue(const void* p) {
+  pub_u32x4_t v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=&v"(v) : "v"(p) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void publish_load16_wait(pub_u32x4_t (&v)[N]) {
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+// Every vector memory operation this wave issued so far has completed (s_waitcnt vmcnt(0)); with the
+// workgroup-scope fence the compiler keeps the preceding stores before it.
+__device__ __forceinline__ void publish_complete() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt left at their maxima
+}
+// Counter update of a publication: returns the previous value (one lane per workgroup calls it).
+__device__ __forceinline__ unsigned publish_count(unsigned* c) {
+  return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_reset(unsigned* c) {
+  __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// After a counter read that says every publisher is done: no later load may move above it.
+__device__ __forceinline__ void acquire_published() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 // Host side: error slot and launch checking.
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);

@@ -7,12 +7,18 @@ epilogues; larger products (prefill chunks) and fp32 go to the vendor GEMM throu
 ROCm) followed by the standalone HIP token-wise kernels. Both routes round where the unfused PyTorch ops
 round, so they differ only in the fp32 summation order of the products.
 
+RMSNorm between projections is not a pass of its own on the skinny route: the projection that produces
+the residual stream also writes per-64-column row sums of its square, and the projection that consumes
+rms_norm(residual) normalises its input fragments as it loads them ("norm on load"). Such an input is a
+NormedRows (r, row_sumsq, weight, eps); NormedRows.tensor() materialises h with the same arithmetic.
+
 Fused entry points (each with the unfused composition it equals):
   linear(x, w, b)                                   F.linear(x, w, b)
   linear_silu_mul(x, w_gate_up)                     silu_mul(F.linear(x, w_gate_up))
   linear_residual_rms_norm(x, w, residual, nw, eps) rms_norm(F.linear(x, w), nw, eps, residual=residual)
                                                     -> (h, residual + F.linear(x, w)); nw=None -> (None, sum)
   linear_rope_qkv(x, w, b, cos, sin, ...)           rope_qkv(F.linear(x, w, b), cos, sin, ...)
+where x may be a tensor or a NormedRows, and h comes back as a NormedRows on the skinny route.
 """
 from __future__ import annotations
 
@@ -23,6 +29,7 @@ from nanoserve_amd import _lib
 from nanoserve_amd.kernels.fused import rms_norm, rope_qkv, silu_mul
 
 SKINNY_MAX_M = 64
+NORM_TILE = 64   # columns per row-sum partial of a NormedRows
 
 _WS: dict[int, torch.Tensor] = {}
 _WS_RETIRED: list[torch.Tensor] = []   # superseded buffers stay alive: captured graphs may point at them
@@ -38,52 +45,107 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
             raise RuntimeError("skinny GEMM workspace must be sized by an eager call before graph capture")
         if ws is not None:
             _WS_RETIRED.append(ws)
-        ws = torch.empty(max(nbytes, 1 << 22), dtype=torch.uint8, device=device)
+        # zero-filled once: the kernels' tile counters start at zero and every call leaves them there
+        ws = torch.zeros(max(nbytes, 1 << 22), dtype=torch.uint8, device=device)
         _WS[idx] = ws
     return ws
 
 
-def skinny_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
-    M, K = x.shape
-    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.device.type == "cuda" and 1 <= M <= SKINNY_MAX_M
-            and K % 32 == 0 and x.is_contiguous() and w.is_contiguous() and x.data_ptr() % 16 == 0
+class NormedRows:
+    """rms_norm(r) held as r (bf16 [M, K]) plus the row statistics of r: sumsq (fp32 [ceil(K/64), 64],
+    column m = row m, each entry the sum of r^2 over 64 columns), the norm weight [K] and eps."""
+
+    def __init__(self, r: torch.Tensor, sumsq: torch.Tensor, weight: torch.Tensor, eps: float):
+        self.r, self.sumsq, self.weight, self.eps = r, sumsq, weight, float(eps)
+        self._h: torch.Tensor | None = None
+
+    @property
+    def shape(self):
+        return self.r.shape
+
+    @property
+    def dtype(self):
+        return self.r.dtype
+
+    @property
+    def device(self):
+        return self.r.device
+
+    def tensor(self) -> torch.Tensor:
+        """h = rms_norm(r), bitwise what the GEMMs compute on load."""
+        if self._h is None:
+            M, K = self.r.shape
+            h = torch.empty_like(self.r)
+            _lib.check(_lib.lib().ns_rms_norm_apply(self.r.data_ptr(), self.sumsq.data_ptr(), self.weight.data_ptr(),
+                                                    self.eps, h.data_ptr(), M, K, 1, _lib.stream_of(self.r)),
+                       "rms_norm_apply")
+            self._h = h
+        return self._h
+
+    def rows(self, idx: torch.Tensor) -> "NormedRows":
+        """The rows idx (in that order) as a NormedRows."""
+        n = idx.shape[0]
+        sq = torch.zeros(self.sumsq.shape[0], NORM_TILE, dtype=self.sumsq.dtype, device=self.sumsq.device)
+        sq[:, :n] = self.sumsq[:, idx]
+        return NormedRows(self.r[idx].contiguous(), sq, self.weight, self.eps)
+
+
+def _dense(x) -> torch.Tensor:
+    return x.tensor() if isinstance(x, NormedRows) else x
+
+
+def skinny_ok(x, w: torch.Tensor) -> bool:
+    t = x.r if isinstance(x, NormedRows) else x
+    M, K = t.shape
+    return (t.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and t.device.type == "cuda" and 1 <= M <= SKINNY_MAX_M
+            and K % 32 == 0 and t.is_contiguous() and w.is_contiguous() and t.data_ptr() % 16 == 0
             and w.data_ptr() % 16 == 0)
 
 
-def _ws_args(x: torch.Tensor, N: int):
+def _x_args(x):
+    """(x pointer, x_sumsq, x_norm_w, x_eps) of a tensor or NormedRows input."""
+    if isinstance(x, NormedRows):
+        return x.r.data_ptr(), x.sumsq.data_ptr(), x.weight.data_ptr(), x.eps
+    return x.data_ptr(), None, None, 0.0
+
+
+def _ws_args(x, N: int):
     M, K = x.shape
     ws = _workspace(x.device, _lib.lib().ns_gemm_workspace_bytes(M, N, K))
     return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
+def linear(x, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
     if not skinny_ok(x, w):
-        return F.linear(x, w, b)
+        return F.linear(_dense(x), w, b)
     M, K = x.shape
     N = w.shape[0]
     y = torch.empty(M, N, device=x.device, dtype=x.dtype)
     wsp, wsn = _ws_args(x, N)
-    _lib.check(_lib.lib().ns_gemm(x.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), M, N, K, 1, wsp, wsn,
-                                  _lib.stream_of(x)), "linear")
+    xp, sq, nw, eps = _x_args(x)
+    _lib.check(_lib.lib().ns_gemm(xp, w.data_ptr(), _lib.ptr(b), y.data_ptr(), M, N, K, 1, sq, nw, eps, wsp, wsn,
+                                  _lib.stream_of(w)), "linear")
     return y
 
 
-def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+def linear_silu_mul(x, w_gate_up: torch.Tensor) -> torch.Tensor:
     if not skinny_ok(x, w_gate_up):
-        return silu_mul(F.linear(x, w_gate_up))
+        return silu_mul(F.linear(_dense(x), w_gate_up))
     M, K = x.shape
     N2 = w_gate_up.shape[0]
     out = torch.empty(M, N2 // 2, device=x.device, dtype=x.dtype)
-    _lib.check(_lib.lib().ns_gemm_silu_mul(x.data_ptr(), w_gate_up.data_ptr(), out.data_ptr(), M, N2, K, 1,
-                                           _lib.stream_of(x)), "linear_silu_mul")
+    wsp, wsn = _ws_args(x, N2)
+    xp, sq, nw, eps = _x_args(x)
+    _lib.check(_lib.lib().ns_gemm_silu_mul(xp, w_gate_up.data_ptr(), out.data_ptr(), M, N2, K, 1, sq, nw, eps, wsp, wsn,
+                                           _lib.stream_of(w_gate_up)), "linear_silu_mul")
     return out
 
 
 def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor | None,
                              eps: float):
     """(rms_norm(residual + x W^T), residual + x W^T) with the sum rounded to the dtype; norm_w None -> (None, sum).
-    x [M, K], residual [M, N]."""
-    if not skinny_ok(x, w) or not residual.is_contiguous():
+    x [M, K], residual [M, N]. On the skinny route the first element is a NormedRows."""
+    if not skinny_ok(x, w) or not residual.is_contiguous() or w.shape[0] % 8 != 0:
         y = F.linear(x, w)
         if norm_w is None:
             return None, residual + y
@@ -91,18 +153,20 @@ def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.T
     M, K = x.shape
     N = w.shape[0]
     res_out = torch.empty(M, N, device=x.device, dtype=x.dtype)
-    h = torch.empty(M, N, device=x.device, dtype=x.dtype) if norm_w is not None else None
+    sumsq = torch.empty(-(-N // NORM_TILE), NORM_TILE, device=x.device, dtype=torch.float32) if norm_w is not None else None
     wsp, wsn = _ws_args(x, N)
-    _lib.check(_lib.lib().ns_gemm_residual_rms_norm(
-        x.data_ptr(), w.data_ptr(), residual.data_ptr(), res_out.data_ptr(), _lib.ptr(norm_w), _lib.ptr(h),
-        float(eps), M, N, K, 1, wsp, wsn, _lib.stream_of(x)), "linear_residual_rms_norm")
-    return h, res_out
+    _lib.check(_lib.lib().ns_gemm_residual_norm_stats(
+        x.data_ptr(), w.data_ptr(), residual.data_ptr(), res_out.data_ptr(), _lib.ptr(sumsq), M, N, K, 1, wsp, wsn,
+        _lib.stream_of(x)), "linear_residual_rms_norm")
+    if norm_w is None:
+        return None, res_out
+    return NormedRows(res_out, sumsq, norm_w, eps), res_out
 
 
-def linear_rope_qkv(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
+def linear_rope_qkv(x, w: torch.Tensor, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
                     n_heads: int, n_kv_heads: int, head_dim: int, k_cache=None, v_cache=None, slots=None):
-    if not skinny_ok(x, w) or not (cos.is_contiguous() and sin.is_contiguous()):
-        return rope_qkv(F.linear(x, w, b), cos, sin, n_heads, n_kv_heads, head_dim, k_cache, v_cache, slots)
+    if not skinny_ok(x, w) or not (cos.is_contiguous() and sin.is_contiguous()) or head_dim not in (64, 128):
+        return rope_qkv(F.linear(_dense(x), w, b), cos, sin, n_heads, n_kv_heads, head_dim, k_cache, v_cache, slots)
     M, K = x.shape
     N = w.shape[0]
     assert N == (n_heads + 2 * n_kv_heads) * head_dim and cos.shape == (M, head_dim) and sin.shape == (M, head_dim)
@@ -113,8 +177,9 @@ def linear_rope_qkv(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, co
     k = torch.empty(M, n_kv_heads, head_dim, device=x.device, dtype=x.dtype)
     v = torch.empty_like(k)
     wsp, wsn = _ws_args(x, N)
+    xp, sq, nw, eps = _x_args(x)
     _lib.check(_lib.lib().ns_gemm_rope_qkv(
-        x.data_ptr(), w.data_ptr(), _lib.ptr(b), cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr(),
+        xp, w.data_ptr(), _lib.ptr(b), cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr(),
         v.data_ptr(), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(slots) if k_cache is not None else None,
-        M, K, n_heads, n_kv_heads, head_dim, 1, wsp, wsn, _lib.stream_of(x)), "linear_rope_qkv")
+        M, K, n_heads, n_kv_heads, head_dim, 1, sq, nw, eps, wsp, wsn, _lib.stream_of(w)), "linear_rope_qkv")
     return q, k, v

@@ -359,20 +359,23 @@ class Qwen2Model:
             next_norm = self.layers[i + 1].ln1 if i + 1 < L else self.norm
             h, x = self._mlp(i, x, o, next_norm)       # h: the next layer's normed input / the final norm
         self._rows_cache = None
-        return self.lm_head_rows(h[None], seqs, logits)
+        return self.lm_head_rows(h, seqs, logits)
 
-    def lm_head_rows(self, x: torch.Tensor, seqs: list[SeqInput], logits="last") -> torch.Tensor:
-        """Final-normed hidden states [1, N, H] -> logits of the requested rows."""
-        from nanoserve_amd.kernels.linear import linear
+    def lm_head_rows(self, x, seqs: list[SeqInput], logits="last") -> torch.Tensor:
+        """Final-normed hidden states ([1, N, H] / [N, H] tensor, or a NormedRows) -> logits of the requested
+        rows."""
+        from nanoserve_amd.kernels.linear import NormedRows, linear
+        if isinstance(x, torch.Tensor) and x.dim() == 3:
+            x = x[0]
+        idx = None
         if isinstance(logits, torch.Tensor):
-            x = x[:, logits, :]
+            idx = logits
         elif logits == "last":
-            if len(seqs) == 1:
-                x = x[:, -1:, :]
-            else:
-                ends = torch.tensor([s.n_tokens for s in seqs], device=x.device).cumsum(0) - 1
-                x = x[:, ends, :]
-        return linear(x[0].contiguous(), self.lm_head)
+            ends = torch.tensor([s.n_tokens for s in seqs], device=x.device).cumsum(0) - 1
+            idx = ends
+        if idx is not None:
+            x = x.rows(idx) if isinstance(x, NormedRows) else x[idx]
+        return linear(x if isinstance(x, NormedRows) else x.contiguous(), self.lm_head)
 
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, cache=None, logits: str = "last"):
         raise NotImplementedError("the single-sequence contiguous-cache API (M1) is not part of the HIP path; "

@@ -111,7 +111,7 @@ def test_linear_residual_rms_norm(hiplib, M, N, K, norm):
         er = e + ulp(ref_r)
         rel = (er.abs() / rf.abs().clamp(min=1e-6)).max(dim=-1, keepdim=True).values.clamp(max=1.0)
         bound = nw.float().abs() * inv * (er + rf.abs() * rel) * 2
-        bf16_check(h, ops.rms_norm(ref_r, nw, 1e-6), "rms_norm of the sum", bound)
+        bf16_check(h.tensor(), ops.rms_norm(ref_r, nw, 1e-6), "rms_norm of the sum", bound)
     else:
         assert h is None
 
@@ -158,7 +158,7 @@ def test_deterministic_and_graph_replay(hiplib):
         a = linear(dx, dw)
         b = linear_silu_mul(dx2, dwgu)
         h, r = linear_residual_rms_norm(dx, dw, res, nw, 1e-6)
-        return a, b, h, r
+        return a, b, h.tensor(), r
 
     eager1 = [t.clone() for t in step()]
     eager2 = [t.clone() for t in step()]
@@ -174,3 +174,37 @@ def test_deterministic_and_graph_replay(hiplib):
         for a, b in zip(outs, eager1):
             assert torch.equal(a, b)
         step()   # eager work between replays
+
+
+@pytest.mark.parametrize("M", [1, 32, 64])
+@pytest.mark.parametrize("K", [1536, 896])
+def test_norm_on_load_equals_the_materialised_norm(hiplib, M, K):
+    """A projection of a NormedRows (r + its row statistics, normalised fragment by fragment as the GEMM
+    loads it) equals the same projection of NormedRows.tensor() bitwise, for every consumer kind, and row
+    selection (the LM head's) keeps that."""
+    from nanoserve_amd.kernels.linear import linear, linear_residual_rms_norm, linear_rope_qkv, linear_silu_mul
+    x0, w0 = operands(M, K, 512, seed=12)
+    res = torch.randn(M, K, generator=cpu_gen(13)).to(BF).cuda()
+    nw = (1 + 0.1 * torch.randn(K, generator=cpu_gen(14))).to(BF).cuda()
+    hn, r = linear_residual_rms_norm(x0.cuda(), w0.cuda(), res, nw, 1e-6)
+    h = hn.tensor()
+    assert torch.equal(h, hn.tensor())
+    # the materialised norm agrees with the oracle's rms_norm of the same r (different summation order)
+    ref = ops.rms_norm(r.cpu(), nw.cpu(), 1e-6)
+    same, ulps = ops.bf16_ulp_close(h.cpu(), ref)
+    assert same >= 0.99 and ulps <= 1.0, (same, ulps)
+
+    _, w = operands(M, 1000, K, seed=15)
+    b = (torch.randn(1000, generator=cpu_gen(16)) * 0.1).to(BF).cuda()
+    assert torch.equal(linear(hn, w.cuda(), b), linear(h, w.cuda(), b))
+    _, wgu = operands(M, 2 * 1024, K, seed=17)
+    assert torch.equal(linear_silu_mul(hn, wgu.cuda()), linear_silu_mul(h, wgu.cuda()))
+    nh, nkv, hd = 12, 2, 128
+    _, wq = operands(M, (nh + 2 * nkv) * hd, K, seed=18)
+    cos, sin = ops.rope_tables(torch.arange(M) + 7, hd, 1e6, BF)
+    qa = linear_rope_qkv(hn, wq.cuda(), None, cos.cuda(), sin.cuda(), nh, nkv, hd)
+    qb = linear_rope_qkv(h, wq.cuda(), None, cos.cuda(), sin.cuda(), nh, nkv, hd)
+    for a_, b_ in zip(qa, qb):
+        assert torch.equal(a_, b_)
+    idx = torch.arange(M - 1, -1, -2, device="cuda")
+    assert torch.equal(linear(hn.rows(idx), w.cuda()), linear(h[idx].contiguous(), w.cuda()))
