@@ -20,10 +20,12 @@
 //     4*r4 .. 4*r4+3, which are four coalesced row-slice loads, and a 4x4 register transpose
 //     (v_perm) turns them into the NT operand fragments. No LDS on the per-page path.
 //   * Softmax statistics per head: a lane's 4 tokens, then 2 butterfly shuffles (xor 16, xor 32).
-//   * Waves merge through LDS; a row with one partition writes its output directly, otherwise each
-//     partition writes (m, l, acc) to the workspace and a second small kernel merges them. (A
-//     last-block-done counter would need device-scope fences, which on gfx950 write back and
-//     invalidate the L2 of the XCD in every workgroup.)
+//   * Waves merge through LDS; a row with one partition writes its output directly. Otherwise each
+//     partition publishes (m, l, acc) to the workspace, bumps the row's arrival counter, and the last
+//     partition to arrive merges all of them in partition order and writes the output -- one launch.
+//     The hand-off uses agent-scope atomic stores/loads and a store-completion wait before the counter
+//     (ns_common.h, publish_*), not device-scope fences, which on gfx950 write back and invalidate the
+//     XCD's whole L2 in every workgroup.
 // fp32 design: one wave per (row, KV head), VALU dot products with wave reductions; kept simple,
 // it serves the fp32 correctness paths.
 #include "ns_common.h"
@@ -75,13 +77,17 @@ __device__ __forceinline__ Words<NW32> load_words(const bf16_t* p) {
 __device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
 __device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
+// Partitions per row (table width / partition pages) the kernel accepts.
+template <int HD>
+constexpr int MERGE_MAX_PARTS = 256;
+
 template <int HD>
 __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kernel(
     const bf16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, const bf16_t* __restrict__ kp,
     const bf16_t* __restrict__ vp, int64_t s_blk, int64_t s_pos, int64_t s_h, const int32_t* __restrict__ bt,
     int64_t bt_sb, const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G,
     int max_blocks, int num_blocks, float scale_log2, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    int B_, int nkv_, int n_parts) {
+    unsigned* __restrict__ ws_cnt, int B_, int nkv_, int n_parts) {
   constexpr int NW = DecodeCfg<HD>::NW, PPW = DecodeCfg<HD>::PPW, PART = NW * PPW;
   constexpr int KS = HD / 32;  // 32-dim k-steps of the QK^T product (8 bf16 per lane per step)
   constexpr int NT = HD / 16;  // 16-row output tiles of the PV product
@@ -231,95 +237,94 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
   __syncthreads();
 
   const int64_t bg = int64_t(b) * nkv + g;
-  for (int idx = tid; idx < G * HD; idx += NW * 64) {
-    const int h = idx / HD, d = idx - (idx / HD) * HD;
-    float M = -INFINITY;
+  // this partition's softmax state, 4 consecutive dims of one head per item
+  auto part_state = [&](int h, int d4, float& M, float& L, float (&A)[4]) __attribute__((always_inline)) {
+    M = -INFINITY;
 #pragma unroll
     for (int x = 0; x < NW; ++x) M = fmaxf(M, sm_m[x][h]);
     const float Mu = M == -INFINITY ? 0.f : M;
-    float L = 0.f, A = 0.f;
+    L = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) A[e] = 0.f;
 #pragma unroll
     for (int x = 0; x < NW; ++x) {
       const float wgt = exp2f(sm_m[x][h] - Mu);  // waves without live pages: m = -inf -> weight 0
       L += wgt * sm_l[x][h];
-      A += wgt * sm_acc[x][h * AROW + d];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) A[e] += wgt * sm_acc[x][h * AROW + 4 * d4 + e];
     }
-    if (n_active == 1) {
-      out[int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + d] = f32_to_bf16(A / L);
-    } else {
-      ws_acc[(bg * n_parts + part) * (16 * HD) + h * HD + d] = A;
-      if (d == 0) {
-        ws_ml[((bg * n_parts + part) * 16 + h) * 2 + 0] = M;
-        ws_ml[((bg * n_parts + part) * 16 + h) * 2 + 1] = L;
-      }
+  };
+  if (n_active == 1) {   // the row fits one partition: finish it here
+    for (int idx = tid; idx < G * (HD / 4); idx += NW * 64) {
+      const int h = idx / (HD / 4), d4 = idx - h * (HD / 4);
+      float M, L, A[4];
+      part_state(h, d4, M, L, A);
+      bf16_t* o = out + int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + 4 * d4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(A[e] / L);
     }
+    return;
   }
-}
-
-// Second pass of the split-K decode: for each (row, KV head) whose context spans more than one
-// partition, combine the partitions' (m, l, acc) with weights 2^(m_p - max m) / L. Rows that fit
-// one partition were finished by the first pass and are skipped.
-constexpr int MERGE_MAX_PARTS = 256;  // partitions per row the merge kernel handles
-constexpr int MERGE_BATCH = 8;        // partitions whose loads each thread keeps in flight
-
-template <int HD>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out,
-                                                                 int64_t o_sb, int64_t o_sh, int G, int max_blocks, int n_parts,
-                                                                 const float* __restrict__ ws_acc,
-                                                                 const float* __restrict__ ws_ml) {
-  constexpr int PART = DecodeCfg<HD>::NW * DecodeCfg<HD>::PPW;
-  const int g = blockIdx.x, b = blockIdx.y, nkv = gridDim.x;
-  const int ctx = ctxl[b];
-  int n_pages = ctx > 0 ? (ctx + PAGE - 1) / PAGE : 0;
-  if (n_pages > max_blocks) n_pages = max_blocks;
-  const int n_active = (n_pages + PART - 1) / PART;
-  if (n_active <= 1) return;
-  const int64_t bg = int64_t(b) * nkv + g;
-  const float* ml = ws_ml + bg * n_parts * 32;           // [part][16 heads][m, l]
-  const float* accp = ws_acc + bg * n_parts * (16 * HD);  // [part][16 heads][HD]
-  __shared__ float sm[MERGE_MAX_PARTS][16];               // m, then the merge weight
-  __shared__ float sl[MERGE_MAX_PARTS][16];
-  for (int i = threadIdx.x; i < n_active * 16; i += blockDim.x) {
-    sm[i >> 4][i & 15] = ml[(i >> 4) * 32 + (i & 15) * 2];
-    sl[i >> 4][i & 15] = ml[(i >> 4) * 32 + (i & 15) * 2 + 1];
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int h = threadIdx.x;
-    float M = -INFINITY;
-    for (int x = 0; x < n_active; ++x) M = fmaxf(M, sm[x][h]);
-    float L = 0.f;
-    for (int x = 0; x < n_active; ++x) L += exp2f(sm[x][h] - M) * sl[x][h];
-    const float inv = 1.0f / L;
-    for (int x = 0; x < n_active; ++x) sm[x][h] = exp2f(sm[x][h] - M) * inv;
-  }
-  __syncthreads();
-  // each thread: 4 consecutive dims of one head; MERGE_BATCH partitions' 16-byte loads in flight
-  for (int idx = threadIdx.x; idx < G * (HD / 4); idx += blockDim.x) {
+  // Publish this partition's (m, l, acc); the last partition of the row to arrive merges all of them
+  // in partition order (so the result does not depend on arrival order) and writes the output.
+  for (int idx = tid; idx < G * (HD / 4); idx += NW * 64) {
     const int h = idx / (HD / 4), d4 = idx - h * (HD / 4);
-    const float* src = accp + h * HD + 4 * d4;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int x0 = 0; x0 < n_active; x0 += MERGE_BATCH) {
-      float4 u[MERGE_BATCH];
+    float M, L, A[4];
+    part_state(h, d4, M, L, A);
+    const pub_u32x4_t bits = {__float_as_uint(A[0]), __float_as_uint(A[1]), __float_as_uint(A[2]), __float_as_uint(A[3])};
+    publish_store16(ws_acc + ((bg * n_parts + part) * 16 + h) * HD + 4 * d4, bits);
+    if (d4 == 0) {
+      publish_store(ws_ml + ((bg * n_parts + part) * 16 + h) * 2 + 0, M);
+      publish_store(ws_ml + ((bg * n_parts + part) * 16 + h) * 2 + 1, L);
+    }
+  }
+  publish_complete();
+  __shared__ unsigned s_last;
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = publish_count(ws_cnt + bg);
+    const unsigned last = prev == unsigned(n_active - 1);
+    if (last) publish_reset(ws_cnt + bg);
+    s_last = last;
+  }
+  __syncthreads();
+  if (s_last == 0u) return;
+  acquire_published();
+  // Merge in partition order with a running max: every thread loads, for its head and 4 dims, the (m, l,
+  // acc) of MB partitions at once (one memory latency per MB partitions) and folds them in.
+  const float* ml = ws_ml + bg * n_parts * 32;
+  const float* accp = ws_acc + bg * n_parts * (16 * HD);
+  constexpr int MB = 8;
+  for (int idx = tid; idx < G * (HD / 4); idx += NW * 64) {
+    const int h = idx / (HD / 4), d4 = idx - h * (HD / 4);
+    float M = -INFINITY, L = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int x0 = 0; x0 < n_active; x0 += MB) {
+      pub_u32x4_t u[MB];
+      float pm[MB], pl[MB];
 #pragma unroll
-      for (int e = 0; e < MERGE_BATCH; ++e) {
+      for (int e = 0; e < MB; ++e) {
         const int x = min(x0 + e, n_active - 1);
-        u[e] = *reinterpret_cast<const float4*>(src + int64_t(x) * (16 * HD));
+        u[e] = publish_load16_issue(accp + int64_t(x) * (16 * HD) + h * HD + 4 * d4);
+        pm[e] = publish_load(ml + x * 32 + h * 2);
+        pl[e] = publish_load(ml + x * 32 + h * 2 + 1);
       }
+      publish_load16_wait(u);
 #pragma unroll
-      for (int e = 0; e < MERGE_BATCH; ++e) {
-        const float wgt = (x0 + e < n_active) ? sm[min(x0 + e, n_active - 1)][h] : 0.f;
-        a.x += wgt * u[e].x;
-        a.y += wgt * u[e].y;
-        a.z += wgt * u[e].z;
-        a.w += wgt * u[e].w;
+      for (int e = 0; e < MB; ++e) {
+        if (x0 + e < n_active) {
+          const float Mn = fmaxf(M, pm[e]);
+          const float a_old = M == -INFINITY ? 0.f : exp2f(M - Mn), a_new = exp2f(pm[e] - Mn);
+          L = L * a_old + pl[e] * a_new;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) A[c] = A[c] * a_old + __uint_as_float(u[e][c]) * a_new;
+          M = Mn;
+        }
       }
     }
+    const float inv = 1.0f / L;
     bf16_t* o = out + int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + 4 * d4;
-    o[0] = f32_to_bf16(a.x);
-    o[1] = f32_to_bf16(a.y);
-    o[2] = f32_to_bf16(a.z);
-    o[3] = f32_to_bf16(a.w);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = f32_to_bf16(A[c] * inv);
   }
 }
 
@@ -392,13 +397,15 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 using namespace ns;
 
+// Workspace: [B * n_kv] arrival counters (zeroed once by the owner; every launch leaves them at zero),
+// then the partitions' (m, l) and accumulators.
 extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype) {
   if (dtype != NS_DTYPE_BF16 || B <= 0 || n_kv_heads <= 0 || max_blocks <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
   const size_t parts = size_t(decode_parts(head_dim, max_blocks));
   if (parts <= 1) return 0;
-  const size_t slots = size_t(B) * n_kv_heads * parts;
-  return align256(slots * 16 * 2 * sizeof(float)) +
+  const size_t rows = size_t(B) * n_kv_heads, slots = rows * parts;
+  return align256(rows * sizeof(unsigned)) + align256(slots * 16 * 2 * sizeof(float)) +
          align256(slots * 16 * size_t(head_dim) * sizeof(float));
 }
 
@@ -444,21 +451,25 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                  0,
              "paged_attention_decode: q / k_pool / v_pool must be 16-byte aligned");
   const int parts = decode_parts(head_dim, max_blocks);
-  NS_REQUIRE(parts <= MERGE_MAX_PARTS, "paged_attention_decode: %d partitions (table width %d) exceed %d", parts,
-             max_blocks, MERGE_MAX_PARTS);
+  const int max_parts = head_dim == 64 ? MERGE_MAX_PARTS<64> : MERGE_MAX_PARTS<128>;
+  NS_REQUIRE(parts <= max_parts, "paged_attention_decode: %d partitions (table width %d) exceed %d", parts, max_blocks,
+             max_parts);
   float* ws_acc = nullptr;
   float* ws_ml = nullptr;
+  unsigned* ws_cnt = nullptr;
   if (parts > 1) {
     const size_t need = ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype);
     if (workspace == nullptr || workspace_bytes < need) {
-      set_error("paged_attention_decode: workspace of %zu bytes needed, got %zu", need,
+      set_error("paged_attention_decode: zero-initialised workspace of %zu bytes needed, got %zu", need,
                 workspace == nullptr ? size_t(0) : workspace_bytes);
       return NS_E_WORKSPACE;
     }
     NS_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "paged_attention_decode: workspace not 256-byte aligned");
-    const size_t slots = size_t(B) * n_kv_heads * parts;
-    ws_ml = static_cast<float*>(workspace);
-    ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(slots * 16 * 2 * sizeof(float)));
+    const size_t rows = size_t(B) * n_kv_heads, slots = rows * parts;
+    char* w = static_cast<char*>(workspace);
+    ws_cnt = reinterpret_cast<unsigned*>(w);
+    ws_ml = reinterpret_cast<float*>(w + align256(rows * sizeof(unsigned)));
+    ws_acc = reinterpret_cast<float*>(w + align256(rows * sizeof(unsigned)) + align256(slots * 16 * 2 * sizeof(float)));
   }
   const float sl2 = scale * LOG2E;
   const dim3 grid(unsigned(parts) * unsigned(n_kv_heads) * unsigned(B));
@@ -466,19 +477,13 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
     hipLaunchKernelGGL(paged_decode_bf16_kernel<64>, grid, dim3(DecodeCfg<64>::NW * 64), 0, s,
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
-                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, B, n_kv_heads, parts);
+                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, ws_cnt, B,
+                       n_kv_heads, parts);
   else
     hipLaunchKernelGGL(paged_decode_bf16_kernel<128>, grid, dim3(DecodeCfg<128>::NW * 64), 0, s,
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
-                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, B, n_kv_heads, parts);
-  int st = check_launch("paged_attention_decode(bf16)");
-  if (st != NS_OK || parts <= 1) return st;
-  if (head_dim == 64)
-    hipLaunchKernelGGL(paged_decode_merge_kernel<64>, dim3(n_kv_heads, B), dim3(256), 0, s, context_lens,
-                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, parts, ws_acc, ws_ml);
-  else
-    hipLaunchKernelGGL(paged_decode_merge_kernel<128>, dim3(n_kv_heads, B), dim3(256), 0, s, context_lens,
-                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, parts, ws_acc, ws_ml);
-  return check_launch("paged_attention_decode(bf16 merge)");
+                       static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, ws_cnt, B,
+                       n_kv_heads, parts);
+  return check_launch("paged_attention_decode(bf16)");
 }

@@ -9,10 +9,11 @@ q: [B, n_heads, head_dim] (last dim contiguous); k_pool / v_pool: ONE layer's po
 (padding entries never read); context_lens: int32 [B], including the new token whose K/V must already be
 written. Returns out = torch.empty_like(q) filled with the attention output.
 
-The bf16 kernel splits long contexts across workgroups; a second small kernel merges the partial softmax
-states. That merge needs a small device workspace; one per (device, B, n_kv_heads, head_dim, max_blocks) is
-allocated on first use (outside any graph capture: the graph runners warm up eagerly first) and reused by
-every later call and graph replay. Calls on one stream never overlap, so sharing it is safe.
+The bf16 kernel splits long contexts across workgroups; the last partition of a row to finish merges the
+partial softmax states (one launch). That needs a small device workspace; one per (device, B, n_kv_heads,
+head_dim, max_blocks) is allocated zero-filled on first use (outside any graph capture: the graph runners warm
+up eagerly first) and reused by every later call and graph replay. Calls on one stream never overlap, so
+sharing it is safe.
 """
 from __future__ import annotations
 
@@ -36,7 +37,8 @@ def decode_workspace(device: torch.device, B: int, n_kv_heads: int, head_dim: in
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("paged_attention_decode: first call for this shape happened inside a graph capture; "
                                "run one eager call (warm-up) before capturing")
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        # zero-filled once: the kernel's per-row arrival counters start at zero and every call leaves them there
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 
