@@ -51,11 +51,12 @@ const char* ns_version(void);
  * (a row with ctx_b <= 0 gets zeros). Guards that keep every access inside the caller's buffers:
  * a row's page count is clamped to max_blocks (the table width), and the tokens of a table entry
  * outside [0, num_blocks) are masked out (no memory outside the pool is read).
- * Long contexts are split into partitions that run in parallel (split-K); a second small kernel on
- * the same stream merges their partial softmax states. That needs `workspace` of at least
- * ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype) bytes (256-byte aligned; no
- * initialisation needed; 0 bytes means none is needed). Calls sharing a workspace must be ordered
- * (same stream), which every caller in the decode loop is.
+ * Long contexts are split into partitions that run in parallel (split-K); in the same launch the last
+ * partition of a row to finish merges their partial softmax states in partition order. That needs
+ * `workspace` of at least ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype) bytes
+ * (256-byte aligned, zero-filled once by the owner: it starts with per-row arrival counters, which every
+ * call leaves at zero; 0 bytes means none is needed). Calls sharing a workspace must be ordered (same
+ * stream), which every caller in the decode loop is.
  */
 int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                          const void* k_pool, const void* v_pool,
@@ -67,6 +68,33 @@ int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype);
+
+/*
+ * Paged chunked-prefill attention: several sequences' new tokens attend to their cached context plus
+ * themselves, causally. seq_info (device, int32 [n_seqs, 4]) holds per sequence s:
+ *   q_start (first row of s in q / out), n_new (T, its new tokens), ctx_len (tokens cached before this
+ *   step), and an unused fourth entry.
+ * New token j of s (absolute position ctx_len + j) and query head h (KV head g = h / (n_heads / n_kv_heads))
+ *   out[q_start + j, h, :] = softmax(q[q_start + j, h, :] . K[0 : ctx_len + j + 1]^T * scale) . V[...]
+ * with token t of s at pool block block_tables[s, t / block_size], position t % block_size; the new tokens'
+ * K/V must already be in the pages (rope_qkv writes them). This is the causal-offset mask of
+ * nanoserve/model.py:292-309 (continuation) and the causal SDPA of :310-318 (fresh prefill, ctx_len = 0),
+ * over the pages PagedKVCache.gather (kv_cache.py:281-288) would gather; the reference computes it with
+ * gather + repeat_interleave + SDPA. Online softmax in fp32; probabilities rounded to bf16 before P.V.
+ * max_new = max over s of n_new (it sizes the grid; sequences with fewer tokens exit early).
+ *
+ * Limits: bf16 only; head_dim in {64, 128}; block_size == 16; strides multiples of 8 elements and
+ * 16-byte aligned bases. Pages past ceil((ctx_len + n_new) / 16) are never read and a sequence's page
+ * count is clamped to max_blocks; the tokens of a table entry outside [0, num_blocks) are masked out.
+ * No workspace; rows of out that belong to no sequence are not written.
+ */
+int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh,
+                          const void* k_pool, const void* v_pool,
+                          int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                          const int32_t* block_tables, int64_t bt_sb, const int32_t* seq_info,
+                          int n_seqs, int max_new, void* out, int64_t o_st, int64_t o_sh,
+                          int n_heads, int n_kv_heads, int head_dim, int block_size,
+                          int max_blocks, int num_blocks, float scale, int dtype, void* stream);
 
 /*
  * RMSNorm over rows of length n (row-major, contiguous):

@@ -322,7 +322,13 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSourc
 // butterfly steps, which gives every lane of the 4 the same bits. Called by all 64 lanes of a wave.
 __device__ __forceinline__ float rms_norm_row_inv(const float* sumsq, int ptiles, int m, int r4, int K, float eps) {
   float part = 0.f;
-  for (int p = r4; p < ptiles; p += 4) part += sumsq[int64_t(p) * G_MAX_M + m];
+  for (int p0 = r4; p0 < ptiles; p0 += 32) {   // 8 loads in flight, added in tile order
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = p0 + 4 * e < ptiles ? sumsq[int64_t(p0 + 4 * e) * G_MAX_M + m] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part += v[e];
+  }
   part += __shfl_xor(part, 16, 64);
   part += __shfl_xor(part, 32, 64);
   return rsqrtf(part / float(K) + eps);

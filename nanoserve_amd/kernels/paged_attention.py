@@ -1,4 +1,5 @@
-"""Paged-attention DECODE on the GPU through the HIP kernel (csrc/paged_attention.hip).
+"""Paged attention on the GPU through the HIP kernels: decode (csrc/paged_attention.hip) and chunked
+prefill (csrc/prefill_attention.hip).
 
 Same entry point and argument meaning as nanoserve/kernels/paged_attention.py:85-105:
 
@@ -14,6 +15,14 @@ partial softmax states (one launch). That needs a small device workspace; one pe
 head_dim, max_blocks) is allocated zero-filled on first use (outside any graph capture: the graph runners warm
 up eagerly first) and reused by every later call and graph replay. Calls on one stream never overlap, so
 sharing it is safe.
+
+    paged_attention_prefill(q, k_pool, v_pool, block_tables, seq_info, max_new, scale, out=None) -> out
+
+The new tokens of several sequences at once (nanoserve/model.py:283-318, the per-sequence SDPA branch):
+q [N, n_heads, head_dim] holds the step's tokens; seq_info int32 [S, 4] (device) holds per sequence
+(q_start, n_new, ctx_len, 0); block_tables int32 [S, W]. Token j of sequence s attends to keys
+0 .. ctx_len + j of its pages, which must already hold the new tokens' K/V. Rows of `out` outside every
+sequence are left untouched. bf16 only; `prefill_seq_info` builds seq_info from host lists.
 """
 from __future__ import annotations
 
@@ -68,4 +77,38 @@ def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
         B, n_heads, n_kv_heads, head_dim, block_size, max_blocks, num_blocks, float(scale), _lib.dtype_code(q),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _lib.stream_of(q)),
         "paged_attention_decode")
+    return out
+
+
+def prefill_seq_info(q_starts: list[int], n_new: list[int], ctx_lens: list[int], device) -> torch.Tensor:
+    """int32 [S, 4] (q_start, n_new, ctx_len, 0) on `device`, from host lists."""
+    rows = [[a, b, c, 0] for a, b, c in zip(q_starts, n_new, ctx_lens)]
+    return torch.tensor(rows, dtype=torch.int32).reshape(-1, 4).to(device)
+
+
+def paged_attention_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
+                            seq_info: torch.Tensor, max_new: int, scale: float,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    N, n_heads, head_dim = q.shape
+    num_blocks, block_size, n_kv_heads, hd2 = k_pool.shape
+    assert hd2 == head_dim and q.dtype == k_pool.dtype == v_pool.dtype
+    assert q.stride(-1) == 1 and k_pool.stride(-1) == 1 and v_pool.stride() == k_pool.stride()
+    assert v_pool.shape == k_pool.shape
+    S = seq_info.shape[0]
+    assert seq_info.dtype == torch.int32 and seq_info.shape == (S, 4) and seq_info.is_contiguous()
+    assert block_tables.dtype == torch.int32 and block_tables.dim() == 2 and block_tables.shape[0] == S
+    assert block_tables.stride(1) == 1 or block_tables.shape[1] == 1
+    if out is None:
+        out = torch.empty_like(q)
+    assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
+    _lib.require_gpu(q, k_pool, v_pool, block_tables, seq_info, out)
+    if S == 0 or max_new == 0:
+        return out
+    _lib.check(_lib.lib().ns_paged_attn_prefill(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        block_tables.data_ptr(), block_tables.stride(0), seq_info.data_ptr(), S, int(max_new),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        n_heads, n_kv_heads, head_dim, block_size, block_tables.shape[1], num_blocks, float(scale),
+        _lib.dtype_code(q), _lib.stream_of(q)), "paged_attention_prefill")
     return out

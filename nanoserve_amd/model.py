@@ -11,15 +11,17 @@ the same way. The math of one layer on N flattened tokens (nanoserve/model.py:22
     x      = x + silu_mul(h @ [Wg;Wu]^T) @ Wd^T
 
 For decode-sized bf16 batches (M <= 64) each projection is one skinny HIP GEMM with the neighbouring op in
-its epilogue (kernels/linear.py): QKV + bias + RoPE + KV write; O + residual + RMSNorm; gate/up + SiLU*mul;
-down + residual + the NEXT RMSNorm (the next layer's ln1, or the final norm after the last layer), so a
-layer is 4 GEMM launches (+ split-K epilogues) and 2 attention launches. Larger batches use the vendor GEMM
+its epilogue (kernels/linear.py): QKV + bias + RoPE + KV write; O + residual + RMSNorm statistics;
+gate/up + SiLU*mul with ln2 applied on load; down + residual + statistics for the NEXT RMSNorm (the next
+layer's ln1, or the final norm after the last layer), applied on load by its consumer -- so a decode layer
+is 4 GEMM launches and 1 attention launch. Larger batches use the vendor GEMM
 and the standalone HIP kernels; both round where PyTorch's unfused ops round.
 
-Attention: one-token decode rows (DecodeMeta) and the tokens of prefill / chunked-prefill rows all go
-through the paged kernel. Prefill token j of a sequence with ctx_len cached tokens is a row whose context
-is ctx_len + j + 1 tokens of that sequence's table: exactly the causal offset mask of
-nanoserve/model.py:292-309, with K/V read in place from the pages rope_qkv has just written.
+Attention reads K/V in place from the pages rope_qkv has just written. One-token decode rows (DecodeMeta)
+go through the paged decode kernel; the tokens of prefill / chunked-prefill sequences go through the paged
+chunked-prefill kernel (bf16), where token j of a sequence with ctx_len cached tokens sees keys
+0 .. ctx_len + j: exactly the causal offset mask of nanoserve/model.py:292-309. In fp32 (the correctness
+configuration) those tokens run as decode rows with context ctx_len + j + 1, the same mask.
 
 Only the HIP path exists here: a CPU tensor, the contiguous cache or a missing kernel library raise. The
 unfused PyTorch restatement (the CPU oracle used by the tests) lives outside this package.
@@ -293,22 +295,30 @@ class Qwen2Model:
             o_dec = paged_attention_decode(q[0][decode_meta.token_idx], paged.k[i], paged.v[i],
                                            decode_meta.block_tables, decode_meta.context_lens, scale)
             o_all[0].index_copy_(0, decode_meta.token_idx, o_dec.reshape(o_dec.shape[0], -1))
-        rows = self._prefill_rows(seqs, paged, slot_mapping)
-        if rows is not None:
-            idx, tables, lens = rows
+        pre = self._prefill_meta(seqs, paged, slot_mapping, q.dtype)
+        if pre is not None and pre[0] == "chunks":
+            from nanoserve_amd.kernels.paged_attention import paged_attention_prefill
+            _, tables, info, max_new = pre
+            paged_attention_prefill(q[0], paged.k[i], paged.v[i], tables, info, max_new, scale,
+                                    out=o_all[0].view(N, nh, hd))
+        elif pre is not None:
+            _, idx, tables, lens = pre
             o_pf = paged_attention_decode(q[0][idx], paged.k[i], paged.v[i], tables, lens, scale)
             o_all[0].index_copy_(0, idx, o_pf.reshape(o_pf.shape[0], -1))
         return o_all
 
-    def _prefill_rows(self, seqs: list[SeqInput], paged, slot_mapping):
-        """(token index, block tables, context lengths) of every non-decode token of the step, one row per
-        token: token j of a sequence with ctx_len cached tokens sees ctx_len + j + 1 tokens. Cached per step
-        (all layers share it) on the SeqInput list object."""
+    def _prefill_meta(self, seqs: list[SeqInput], paged, slot_mapping, dtype: torch.dtype):
+        """Attention inputs of the step's non-decode tokens (prefills and chunk continuations), cached per
+        step (all layers share them):
+          bf16: ("chunks", tables int32 [S, W], seq_info int32 [S, 4], max_new) for the chunked-prefill kernel;
+          fp32: ("rows", token index, tables [n, W], context lengths [n]) -- one decode row per token, token j
+                of a sequence with ctx_len cached tokens seeing ctx_len + j + 1 tokens."""
         cache = getattr(self, "_rows_cache", None)
         if cache is not None and cache[0] is seqs and cache[1] is slot_mapping:
             return cache[2]
+        from nanoserve_amd.kernels.paged_attention import prefill_seq_info
         dev, bs = self.device, paged.block_size
-        idx_parts, lens_parts, tabs = [], [], []
+        tabs, starts, news, ctxs = [], [], [], []
         start = 0
         for s in seqs:
             T = s.n_tokens
@@ -316,24 +326,34 @@ class Qwen2Model:
                 n_pages = -(-(s.ctx_len + T) // bs)
                 if s.block_table is not None:
                     bt = s.block_table.to(device=dev, dtype=torch.int32)[:n_pages]
+                    if bt.shape[0] < n_pages:
+                        raise ValueError(f"block_table holds {bt.shape[0]} blocks, {n_pages} needed")
                 elif s.ctx_len == 0:
                     if slot_mapping is None:
                         raise ValueError("a fresh prefill without block_table needs slot_mapping")
                     bt = (slot_mapping[start:start + T:bs] // bs).to(torch.int32)
                 else:
                     raise ValueError("a continuation chunk (ctx_len > 0) needs its block_table")
-                idx_parts.append(torch.arange(start, start + T, device=dev))
-                lens_parts.append(torch.arange(s.ctx_len + 1, s.ctx_len + T + 1, device=dev, dtype=torch.int32))
-                tabs.append((bt, T))
+                tabs.append(bt)
+                starts.append(start)
+                news.append(T)
+                ctxs.append(s.ctx_len)
             start += T
-        if not idx_parts:
-            rows = None
+        if not tabs:
+            meta = None
         else:
-            width = max(bt.shape[0] for bt, _ in tabs)
-            tables = torch.cat([F.pad(bt, (0, width - bt.shape[0]))[None].expand(T, width) for bt, T in tabs])
-            rows = (torch.cat(idx_parts), tables.contiguous(), torch.cat(lens_parts))
-        self._rows_cache = (seqs, slot_mapping, rows)
-        return rows
+            width = max(bt.shape[0] for bt in tabs)
+            padded = [F.pad(bt, (0, width - bt.shape[0])) for bt in tabs]
+            if dtype == torch.bfloat16:
+                meta = ("chunks", torch.stack(padded).contiguous(), prefill_seq_info(starts, news, ctxs, dev), max(news))
+            else:
+                idx = torch.cat([torch.arange(a, a + t, device=dev) for a, t in zip(starts, news)])
+                lens = torch.cat([torch.arange(c + 1, c + t + 1, device=dev, dtype=torch.int32)
+                                  for c, t in zip(ctxs, news)])
+                tables = torch.cat([bt[None].expand(t, width) for bt, t in zip(padded, news)]).contiguous()
+                meta = ("rows", idx, tables, lens)
+        self._rows_cache = (seqs, slot_mapping, meta)
+        return meta
 
     @torch.inference_mode()
     def forward_batch(self, token_ids: torch.Tensor, positions: torch.Tensor, seqs: list[SeqInput],

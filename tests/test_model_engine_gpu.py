@@ -94,6 +94,59 @@ def test_fp32_mixed_step_matches_oracle(hiplib, cfg):
     assert err < 1e-3
 
 
+@pytest.mark.parametrize("cfg", [SMALL, SMALL128], ids=["hd64", "hd128"])
+def test_bf16_mixed_step_chunk_kernel_matches_per_token_rows(hiplib, cfg, monkeypatch):
+    """bf16 mixed step (fresh prefill + continuation chunk + decode rows): the chunked-prefill kernel path
+    against the same step with every prefill token run as a decode row (the fp32 route, which the fp32
+    gate above pins to the oracle), and both against the fp32 oracle on the same bf16 weights."""
+    from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
+    model, sd = gpu_model(cfg, torch.bfloat16, seed=3)
+    orc = OracleModel(cfg, sd, dtype=torch.float32)
+    A, B, C = prompts(3, 100, cfg.vocab_size, seed=4)
+
+    def step(force_rows):
+        pool = PagedKVCache.from_token_budget(cfg, 4096, 16, "cuda", torch.bfloat16)
+        random.Random(2).shuffle(pool.allocator._free)
+        if force_rows:
+            monkeypatch.setattr(model, "_prefill_meta",
+                                lambda seqs, paged, sm, dtype: Qwen2Model._prefill_meta(model, seqs, paged, sm,
+                                                                                        torch.float32))
+        tb, tc = BlockTable(16), BlockTable(16)
+        for t, ids in ((tb, B[:35]), (tc, C[:70])):
+            t.reserve(len(ids) + 40, pool.allocator)
+            model.forward_batch(torch.tensor(ids, device="cuda"), torch.arange(len(ids), device="cuda"),
+                                [SeqInput(len(ids))], paged=pool,
+                                slot_mapping=torch.tensor(t.slots(len(ids)), device="cuda"))
+            t.commit(len(ids))
+        ta = BlockTable(16)
+        ta.reserve(83, pool.allocator)
+        tokens = A[:83] + B[35:74] + [C[70]]
+        positions = list(range(83)) + list(range(35, 74)) + [70]
+        slots = ta.slots(83) + tb.slots(39) + tc.slots(1)
+        seqs = [SeqInput(83, block_table=torch.tensor(ta.blocks, device="cuda")),
+                SeqInput(39, block_table=torch.tensor(tb.blocks, device="cuda"), ctx_len=35),
+                SeqInput(1, ctx_len=70, use_kernel=True)]
+        meta = DecodeMeta(token_idx=torch.tensor([122], device="cuda"),
+                          block_tables=torch.tensor([tc.blocks], dtype=torch.int32, device="cuda"),
+                          context_lens=torch.tensor([71], dtype=torch.int32, device="cuda"))
+        out = model.forward_batch(torch.tensor(tokens, device="cuda"), torch.tensor(positions, device="cuda"), seqs,
+                                  logits="all", paged=pool, slot_mapping=torch.tensor(slots, device="cuda"),
+                                  decode_meta=meta).float().cpu()
+        monkeypatch.undo()
+        return out
+
+    chunks, rows = step(False), step(True)
+    ends = [82, 121, 122]
+    ref = orc.step([(orc.new_cache(256), A[:83]), (orc.new_cache(256), B[:74]), (orc.new_cache(256), C[:71])])
+    d_paths = (chunks - rows).abs().max().item()
+    d_oracle = (chunks[ends] - ref).abs().max().item()
+    d_oracle_rows = (rows[ends] - ref).abs().max().item()
+    print(f"bf16 mixed step ({cfg.head_dim}): chunks vs rows {d_paths:.3e}; vs oracle {d_oracle:.3e} "
+          f"(rows path {d_oracle_rows:.3e})")
+    assert d_paths <= 0.05
+    assert d_oracle <= max(2 * d_oracle_rows, 0.05)
+
+
 def test_fresh_prefill_without_table_reads_pages_off_the_slot_mapping(hiplib):
     """SeqInput(n) with no block table (the reference's prefill call shape) == the same with a table."""
     from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
