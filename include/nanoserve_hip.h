@@ -81,20 +81,29 @@ size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_bl
  * nanoserve/model.py:292-309 (continuation) and the causal SDPA of :310-318 (fresh prefill, ctx_len = 0),
  * over the pages PagedKVCache.gather (kv_cache.py:281-288) would gather; the reference computes it with
  * gather + repeat_interleave + SDPA. Online softmax in fp32; probabilities rounded to bf16 before P.V.
- * max_new = max over s of n_new (it sizes the grid; sequences with fewer tokens exit early).
+ * max_new = max over s of n_new and max_kv = max over s of ctx_len + n_new size the grid (sequences with
+ * fewer tokens exit early); a sequence with more new tokens than max_new is not computed.
  *
  * Limits: bf16 only; head_dim in {64, 128}; block_size == 16; strides multiples of 8 elements and
  * 16-byte aligned bases. Pages past ceil((ctx_len + n_new) / 16) are never read and a sequence's page
  * count is clamped to max_blocks; the tokens of a table entry outside [0, num_blocks) are masked out.
- * No workspace; rows of out that belong to no sequence are not written.
+ * Rows of out that belong to no sequence are not written.
+ * Long contexts split a query tile's keys over several workgroups; in the same launch the last of them
+ * merges the partial softmax states in order. That needs `workspace` of at least
+ * ns_prefill_workspace_bytes(n_seqs, n_heads, head_dim, max_new, max_kv) bytes (256-byte aligned,
+ * zero-filled once by the owner: it starts with arrival counters, which every call leaves at zero; 0 bytes
+ * means none is needed). Calls sharing a workspace must be ordered (same stream).
  */
 int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh,
                           const void* k_pool, const void* v_pool,
                           int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
                           const int32_t* block_tables, int64_t bt_sb, const int32_t* seq_info,
-                          int n_seqs, int max_new, void* out, int64_t o_st, int64_t o_sh,
+                          int n_seqs, int max_new, int max_kv, void* out, int64_t o_st, int64_t o_sh,
                           int n_heads, int n_kv_heads, int head_dim, int block_size,
-                          int max_blocks, int num_blocks, float scale, int dtype, void* stream);
+                          int max_blocks, int num_blocks, float scale, int dtype,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+size_t ns_prefill_workspace_bytes(int n_seqs, int n_heads, int head_dim, int max_new, int max_kv);
 
 /*
  * RMSNorm over rows of length n (row-major, contiguous):

@@ -39,10 +39,12 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "ns_paged_attn_prefill": (_c_int, [
         _c_vp, _c_i64, _c_i64,                  # q, q_st, q_sh
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,   # k_pool, v_pool, kv_sblk, kv_spos, kv_sh
-        _c_vp, _c_i64, _c_vp, _c_int, _c_int,   # block_tables, bt_sb, seq_info, n_seqs, max_new
+        _c_vp, _c_i64, _c_vp, _c_int, _c_int, _c_int,   # block_tables, bt_sb, seq_info, n_seqs, max_new, max_kv
         _c_vp, _c_i64, _c_i64,                  # out, o_st, o_sh
         _c_int, _c_int, _c_int, _c_int,         # n_heads, n_kv_heads, head_dim, block_size
-        _c_int, _c_int, _c_f32, _c_int, _c_vp]),   # max_blocks, num_blocks, scale, dtype, stream
+        _c_int, _c_int, _c_f32, _c_int,         # max_blocks, num_blocks, scale, dtype
+        _c_vp, _c_sz, _c_vp]),                  # workspace, workspace_bytes, stream
+    "ns_prefill_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ns_rms_norm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_f32, _c_int, _c_vp]),
     "ns_silu_mul": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "ns_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,

@@ -62,24 +62,21 @@ __device__ __forceinline__ float publish_load(const float* p) {
 __device__ __forceinline__ uint32_t publish_load(const uint32_t* p) {
   return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// 16-byte forms (a single agent-scope vector store / load: the compiler has no 128-bit atomic, so these
-// are written out; it does not count them in its own wait bookkeeping, which only makes its waits
-// stronger). A batch of publish_load16_issue calls is completed by publish_load16_wait on the same
-// registers, which waits for every load of the wave and pins the registers' uses after that wait.
+// 16-byte forms: two 8-byte agent-scope atomic accesses each, which the compiler sees, orders and waits
+// for itself. (A written-out vector store or load would hide its register use from the compiler's hazard
+// and wait bookkeeping: a store could read its data registers before a preceding accumulator move has
+// written them, and a load's destination could be copied before the data has arrived.)
 typedef __attribute__((ext_vector_type(4))) unsigned int pub_u32x4_t;
 __device__ __forceinline__ void publish_store16(void* p, pub_u32x4_t v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+  uint64_t* q = static_cast<uint64_t*>(p);
+  __hip_atomic_store(q, uint64_t(v[0]) | (uint64_t(v[1]) << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, uint64_t(v[2]) | (uint64_t(v[3]) << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ pub_u32x4_t publish_load16_issue(const void* p) {
-  pub_u32x4_t v;
-  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=&v"(v) : "v"(p) : "memory");
-  return v;
-}
-template <int N>
-__device__ __forceinline__ void publish_load16_wait(pub_u32x4_t (&v)[N]) {
-  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-#pragma unroll
-  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+__device__ __forceinline__ pub_u32x4_t publish_load16(const void* p) {
+  uint64_t* q = static_cast<uint64_t*>(const_cast<void*>(p));
+  const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return pub_u32x4_t{uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32)};
 }
 // Every vector memory operation this wave issued so far has completed (s_waitcnt vmcnt(0)); with the
 // workgroup-scope fence the compiler keeps the preceding stores before it.

@@ -304,11 +304,10 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
 #pragma unroll
       for (int e = 0; e < MB; ++e) {
         const int x = min(x0 + e, n_active - 1);
-        u[e] = publish_load16_issue(accp + int64_t(x) * (16 * HD) + h * HD + 4 * d4);
+        u[e] = publish_load16(accp + int64_t(x) * (16 * HD) + h * HD + 4 * d4);
         pm[e] = publish_load(ml + x * 32 + h * 2);
         pl[e] = publish_load(ml + x * 32 + h * 2 + 1);
       }
-      publish_load16_wait(u);
 #pragma unroll
       for (int e = 0; e < MB; ++e) {
         if (x0 + e < n_active) {

@@ -16,13 +16,16 @@ head_dim, max_blocks) is allocated zero-filled on first use (outside any graph c
 up eagerly first) and reused by every later call and graph replay. Calls on one stream never overlap, so
 sharing it is safe.
 
-    paged_attention_prefill(q, k_pool, v_pool, block_tables, seq_info, max_new, scale, out=None) -> out
+    paged_attention_prefill(q, k_pool, v_pool, block_tables, seq_info, max_new, max_kv, scale, out=None)
 
 The new tokens of several sequences at once (nanoserve/model.py:283-318, the per-sequence SDPA branch):
 q [N, n_heads, head_dim] holds the step's tokens; seq_info int32 [S, 4] (device) holds per sequence
-(q_start, n_new, ctx_len, 0); block_tables int32 [S, W]. Token j of sequence s attends to keys
-0 .. ctx_len + j of its pages, which must already hold the new tokens' K/V. Rows of `out` outside every
-sequence are left untouched. bf16 only; `prefill_seq_info` builds seq_info from host lists.
+(q_start, n_new, ctx_len, 0); block_tables int32 [S, W]; max_new / max_kv = the largest n_new and
+ctx_len + n_new (host ints: they size the grid). Token j of sequence s attends to keys 0 .. ctx_len + j of
+its pages, which must already hold the new tokens' K/V. Rows of `out` outside every sequence are left
+untouched. bf16 only; `prefill_seq_info` builds seq_info from host lists. Long tiles are split over
+several workgroups whose partial states meet in a zero-filled workspace, kept per (device, shape) like
+the decode one (the prefill path runs eagerly, so it is never first allocated inside a capture).
 """
 from __future__ import annotations
 
@@ -86,8 +89,26 @@ def prefill_seq_info(q_starts: list[int], n_new: list[int], ctx_lens: list[int],
     return torch.tensor(rows, dtype=torch.int32).reshape(-1, 4).to(device)
 
 
+_PREFILL_WS: dict[int, torch.Tensor] = {}
+
+
+def prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """A zero-filled workspace of at least nbytes on `device` (grown, never shrunk), or None for 0 bytes."""
+    if nbytes == 0:
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _PREFILL_WS.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("paged_attention_prefill: workspace must be sized by an eager call before capture")
+        # zero-filled: the kernel's arrival counters start at zero and every call leaves them there
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _PREFILL_WS[idx] = ws
+    return ws
+
+
 def paged_attention_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
-                            seq_info: torch.Tensor, max_new: int, scale: float,
+                            seq_info: torch.Tensor, max_new: int, max_kv: int, scale: float,
                             out: torch.Tensor | None = None) -> torch.Tensor:
     N, n_heads, head_dim = q.shape
     num_blocks, block_size, n_kv_heads, hd2 = k_pool.shape
@@ -104,11 +125,16 @@ def paged_attention_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     _lib.require_gpu(q, k_pool, v_pool, block_tables, seq_info, out)
     if S == 0 or max_new == 0:
         return out
-    _lib.check(_lib.lib().ns_paged_attn_prefill(
+    L = _lib.lib()
+    ws = None
+    if head_dim in (64, 128):
+        ws = prefill_workspace(q.device, L.ns_prefill_workspace_bytes(S, n_heads, head_dim, int(max_new), int(max_kv)))
+    _lib.check(L.ns_paged_attn_prefill(
         q.data_ptr(), q.stride(0), q.stride(1),
         k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
-        block_tables.data_ptr(), block_tables.stride(0), seq_info.data_ptr(), S, int(max_new),
+        block_tables.data_ptr(), block_tables.stride(0), seq_info.data_ptr(), S, int(max_new), int(max_kv),
         out.data_ptr(), out.stride(0), out.stride(1),
         n_heads, n_kv_heads, head_dim, block_size, block_tables.shape[1], num_blocks, float(scale),
-        _lib.dtype_code(q), _lib.stream_of(q)), "paged_attention_prefill")
+        _lib.dtype_code(q), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+        _lib.stream_of(q)), "paged_attention_prefill")
     return out

@@ -298,8 +298,8 @@ class Qwen2Model:
         pre = self._prefill_meta(seqs, paged, slot_mapping, q.dtype)
         if pre is not None and pre[0] == "chunks":
             from nanoserve_amd.kernels.paged_attention import paged_attention_prefill
-            _, tables, info, max_new = pre
-            paged_attention_prefill(q[0], paged.k[i], paged.v[i], tables, info, max_new, scale,
+            _, tables, info, max_new, max_kv = pre
+            paged_attention_prefill(q[0], paged.k[i], paged.v[i], tables, info, max_new, max_kv, scale,
                                     out=o_all[0].view(N, nh, hd))
         elif pre is not None:
             _, idx, tables, lens = pre
@@ -310,7 +310,8 @@ class Qwen2Model:
     def _prefill_meta(self, seqs: list[SeqInput], paged, slot_mapping, dtype: torch.dtype):
         """Attention inputs of the step's non-decode tokens (prefills and chunk continuations), cached per
         step (all layers share them):
-          bf16: ("chunks", tables int32 [S, W], seq_info int32 [S, 4], max_new) for the chunked-prefill kernel;
+          bf16: ("chunks", tables int32 [S, W], seq_info int32 [S, 4], max_new, max_kv) for the chunked-prefill
+                kernel;
           fp32: ("rows", token index, tables [n, W], context lengths [n]) -- one decode row per token, token j
                 of a sequence with ctx_len cached tokens seeing ctx_len + j + 1 tokens."""
         cache = getattr(self, "_rows_cache", None)
@@ -345,7 +346,8 @@ class Qwen2Model:
             width = max(bt.shape[0] for bt in tabs)
             padded = [F.pad(bt, (0, width - bt.shape[0])) for bt in tabs]
             if dtype == torch.bfloat16:
-                meta = ("chunks", torch.stack(padded).contiguous(), prefill_seq_info(starts, news, ctxs, dev), max(news))
+                meta = ("chunks", torch.stack(padded).contiguous(), prefill_seq_info(starts, news, ctxs, dev), max(news),
+                        max(c + t for c, t in zip(ctxs, news)))
             else:
                 idx = torch.cat([torch.arange(a, a + t, device=dev) for a, t in zip(starts, news)])
                 lens = torch.cat([torch.arange(c + 1, c + t + 1, device=dev, dtype=torch.int32)

@@ -52,7 +52,8 @@ def run(q, kpool, vpool, tables, seqs, scale, out=None):
     from nanoserve_amd.kernels.paged_attention import paged_attention_prefill, prefill_seq_info
     info = prefill_seq_info([s[0] for s in seqs], [s[1] for s in seqs], [s[2] for s in seqs], "cuda")
     o = paged_attention_prefill(q.cuda(), kpool.cuda(), vpool.cuda(), tables.cuda(), info,
-                                max(s[1] for s in seqs), scale, out=None if out is None else out.cuda())
+                                max(s[1] for s in seqs), max(s[1] + s[2] for s in seqs), scale,
+                                out=None if out is None else out.cuda())
     return o.cpu()
 
 
@@ -144,8 +145,18 @@ def test_rejects_unsupported_arguments(hiplib):
     q, kp, vp, tables, seqs, _, _ = make_seqs([(0, 20)], 12, 2, 128)
     info = prefill_seq_info([0], [20], [0], "cuda")
     with pytest.raises(RuntimeError, match="bf16 only"):
-        paged_attention_prefill(q.float().cuda(), kp.float().cuda(), vp.float().cuda(), tables.cuda(), info, 20, 0.1)
+        paged_attention_prefill(q.float().cuda(), kp.float().cuda(), vp.float().cuda(), tables.cuda(), info, 20, 20, 0.1)
     q96 = torch.zeros(20, 12, 96, dtype=torch.bfloat16, device="cuda")
     kp96 = torch.zeros(kp.shape[0], BS, 2, 96, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError, match="head_dim"):
-        paged_attention_prefill(q96, kp96, kp96, tables.cuda(), info, 20, 0.1)
+        paged_attention_prefill(q96, kp96, kp96, tables.cuda(), info, 20, 20, 0.1)
+
+
+def test_long_partition_refreshes_its_block_window(hiplib):
+    """max_kv understated (here: n_new) gives one partition per tile; its 25 stages outrun the kernel's
+    16-stage window of block ids, which is then refreshed mid-loop. Results must not change."""
+    from nanoserve_amd.kernels.paged_attention import paged_attention_prefill, prefill_seq_info
+    q, kp, vp, tables, seqs, ks, vs = make_seqs([(1500, 100)], 12, 2, 128, seed=31)
+    info = prefill_seq_info([0], [100], [1500], "cuda")
+    out = paged_attention_prefill(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), info, 100, 100, 128 ** -0.5).cpu()
+    check(out, q, seqs, ks, vs, 128 ** -0.5)
