@@ -15,9 +15,12 @@ ctx U[512, 4096], 16-token pages scattered over a 64k-block pool, 8 disjoint dra
 256 MB Infinity Cache cannot serve them). Algorithmic bytes per call = sum_b ctx_b*n_kv*hd*2(K,V)*2B +
 Q and O (2*B*n_heads*hd*2B) + block-table entries read (4B per page) + context lengths (4B per row);
 duration = (time between two HIP events bracketing 400 back-to-back calls on the launch stream) / 400,
-each call being the split-K pass + the merge pass.
+each call one launch (partitions and their merge).
 step_roofline: the decode step's algorithmic HBM bytes (every weight once, the KV cache of every row, the
 new K/V and the logits) over the measured step time.
+mixed_step: BASELINE config 4 (one 1536-token chunk on 512 cached tokens + 16 decode rows, eager) --
+step time and algorithmic TFLOP/s against the bf16 MFMA peak, and the chunked-prefill attention kernel
+alone at that shape (FLOPs = sum_j (512 + j + 1) * n_heads * hd * 4 per layer).
 
 cpu_baseline: the CPU oracle (oracle/model.py, the reference algorithm restated in PyTorch) on this
 host's cores: one fp32 decode step of the same 1.5B shape at batch 32 with 1024-token contexts
@@ -36,6 +39,7 @@ import time
 import torch
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0   # dense bf16 MFMA
 
 
 def log(msg: str) -> None:
@@ -104,10 +108,97 @@ def paged_attention_roofline() -> dict:
     avg_bytes = sum(d[3] for d in draws) / R
     achieved = avg_bytes / (ms * 1e-3) / 1e9
     del k, v
-    return {"bound": "hbm", "kernel": "paged_attention_decode (split-K + merge), BASELINE config 2",
+    return {"bound": "hbm", "kernel": "paged_attention_decode (split-K partitions merged in the same launch), BASELINE config 2",
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
             "bytes_per_launch": int(avg_bytes), "us_per_launch": round(ms * 1e3, 2)}
+
+
+def mixed_step_bench(model, cfg, reps: int = 5) -> dict:
+    """one engine-sized mixed step on the 1.5B model -- sequence A continues a 1536-token
+    chunk on 512 cached tokens while 16 sequences (contexts U[256, 2048], seed 2) decode one token each
+    (1552 rows: vendor GEMMs for the projections, the chunked-prefill kernel for A, the paged decode kernel
+    for the 16 rows, LM head on the 17 last rows). The step is repeated `reps` times on the same inputs (it
+    rewrites the same K/V slots with the same values); median time. Also the chunked-prefill attention
+    alone at this step's shape, against the bf16 MFMA peak."""
+    from nanoserve_amd.kernels.paged_attention import paged_attention_prefill, prefill_seq_info
+    from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
+    from nanoserve_amd.model import DecodeMeta, SeqInput
+    dev = "cuda"
+    g = torch.Generator().manual_seed(2)
+    ctxs = torch.randint(256, 2049, (16,), generator=g).tolist()
+    toks_a = torch.randint(0, cfg.vocab_size, (2048,), generator=g).tolist()
+    pool = PagedKVCache.from_token_budget(cfg, 2048 + sum(ctxs) + 16 * 17 + 64, 16, dev, torch.bfloat16)
+    ta = BlockTable(16)
+    ta.reserve(2048, pool.allocator)
+    model.forward_batch(torch.tensor(toks_a[:512], device=dev), torch.arange(512, device=dev), [SeqInput(512)],
+                        paged=pool, slot_mapping=torch.tensor(ta.slots(512), device=dev))
+    ta.commit(512)
+    dec_tables, last = [], []
+    for c in ctxs:                                     # the decode rows' contexts (prefilled, not timed)
+        t = BlockTable(16)
+        t.reserve(c + 1, pool.allocator)
+        ids = torch.randint(0, cfg.vocab_size, (c,), generator=g).tolist()
+        model.forward_batch(torch.tensor(ids, device=dev), torch.arange(c, device=dev), [SeqInput(c)],
+                            paged=pool, slot_mapping=torch.tensor(t.slots(c), device=dev))
+        t.commit(c)
+        dec_tables.append(t)
+        last.append(ids[-1])
+    T = 1536
+    tokens = toks_a[512:] + last
+    positions = list(range(512, 2048)) + ctxs
+    slots = ta.slots(T) + [s for t in dec_tables for s in t.slots(1)]
+    W = max(len(t.blocks) for t in dec_tables)
+    seqs = [SeqInput(T, block_table=torch.tensor(ta.blocks, device=dev), ctx_len=512)] + \
+           [SeqInput(1, ctx_len=c, use_kernel=True) for c in ctxs]
+    meta = DecodeMeta(token_idx=torch.arange(T, T + 16, device=dev),
+                      block_tables=torch.tensor([t.blocks + [0] * (W - len(t.blocks)) for t in dec_tables],
+                                                dtype=torch.int32, device=dev),
+                      context_lens=torch.tensor([c + 1 for c in ctxs], dtype=torch.int32, device=dev))
+    tok_t, pos_t, slot_t = (torch.tensor(x, device=dev) for x in (tokens, positions, slots))
+
+    def step():
+        return model.forward_batch(tok_t, pos_t, seqs, logits="last", paged=pool, slot_mapping=slot_t,
+                                   decode_meta=meta)
+    step()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3
+    H, I, L, V = cfg.hidden_size, cfg.intermediate_size, cfg.n_layers, cfg.vocab_size
+    qkv_n = (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim
+    rows = T + 16
+    gemm_flops = 2 * rows * L * H * (qkv_n + cfg.n_heads * cfg.head_dim + 2 * I) + 2 * rows * L * I * H
+    attn_pf = sum(512 + j + 1 for j in range(T)) * cfg.n_heads * cfg.head_dim * 4 * L
+    attn_dec = sum(c + 1 for c in ctxs) * cfg.n_heads * cfg.head_dim * 4 * L
+    lm = 2 * 17 * H * V
+    flops = gemm_flops + attn_pf + attn_dec + lm
+
+    # the chunked-prefill kernel alone at this step's shape (one layer's call)
+    q = torch.randn(T, cfg.n_heads, cfg.head_dim, device=dev, dtype=torch.bfloat16)
+    info = prefill_seq_info([0], [T], [512], dev)
+    tab = torch.tensor([ta.blocks], dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+
+    def pf():
+        paged_attention_prefill(q, pool.k[0], pool.v[0], tab, info, T, 512 + T, cfg.head_dim ** -0.5, out=out)
+    pf()
+    pf_ms = gated_region_time(pf, 50) / 50
+    pf_flops = attn_pf / L
+    del pool
+    return {"workload": "BASELINE config 4: 1.5B bf16 mixed step, a 1536-token chunk on 512 cached tokens + 16 "
+                        "decode rows (ctx U[256, 2048]), eager (1552 rows)",
+            "ms_per_step": round(ms, 3), "tflop_per_step": round(flops / 1e12, 3),
+            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1), "peak_tflops": PEAK_BF16_TFLOPS,
+            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "prefill_attention": {"bound": "mfma", "achieved": round(pf_flops / (pf_ms * 1e-3) / 1e12, 1),
+                                  "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": round(pf_flops / (pf_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                  "flop_per_launch": int(pf_flops), "us_per_launch": round(pf_ms * 1e3, 2)}}
 
 
 def copy_calibration(nbytes: int = 512 << 20, reps: int = 4) -> float:
@@ -121,7 +212,7 @@ def copy_calibration(nbytes: int = 512 << 20, reps: int = 4) -> float:
 
 
 def pmc_traffic() -> int | None:
-    """HBM bytes per paged-attention call (split-K pass + merge pass) measured by rocprofv3 --pmc FETCH_SIZE
+    """HBM bytes per paged-attention call (one launch) measured by rocprofv3 --pmc FETCH_SIZE
     and WRITE_SIZE runs of `bench.py --attention-only`, scaled by the copy calibration, as committed in
     profiles/paged_attention_decode_config2_pmc.md (None when that summary is absent)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -170,6 +261,7 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--prompt-len", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-mixed-step", action="store_true", help="skip the config-4 mixed-step measurement")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the paged-attention roofline and the copy calibration (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
@@ -236,6 +328,13 @@ def main() -> int:
 
     del eng
     torch.cuda.empty_cache()
+    mixed = None
+    if not args.no_mixed_step:
+        log("mixed step (config 4 shape)")
+        mixed = mixed_step_bench(model, cfg)
+        torch.cuda.empty_cache()
+        log(f"mixed step: {mixed['ms_per_step']} ms ({mixed['achieved_tflops']} TFLOP/s); chunked-prefill attention "
+            f"{mixed['prefill_attention']['us_per_launch']} us/layer ({mixed['prefill_attention']['achieved']} TFLOP/s)")
     log("paged-attention roofline (config 2 shape)")
     roof = paged_attention_roofline()
     log(f"paged attention: {roof['us_per_launch']} us/call, {roof['achieved']} GB/s")
@@ -260,6 +359,7 @@ def main() -> int:
         "step_roofline": {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / PEAK_HBM_GBS, 4), "bytes_per_step": int(step_bytes),
                           "roofline_tok_s": round(B / (step_bytes / (PEAK_HBM_GBS * 1e9)), 1)},
+        "mixed_step": mixed,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
