@@ -21,6 +21,9 @@ new K/V and the logits) over the measured step time.
 mixed_step: BASELINE config 4 (one 1536-token chunk on 512 cached tokens + 16 decode rows, eager) --
 step time and algorithmic TFLOP/s against the bf16 MFMA peak, and the chunked-prefill attention kernel
 alone at that shape (FLOPs = sum_j (512 + j + 1) * n_heads * hd * 4 per layer).
+prefix_sharing: BASELINE config 5 (3B shape, a 1024-token prefix shared by 32 requests through the prefix
+cache, 211-token suffixes): decode tokens/s and the step's HBM roofline, logical (a shared block counted
+once per row that reads it) and unique bytes.
 
 cpu_baseline: the CPU oracle (oracle/model.py, the reference algorithm restated in PyTorch) on this
 host's cores: one fp32 decode step of the same 1.5B shape at batch 32 with 1024-token contexts
@@ -112,6 +115,91 @@ def paged_attention_roofline() -> dict:
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
             "bytes_per_launch": int(avg_bytes), "us_per_launch": round(ms * 1e3, 2)}
+
+
+def decode_run(model, prompts: list[list[int]], K: int, W: int, prefix_caching: bool = False,
+               first_alone: bool = False) -> dict:
+    """Prefill `prompts` through the engine (not timed), W warm-up and K timed greedy decode steps at the full
+    batch (every timed step must be a graph replay of the full bucket). first_alone: the first prompt is
+    prefilled (and its blocks registered with the prefix cache) before the others are admitted. Returns
+    tokens/s, ms/step and the step's algorithmic HBM bytes (every weight once, the KV of every row --
+    logical, a shared block counted per row -- and the logits), plus the unique KV bytes."""
+    from nanoserve_amd.engine import LLMEngine
+    cfg, B = model.cfg, len(prompts)
+    # Sequences are admitted a few per prefill step, so the first ones start decoding early: max_new_tokens
+    # leaves room for that, and no sequence finishes inside the timed window.
+    max_new = W + K + B + 8
+    max_seq = max(len(p) for p in prompts) + max_new
+    eng = LLMEngine(model, eos_token_ids=[], max_seq_len=max_seq, max_num_seqs=B, max_num_batched_tokens=2048,
+                    batch_wait_s=0.0, kv_cache_tokens=B * (max_seq + 16), piecewise_graphs=False,
+                    prefix_caching=prefix_caching)
+    log(f"prefilling {B} prompts of {len(prompts[0])}..{max(len(p) for p in prompts)} tokens (not timed)")
+    t0 = time.perf_counter()
+    rest = prompts
+    if first_alone:
+        eng.add_request(prompts[0], max_new, ignore_eos=True)
+        while any(s.is_prefill for s in eng.scheduler.running) or eng.scheduler.waiting:
+            eng.step()
+        rest = prompts[1:]
+    for p in rest:
+        eng.add_request(p, max_new, ignore_eos=True)
+    while any(s.is_prefill for s in eng.scheduler.running) or eng.scheduler.waiting:
+        eng.step()
+    torch.cuda.synchronize()
+    hits = eng.stats.get("prefix_hit_tokens", 0) if prefix_caching else 0
+    log(f"prefill done in {time.perf_counter() - t0:.1f} s (prefix hits {hits} tokens); {W} warm-up decode steps "
+        f"(captures bucket {B})")
+    for _ in range(W):
+        eng.step()
+    assert eng.last_step.n_decode == B and eng.last_step.n_prefill == 0
+    g0 = eng.stats["graph_steps"]
+    ctx_sum = sum(s.num_tokens for s in eng.scheduler.running)   # context of the first timed step (incl. new)
+    produced = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        produced += len(eng.step())
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert eng.stats["graph_steps"] - g0 == K, "every timed step must be a graph replay"
+    assert produced == B * K and len(eng.scheduler.running) == B, "every timed step must decode the full batch"
+    wbytes = sum(t.numel() * t.element_size() for name, t in model.named_weights().items()
+                 if name != "model.embed_tokens.weight")
+    wbytes += model.lm_head.numel() * model.lm_head.element_size()           # LM head reads the whole table
+    kv_tok = cfg.kv_bytes_per_token(model.dtype)
+    mean_ctx_total = ctx_sum + B * (K - 1) / 2                                 # sum_b ctx_b averaged over steps
+    shared = hits // (B - 1) if prefix_caching and B > 1 else 0              # tokens every row shares
+    step_bytes = wbytes + mean_ctx_total * kv_tok + B * cfg.vocab_size * 2
+    unique_bytes = step_bytes - (B - 1) * shared * kv_tok
+    del eng
+    torch.cuda.empty_cache()
+    return {"tok_s": produced / elapsed, "ms_step": elapsed / K * 1e3, "step_bytes": step_bytes,
+            "unique_bytes": unique_bytes, "prefix_hit_tokens": hits}
+
+
+def prefix_sharing_bench(K: int, W: int) -> dict:
+    """Qwen2.5-3B shape, bf16, random-init weights (drawn on the GPU: the CPU oracle does
+    not run this config), one 1024-token random prefix shared by 32 requests, each with its own 211-token
+    random suffix; prefix caching on, so the other 31 requests reuse the prefix's 64 blocks (read by every
+    row's decode attention through its block table). K greedy decode steps at batch 32."""
+    from nanoserve_amd.model import QWEN25_3B, Qwen2Model, random_state_dict
+    cfg, B = QWEN25_3B, 32
+    log("generating random-init 3B weights (seeded)")
+    model = Qwen2Model(cfg, random_state_dict(cfg, seed=0, dtype=torch.bfloat16, device="cuda"))
+    g = torch.Generator().manual_seed(5)
+    prefix = torch.randint(0, cfg.vocab_size, (1024,), generator=g).tolist()
+    prompts = [prefix + torch.randint(0, cfg.vocab_size, (211,), generator=g).tolist() for _ in range(B)]
+    run = decode_run(model, prompts, K, W, prefix_caching=True, first_alone=True)
+    del model
+    ms, nbytes, ubytes = run["ms_step"], run["step_bytes"], run["unique_bytes"]
+    return {"workload": "BASELINE config 5: Qwen2.5-3B-shape bf16 greedy decode, batch 32, a shared 1024-token "
+                        "prefix (64 blocks) + 32 distinct 211-token suffixes, prefix caching, hipGraph bucket 32",
+            "value": round(run["tok_s"], 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+            "prefix_hit_tokens": run["prefix_hit_tokens"],
+            "step_roofline": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                              "unit": "GB/s", "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                              "bytes_per_step": int(nbytes), "unique_bytes_per_step": int(ubytes),
+                              "unique_frac": round(ubytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}}
 
 
 def mixed_step_bench(model, cfg, reps: int = 5) -> dict:
@@ -262,6 +350,7 @@ def main() -> int:
     ap.add_argument("--prompt-len", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mixed-step", action="store_true", help="skip the config-4 mixed-step measurement")
+    ap.add_argument("--no-prefix-sharing", action="store_true", help="skip the config-5 prefix-sharing decode run")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the paged-attention roofline and the copy calibration (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
@@ -276,58 +365,20 @@ def main() -> int:
         log(f"copy calibration: {copy_calibration():.0f} GB/s")
         print(json.dumps({"roofline": roof}), flush=True)
         return 0
-    from nanoserve_amd.engine import LLMEngine
-    from nanoserve_amd.model import QWEN25_1_5B, Qwen2Model, random_state_dict
+    from nanoserve_amd.model import QWEN25_1_5B, QWEN25_3B, Qwen2Model, random_state_dict
 
     cfg, B, P, K, W = QWEN25_1_5B, args.batch, args.prompt_len, args.steps, args.warmup
     torch.manual_seed(0)
     log("generating random-init 1.5B weights (CPU, fp32, seeded)")
     sd_cpu = random_state_dict(cfg, seed=0, dtype=torch.float32)
     model = Qwen2Model(cfg, {n: t.to("cuda", torch.bfloat16) for n, t in sd_cpu.items()})
-    # Sequences are admitted two per prefill step, so the first ones start decoding up to B/2 steps early:
-    # max_new_tokens leaves room for that, and no sequence finishes inside the timed window.
-    max_new = W + K + B + 8
-    max_seq = P + max_new
-    eng = LLMEngine(model, eos_token_ids=[], max_seq_len=max_seq, max_num_seqs=B, max_num_batched_tokens=2048,
-                    batch_wait_s=0.0, kv_cache_tokens=B * (max_seq + 16), piecewise_graphs=False)
     g = torch.Generator().manual_seed(1)
-    for _ in range(B):
-        eng.add_request(torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist(), max_new, ignore_eos=True)
-    log(f"prefilling {B} x {P} tokens (not timed)")
-    t0 = time.perf_counter()
-    while any(s.is_prefill for s in eng.scheduler.running) or eng.scheduler.waiting:
-        eng.step()
-    torch.cuda.synchronize()
-    log(f"prefill done in {time.perf_counter() - t0:.1f} s; {W} warm-up decode steps (captures bucket {B})")
-    for _ in range(W):
-        eng.step()
-    assert eng.last_step.n_decode == B and eng.last_step.n_prefill == 0
-    g0 = eng.stats["graph_steps"]
-    ctx_sum = sum(s.num_tokens for s in eng.scheduler.running)   # context of the first timed step (incl. new)
-    produced = 0
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(K):
-        produced += len(eng.step())
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    assert eng.stats["graph_steps"] - g0 == K, "every timed step must be a graph replay"
-    assert produced == B * K and len(eng.scheduler.running) == B, "every timed step must decode the full batch"
-    ms_step = elapsed / K * 1e3
-    tok_s = produced / elapsed
-
-    # algorithmic HBM bytes of one decode step
-    wbytes = sum(t.numel() * t.element_size() for name, t in model.named_weights().items()
-                 if name != "model.embed_tokens.weight")
-    wbytes += model.lm_head.numel() * model.lm_head.element_size()           # LM head reads the whole table
-    kv_tok = cfg.kv_bytes_per_token(torch.bfloat16)
-    mean_ctx_total = ctx_sum + B * (K - 1) / 2                                 # sum_b ctx_b averaged over steps
-    step_bytes = wbytes + mean_ctx_total * kv_tok + B * cfg.vocab_size * 2
+    prompts = [torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist() for _ in range(B)]
+    run = decode_run(model, prompts, K, W)
+    tok_s, ms_step, step_bytes = run["tok_s"], run["ms_step"], run["step_bytes"]
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"decode: {tok_s:.0f} tok/s, {ms_step:.3f} ms/step, {step_gbs:.0f} GB/s algorithmic")
 
-    del eng
-    torch.cuda.empty_cache()
     mixed = None
     if not args.no_mixed_step:
         log("mixed step (config 4 shape)")
@@ -339,10 +390,18 @@ def main() -> int:
     roof = paged_attention_roofline()
     log(f"paged attention: {roof['us_per_launch']} us/call, {roof['achieved']} GB/s")
 
+    prefix = None
+    if not args.no_prefix_sharing:
+        del model
+        torch.cuda.empty_cache()
+        log("prefix sharing (config 5: 3B shape)")
+        prefix = prefix_sharing_bench(K, W)
+        torch.cuda.empty_cache()
+        log(f"prefix sharing: {prefix['value']} tok/s, {prefix['ms_per_step']} ms/step")
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle, fp32)")
-        del model
+        model = None
         torch.cuda.empty_cache()
         cpu = cpu_baseline(sd_cpu, cfg, B, P)
         log(f"cpu: {cpu['value']} tok/s on {cpu['cores']} threads")
@@ -360,6 +419,7 @@ def main() -> int:
                           "frac": round(step_gbs / PEAK_HBM_GBS, 4), "bytes_per_step": int(step_bytes),
                           "roofline_tok_s": round(B / (step_bytes / (PEAK_HBM_GBS * 1e9)), 1)},
         "mixed_step": mixed,
+        "prefix_sharing": prefix,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
