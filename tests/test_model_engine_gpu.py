@@ -316,6 +316,29 @@ def test_fp32_prefix_caching_matches_the_oracle(hiplib):
     assert cached.kv.num_free_blocks == cached.kv.pool.num_blocks - 1
 
 
+def test_bf16_prefix_sharing_follows_the_tie_rule(hiplib):
+    """BASELINE config 5 in small: bf16, one shared system prompt (several full blocks) + distinct suffixes,
+    prefix caching on, requests admitted after the first has registered its blocks, so the others' decode
+    rows read the first request's pages through their block tables; greedy streams against the fp32 oracle
+    on the same bf16 weights under the approved tie rule, and no block leaks."""
+    cfg = SMALL128
+    sd = random_state_dict(cfg, seed=12, dtype=torch.bfloat16)
+    orc = OracleModel(cfg, sd, dtype=torch.float32)
+    g = torch.Generator().manual_seed(13)
+    system = torch.randint(0, cfg.vocab_size, (96,), generator=g).tolist()
+    ps = [system + torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in (13, 20, 7, 31)]
+    ref, ref_logits = orc.generate_greedy(ps, 20, return_logits=True)
+    model = Qwen2Model(cfg, {k: v.to("cuda") for k, v in sd.items()})
+    eng = make_engine(model, max_num_batched_tokens=256, prefix_caching=True)
+    ours = run_all(eng, [(p, 20) for p in ps], waves=((0, 1), (3, 4)))
+    st = eng.stats
+    print(f"bf16 prefix sharing: hits {st['prefix_hit_tokens']} of {st['prefix_query_tokens']}; "
+          f"{sum(a == b for a, b in zip(ours, ref))}/4 identical to the fp32 oracle")
+    assert st["prefix_hit_tokens"] >= 3 * 96
+    check_tokens_with_tie_rule(ours, ref, ref_logits, TIE_GAP_BF16, "bf16 prefix sharing")
+    assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - 1
+
+
 def test_engine_rejects_the_oracle_only_backends(hiplib):
     from nanoserve_amd.engine import LLMEngine
     model, _ = gpu_model(SMALL, torch.float32)
