@@ -375,12 +375,7 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   const bf16_t* xrow[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) xrow[i] = a.x + int64_t(min(16 * i + c16, a.M - 1)) * K + 8 * r4;
-  float xinv[TM];   // normalised input: inv of this lane's X rows
-  if constexpr (NX) {
-    const int ptiles = (K + 63) / 64;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) xinv[i] = rms_norm_row_inv(a.xsq, ptiles, min(16 * i + c16, a.M - 1), r4, K, a.xeps);
-  }
+  float xinv[TM];   // normalised input: inv of this lane's X rows (computed once the first loads are out)
 
   g_float4_t acc[TM][G_TN];
 #pragma unroll
@@ -455,6 +450,11 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   if constexpr (D > 2) {
     load_w(Q2{}, min(c0 + 2, clast));
     load_x(Q2{}, min(c0 + 2, clast));
+  }
+  if constexpr (NX) {   // the row statistics' round trip overlaps the first chunks' loads
+    const int ptiles = (K + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xinv[i] = rms_norm_row_inv(a.xsq, ptiles, min(16 * i + c16, a.M - 1), r4, K, a.xeps);
   }
   int c = c0;
   for (; c + D <= c1; c += D) {   // whole rounds only: no path into the loop header skips a step
@@ -558,8 +558,7 @@ static Plan make_plan(int tiles, int K) {
   } else {
     p.whole = tiles >= T ? T : 0;
     const int rest = tiles - p.whole;
-    int ks = rest > 0 ? (T + rest - 1) / rest : 1;
-    if (tiles >= T) ks = rest > 0 ? T / rest : 1;
+    const int ks = rest > 0 ? T / rest : 1;   // the sliced round fits the target (never a partial extra wave)
     p.ks = ks < 1 ? 1 : (ks > p.chunks ? p.chunks : ks);
   }
   if (p.ks == 1) p.whole = tiles;

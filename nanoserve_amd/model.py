@@ -397,7 +397,9 @@ class Qwen2Model:
             idx = ends
         if idx is not None:
             x = x.rows(idx) if isinstance(x, NormedRows) else x[idx]
-        return linear(x if isinstance(x, NormedRows) else x.contiguous(), self.lm_head)
+        # The LM head streams 2,374 whole tiles, one per workgroup: normalising on load would repeat the
+        # row-statistics prologue in every one of them, so the final norm is materialised once instead.
+        return linear(x.tensor() if isinstance(x, NormedRows) else x.contiguous(), self.lm_head)
 
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, cache=None, logits: str = "last"):
         raise NotImplementedError("the single-sequence contiguous-cache API (M1) is not part of the HIP path; "
