@@ -154,8 +154,8 @@ size_t ns_gemm_workspace_bytes(int M, int N, int K);
  * Normalised inputs. The projections that follow an RMSNorm in the model (QKV after ln1, gate/up after
  * ln2, the LM head after the final norm) take the un-normalised r = residual + ... and normalise each
  * activation fragment as they load it: h = round(w * round(r * inv)), inv = rsqrt(sum / K + eps), where
- * sum adds the per-64-column row sums of r^2 that ns_gemm_residual_norm_stats wrote (x_sumsq, fp32
- * [ceil(K/64)][64], row m at column m) in one fixed order. So the RMSNorm never runs as a separate pass,
+ * sum adds the per-16-column row sums of r^2 that ns_gemm_residual_norm_stats wrote (x_sumsq, fp32
+ * [ceil(K/16)][64], row m at column m) in one fixed order. So the RMSNorm never runs as a separate pass,
  * and every consumer sees bitwise the same h; ns_rms_norm_apply materialises h where a tensor is needed.
  * x_sumsq == NULL: x is used as is (x_norm_w, x_eps ignored).
  */
@@ -177,8 +177,8 @@ int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int
 
 /*
  * Projection + residual add + the statistics of the RMSNorm that follows: o = round(x W^T);
- * res_out = round(residual + o); row_sumsq[t][m] = sum over columns 64t .. 64t+63 of res_out[m]^2 (fp32,
- * [ceil(N/64)][64], may be NULL). N a multiple of 8.
+ * res_out = round(residual + o); row_sumsq[p][m] = sum over columns 16p .. 16p+15 of res_out[m]^2 (fp32,
+ * [ceil(N/16)][64], may be NULL). N a multiple of 8.
  * With a normalised consumer (or ns_rms_norm_apply) this replaces rms_norm(F.linear(o, o_w), ln2, eps,
  * residual=x) (nanoserve/model.py:256, fused.py:45) and x + F.linear(a, down_w) followed by the next
  * layer's rms_norm (model.py:257, :227-231).

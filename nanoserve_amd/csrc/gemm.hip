@@ -27,8 +27,8 @@
 //   STORE    y = round(acc + bias)                                        (F.linear; LM head)
 //   SILU     tile = 32 gate rows + the matching 32 up rows;
 //            out = round(round(silu(round(g))) * round(u))                 (silu_mul(F.linear(x, Wgu)))
-//   RESNORM  o = round(acc); r = round(residual + o) -> res_out, and each 64-column tile's row sums of
-//            r^2 -> row_sumsq[tile][row] (fp32): the statistics of the RMSNorm that follows
+//   RESNORM  o = round(acc); r = round(residual + o) -> res_out, and the row sums of r^2 over each 16
+//            columns -> row_sumsq[column group][row] (fp32): the statistics of the RMSNorm that follows
 // Normalised activations ("norm on load"): a projection whose input is rms_norm(r) takes r itself plus
 // the producer's row_sumsq and the norm weight, and normalises each X fragment as it loads it:
 //   h = round(w * round(r * inv)), inv = rsqrt(sum(row_sumsq) / K + eps)
@@ -59,6 +59,7 @@ constexpr int G_NTB = 8 * G_PAIR;  // LDS bytes of one n-tile (16 rows) of a chu
 constexpr int G_STAGE = G_TN * G_NTB;
 constexpr int G_RED = 65;          // floats per tile row in the cross-wave reduction (64 + 1 pad)
 constexpr int G_MAX_M = 64;
+constexpr int G_NORM_COLS = 16;   // columns per row-sum partial of the RMSNorm statistics
 // The arrival counters sit at the start of every workspace, in a region no other data ever uses, so the
 // "all counters are zero between calls" invariant holds whatever shapes share the buffer.
 constexpr int G_MAX_TILES = 8191;
@@ -76,8 +77,8 @@ struct GemmArgs {
   bf16_t* y;
   const bf16_t* residual;
   bf16_t* res_out;
-  float* sumsq_out;         // RESNORM: [tiles][64] row sums of r^2
-  // normalised input: x holds r; xsq [ceil(K/64)][64] its row sums of r^2, xnw the norm weight [K]
+  float* sumsq_out;         // RESNORM: [ceil(N/16)][64] row sums of r^2 over 16 columns
+  // normalised input: x holds r; xsq [ceil(K/16)][64] its row sums of r^2, xnw the norm weight [K]
   const float* xsq;
   const bf16_t* xnw;
   float xeps;
@@ -111,8 +112,14 @@ __device__ __forceinline__ int tile_row(const GemmArgs& a, int t, int j, int r) 
   }
 }
 
+// Two fp32 -> packed bf16, round to nearest even, by the hardware conversion (v_cvt_pk_bf16_f32): the same
+// bits as f32_to_bf16 for every non-NaN value, in one instruction instead of a dozen integer ones.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  typedef __attribute__((ext_vector_type(2))) __bf16 g_bf16x2_t;
+  g_bf16x2_t r;
+  r[0] = static_cast<__bf16>(lo);
+  r[1] = static_cast<__bf16>(hi);
+  return __builtin_bit_cast(uint32_t, r);
 }
 __device__ __forceinline__ void store_bf16x8(bf16_t* p, const float (&v)[8]) {
   g_u32x4_t u;
@@ -291,7 +298,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSourc
     }
   } else {  // EPI_RESNORM
     const int N = a.N;
-    // res_out and this tile's row sums of r^2 (8 threads per row: lanes 8k .. 8k+7)
+    // res_out and the row sums of r^2 over each 16 columns (8 threads per row: lanes 8k .. 8k+7)
 #pragma unroll
     for (int it = 0; it < g_items8<TM>(); ++it) {
       const int idx = tid + it * G_WAVES * 64;
@@ -309,10 +316,9 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSourc
         }
         store_bf16x8(a.res_out + int64_t(m) * N + n0, r);
       }
-      ss += __shfl_xor(ss, 1, 64);
-      ss += __shfl_xor(ss, 2, 64);
-      ss += __shfl_xor(ss, 4, 64);
-      if (live && cq == 0 && a.sumsq_out != nullptr) a.sumsq_out[int64_t(t) * G_MAX_M + m] = ss;
+      ss += __shfl_xor(ss, 1, 64);   // columns 16p .. 16p+15 (two 8-column groups)
+      if (live && (cq & 1) == 0 && n0 < N && a.sumsq_out != nullptr)
+        a.sumsq_out[int64_t(4 * t + (cq >> 1)) * G_MAX_M + m] = ss;
     }
   }
 }
@@ -334,6 +340,29 @@ __device__ __forceinline__ float rms_norm_row_inv(const float* sumsq, int ptiles
   return rsqrtf(part / float(K) + eps);
 }
 
+// inv of rows 0 .. M-1 into s_inv (LDS), for a whole workgroup at once: thread (row, g) = (tid / 4, tid % 4)
+// adds the partials p = g, g + 4, g + 8, ... in increasing p, then the four combine as (g0 + g1) + (g2 + g3)
+// -- the same operations in the same order as rms_norm_row_inv, so the bits agree. All loads of a thread
+// are issued together (one round trip for K <= 2048). Every thread calls it; the caller synchronises before
+// reading s_inv.
+__device__ __forceinline__ void block_row_inv(const float* sumsq, int ptiles, int M, int K, float eps, float* s_inv) {
+  const int tid = threadIdx.x, m = tid >> 2, g = tid & 3;
+  const bool live = m < M;
+  constexpr int B = 32;
+  float part = 0.f;
+  for (int p0 = g; p0 < ptiles; p0 += 4 * B) {
+    float v[B];
+#pragma unroll
+    for (int e = 0; e < B; ++e) v[e] = live && p0 + 4 * e < ptiles ? sumsq[int64_t(p0 + 4 * e) * G_MAX_M + m] : 0.f;
+#pragma unroll
+    for (int e = 0; e < B; ++e)
+      if (p0 + 4 * e < ptiles) part += v[e];
+  }
+  part += __shfl_xor(part, 1, 64);
+  part += __shfl_xor(part, 2, 64);
+  if (live && g == 0) s_inv[m] = rsqrtf(part / float(K) + eps);
+}
+
 // 8 bf16 of r (one X fragment) -> 8 bf16 of h = round(w * round(r * inv))
 __device__ __forceinline__ g_u32x4_t norm_fragment(g_u32x4_t r, g_u32x4_t w, float inv) {
   g_u32x4_t o;
@@ -341,7 +370,8 @@ __device__ __forceinline__ g_u32x4_t norm_fragment(g_u32x4_t r, g_u32x4_t w, flo
   for (int e = 0; e < 4; ++e) {
     const float r0 = __uint_as_float(r[e] << 16), r1 = __uint_as_float(r[e] & 0xffff0000u);
     const float w0 = __uint_as_float(w[e] << 16), w1 = __uint_as_float(w[e] & 0xffff0000u);
-    o[e] = pack_bf16x2(w0 * round_bf16(r0 * inv), w1 * round_bf16(r1 * inv));
+    const uint32_t hp = pack_bf16x2(r0 * inv, r1 * inv);   // round(r * inv), both halves
+    o[e] = pack_bf16x2(w0 * __uint_as_float(hp << 16), w1 * __uint_as_float(hp & 0xffff0000u));
   }
   return o;
 }
@@ -452,9 +482,11 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
     load_x(Q2{}, min(c0 + 2, clast));
   }
   if constexpr (NX) {   // the row statistics' round trip overlaps the first chunks' loads
-    const int ptiles = (K + 63) / 64;
+    __shared__ float s_inv[G_MAX_M];
+    block_row_inv(a.xsq, (K + G_NORM_COLS - 1) / G_NORM_COLS, a.M, K, a.xeps, s_inv);
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < TM; ++i) xinv[i] = rms_norm_row_inv(a.xsq, ptiles, min(16 * i + c16, a.M - 1), r4, K, a.xeps);
+    for (int i = 0; i < TM; ++i) xinv[i] = s_inv[min(16 * i + c16, a.M - 1)];
   }
   int c = c0;
   for (; c + D <= c1; c += D) {   // whole rounds only: no path into the loop header skips a step
@@ -511,13 +543,204 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   tile_epilogue<TM, EPI>(a, src, t);
 }
 
+// ---------------------------------------------------------------------------------------------------
+// Tile-16 GEMM for projections with few weight rows (QKV, O: N in the low thousands, K <= 2048). A split-K
+// plan would need a cross-workgroup merge whose round trips (publish, counter, reload) cost more than the
+// few microseconds these projections stream for, so here one workgroup owns 16 weight rows over the whole
+// of K and nothing crosses workgroups:
+//   * 16 waves; wave w reads weight row w of the tile row-contiguously (16 bytes per lane, 1 KB per
+//     instruction) and stores it to LDS with its 16-byte chunks XOR-swizzled by the row inside each
+//     256-byte group, so the 16 rows one B-fragment read touches sit in 16 different bank groups.
+//   * wave w multiplies k-steps [w nks / 16, (w + 1) nks / 16): X fragments straight from L2 (normalised
+//     on load when the input is a NormedRows), B fragments from LDS; the 16 partial tiles are summed
+//     through LDS in wave order (deterministic).
+//   * everything the epilogue reads (bias, residual, cos/sin, slots, row statistics) is loaded at kernel
+//     start together with the weights, so the only dependent steps are the one weight round trip, the
+//     barrier and the stores.
+// Tiles: STORE / RESNORM 16 consecutive rows; SILU 8 gate rows + the matching 8 up rows (8 output
+// columns); ROPE 8 dims of a head + the 8 dims half a head further (the rotate-half partners).
+constexpr int T16_WAVES = 16;
+constexpr int T16_MAX_K = 2048;
+constexpr int T16_KSW = T16_MAX_K / 32 / T16_WAVES;   // k-steps per wave at most
+
+template <int EPI>
+__device__ __forceinline__ int t16_row(const GemmArgs& a, int t, int r) {
+  if constexpr (EPI == EPI_SILU) {
+    const int half = a.N >> 1;
+    return r < 8 ? min(8 * t + r, half - 1) : half + min(8 * t + r - 8, half - 1);
+  } else if constexpr (EPI == EPI_ROPE) {
+    const int tph = a.hd >> 4, head = t / tph, f = t - head * tph;
+    return head * a.hd + 8 * f + (r < 8 ? r : (a.hd >> 1) + r - 8);
+  } else {
+    return min(16 * t + r, a.N - 1);
+  }
+}
+
+template <int TM, int EPI, bool NX>
+__global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a) {
+  __shared__ __align__(16) unsigned char lds[16 * 2 * T16_MAX_K];   // weight tile, then the partial tiles
+  const int t = blockIdx.x, M = a.M, K = a.K;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c16 = lane & 15, r4 = lane >> 4;
+  const int rowb = 2 * K;   // bytes of a weight row = LDS pitch
+
+  // weight row wv of the tile, 16 bytes per lane per 1 KB piece
+  g_u32x4_t wr[T16_MAX_K * 2 / 1024];
+  {
+    const unsigned char* src = reinterpret_cast<const unsigned char*>(a.w + int64_t(t16_row<EPI>(a, t, wv)) * K);
+#pragma unroll
+    for (int j = 0; j < T16_MAX_K * 2 / 1024; ++j)
+      if (j * 1024 + lane * 16 < rowb) wr[j] = *reinterpret_cast<const g_u32x4_t*>(src + j * 1024 + lane * 16);
+  }
+  // X fragments (and norm weights) of this wave's k-steps
+  const int nks = K >> 5;
+  const int ks0 = wv * nks / T16_WAVES, ks1 = (wv + 1) * nks / T16_WAVES;
+  g_u32x4_t xr[T16_KSW][TM];
+  g_u32x4_t xw[T16_KSW];
+#pragma unroll
+  for (int s = 0; s < T16_KSW; ++s) {
+    const int k = 32 * max(min(ks0 + s, ks1 - 1), 0) + 8 * r4;   // past the wave's range: an in-bounds re-read
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xr[s][i] = *reinterpret_cast<const g_u32x4_t*>(a.x + int64_t(min(16 * i + c16, M - 1)) * K + k);
+    if constexpr (NX) xw[s] = *reinterpret_cast<const g_u32x4_t*>(a.xnw + k);
+  }
+  __shared__ float s_inv[G_MAX_M];
+  if constexpr (NX) block_row_inv(a.xsq, (K + G_NORM_COLS - 1) / G_NORM_COLS, M, K, a.xeps, s_inv);
+  // epilogue operands of this thread's output(s): thread (m, n) for STORE / RESNORM, (m, j) for the pairs
+  constexpr int PAIR = (EPI == EPI_SILU || EPI == EPI_ROPE) ? 1 : 0;
+  const int em = PAIR ? (tid >> 3) : (tid >> 4);
+  const int en = PAIR ? (tid & 7) : (tid & 15);
+  const bool elive = em < M && tid < TM * 16 * (PAIR ? 8 : 16);
+  const int emc = min(em, M - 1);
+  float e_bias0 = 0.f, e_bias1 = 0.f, e_res = 0.f, e_cl = 0.f, e_ch = 0.f, e_sl = 0.f, e_sh = 0.f;
+  int64_t e_slot = 0;
+  int col = 0;
+  if constexpr (EPI == EPI_STORE) {
+    col = min(16 * t + en, a.N - 1);
+    if (a.bias != nullptr) e_bias0 = bf16_to_f32(a.bias[col]);
+  } else if constexpr (EPI == EPI_RESNORM) {
+    col = min(16 * t + en, a.N - 1);
+    e_res = bf16_to_f32(a.residual[int64_t(emc) * a.N + col]);
+  } else if constexpr (EPI == EPI_ROPE) {
+    const int tph = a.hd >> 4, head = t / tph, f = t - head * tph, hh = a.hd >> 1;
+    const int d = 8 * f + en;
+    if (a.bias != nullptr) {
+      e_bias0 = bf16_to_f32(a.bias[head * a.hd + d]);
+      e_bias1 = bf16_to_f32(a.bias[head * a.hd + hh + d]);
+    }
+    if (head < a.nh + a.nkv) {
+      e_cl = bf16_to_f32(a.cosb[int64_t(emc) * a.hd + d]);
+      e_ch = bf16_to_f32(a.cosb[int64_t(emc) * a.hd + hh + d]);
+      e_sl = bf16_to_f32(a.sinb[int64_t(emc) * a.hd + d]);
+      e_sh = bf16_to_f32(a.sinb[int64_t(emc) * a.hd + hh + d]);
+    }
+    if (head >= a.nh && a.kc != nullptr) e_slot = a.slots[emc];
+  }
+
+  // weight row -> LDS: chunk q of row wv at (q & ~15) | ((q ^ wv) & 15)
+#pragma unroll
+  for (int j = 0; j < T16_MAX_K * 2 / 1024; ++j) {
+    const int q = j * 64 + lane;
+    if (q * 16 < rowb) *reinterpret_cast<g_u32x4_t*>(lds + wv * rowb + (((q & ~15) | ((q ^ wv) & 15)) << 4)) = wr[j];
+  }
+  __syncthreads();
+  float xinv[TM];
+  if constexpr (NX)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xinv[i] = s_inv[min(16 * i + c16, M - 1)];
+  g_float4_t acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) acc[i] = g_float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < T16_KSW; ++s) {
+    const int ks = ks0 + s;
+    if (ks < ks1) {
+      const int q = 4 * ks + r4;   // chunk of row c16 this lane's B fragment is
+      const g_bf16x8_t b = __builtin_bit_cast(
+          g_bf16x8_t, *reinterpret_cast<const g_u32x4_t*>(lds + c16 * rowb + (((q & ~15) | ((q ^ c16) & 15)) << 4)));
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        g_u32x4_t xa = xr[s][i];
+        if constexpr (NX) xa = norm_fragment(xa, xw[s], xinv[i]);
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, xa), b, acc[i], 0, 0, 0);
+      }
+    }
+  }
+  __syncthreads();   // every wave is done with the weight tile: the LDS now takes the partial tiles
+  float* red = reinterpret_cast<float*>(lds);   // [wave][TM * 16 rows][16 columns]
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[(wv * TM * 16 + 16 * i + 4 * r4 + e) * 16 + c16] = acc[i][e];
+  __syncthreads();
+  auto value = [&](int m, int n) __attribute__((always_inline)) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < T16_WAVES; ++w) v += red[(w * TM * 16 + m) * 16 + n];
+    return v;
+  };
+  if constexpr (EPI == EPI_STORE) {
+    if (elive && 16 * t + en < a.N) a.y[int64_t(em) * a.N + 16 * t + en] = f32_to_bf16(value(em, en) + e_bias0);
+  } else if constexpr (EPI == EPI_RESNORM) {
+    float ss = 0.f;
+    if (tid < TM * 256) {
+      const float r = round_bf16(e_res + round_bf16(value(em, en)));
+      if (elive && 16 * t + en < a.N) a.res_out[int64_t(em) * a.N + 16 * t + en] = f32_to_bf16(r);
+      ss = 16 * t + en < a.N ? r * r : 0.f;
+    }
+    // the row's 16 columns are lanes 16k .. 16k+15 of one wave
+    ss += __shfl_xor(ss, 8, 64);
+    ss += __shfl_xor(ss, 4, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 1, 64);
+    if (elive && en == 0 && a.sumsq_out != nullptr) a.sumsq_out[int64_t(t) * G_MAX_M + em] = ss;
+  } else if constexpr (EPI == EPI_SILU) {
+    const int half = a.N >> 1, oc = 8 * t + en;
+    if (elive && oc < half) {
+      const float gb = round_bf16(value(em, en)), ub = round_bf16(value(em, en + 8));
+      a.y[int64_t(em) * half + oc] = f32_to_bf16(round_bf16(gb / (1.0f + expf(-gb))) * ub);
+    }
+  } else {   // EPI_ROPE
+    if (elive) {
+      const int tph = a.hd >> 4, head = t / tph, f = t - head * tph, hh = a.hd >> 1;
+      const int d = 8 * f + en;
+      const float xl = round_bf16(value(em, en) + e_bias0), xh = round_bf16(value(em, en + 8) + e_bias1);
+      float lo = xl, hi = xh;
+      if (head < a.nh + a.nkv) {
+        lo = round_bf16(xl * e_cl) - round_bf16(xh * e_sl);
+        hi = round_bf16(xh * e_ch) + round_bf16(xl * e_sh);
+      }
+      bf16_t* dst;
+      bf16_t* cdst = nullptr;
+      if (head < a.nh) {
+        dst = a.q + (int64_t(em) * a.nh + head) * a.hd;
+      } else if (head < a.nh + a.nkv) {
+        const int kh = head - a.nh;
+        dst = a.k + (int64_t(em) * a.nkv + kh) * a.hd;
+        if (a.kc != nullptr) cdst = a.kc + (e_slot * a.nkv + kh) * a.hd;
+      } else {
+        const int vh = head - a.nh - a.nkv;
+        dst = a.v + (int64_t(em) * a.nkv + vh) * a.hd;
+        if (a.vc != nullptr) cdst = a.vc + (e_slot * a.nkv + vh) * a.hd;
+      }
+      const bf16_t blo = f32_to_bf16(lo), bhi = f32_to_bf16(hi);
+      dst[d] = blo;
+      dst[hh + d] = bhi;
+      if (cdst != nullptr) {
+        cdst[d] = blo;
+        cdst[hh + d] = bhi;
+      }
+    }
+  }
+}
+
 // h = round(w * round(r * inv)) for whole rows, inv exactly as the GEMMs compute it on load: one wave per
 // row, 8 columns (16 bytes) per lane per step.
 __global__ __launch_bounds__(64) void rms_norm_apply_kernel(const bf16_t* __restrict__ r, const float* __restrict__ sumsq,
                                                            const bf16_t* __restrict__ w, bf16_t* __restrict__ h, int N,
                                                            float eps) {
   const int m = blockIdx.x, lane = threadIdx.x;
-  const float inv = rms_norm_row_inv(sumsq, (N + 63) / 64, m, lane >> 4, N, eps);
+  const float inv = rms_norm_row_inv(sumsq, (N + G_NORM_COLS - 1) / G_NORM_COLS, m, lane >> 4, N, eps);
   for (int c = 8 * lane; c < N; c += 8 * 64) {
     const g_u32x4_t rv = *reinterpret_cast<const g_u32x4_t*>(r + int64_t(m) * N + c);
     const g_u32x4_t wv = *reinterpret_cast<const g_u32x4_t*>(w + c);
@@ -607,6 +830,34 @@ static void launch_nx(const GemmArgs& a, hipStream_t st) {
   else
     hipLaunchKernelGGL((skinny_gemm_kernel<4, EPI, NX>), grid, block, 0, st, a);
 }
+// The tile-16 kernel takes projections with K <= 2048 and at most T16_MAX_TILES tiles (two per CU); wider
+// ones stream better through the 64-row tiles above.
+constexpr int T16_MAX_TILES = 512;
+static bool tile16_fits(int K, int tiles) { return K <= T16_MAX_K && tiles <= T16_MAX_TILES; }
+
+template <int EPI, bool NX>
+static void launch_t16_nx(const GemmArgs& a, int tiles, hipStream_t st) {
+  const dim3 grid{unsigned(tiles)}, block{unsigned(T16_WAVES * 64)};
+  if (a.M <= 16)
+    hipLaunchKernelGGL((tile16_gemm_kernel<1, EPI, NX>), grid, block, 0, st, a);
+  else if (a.M <= 32)
+    hipLaunchKernelGGL((tile16_gemm_kernel<2, EPI, NX>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((tile16_gemm_kernel<4, EPI, NX>), grid, block, 0, st, a);
+}
+template <int EPI>
+static int launch_t16(const GemmArgs& a, int tiles, hipStream_t st) {
+  if constexpr (EPI == EPI_RESNORM) {
+    launch_t16_nx<EPI, false>(a, tiles, st);
+  } else {
+    if (a.xsq != nullptr)
+      launch_t16_nx<EPI, true>(a, tiles, st);
+    else
+      launch_t16_nx<EPI, false>(a, tiles, st);
+  }
+  return check_launch("skinny_gemm(tile16)");
+}
+
 template <int EPI>
 static int launch(const GemmArgs& a, hipStream_t st) {
   if constexpr (EPI == EPI_RESNORM) {
@@ -663,6 +914,7 @@ extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, 
   a.bias = static_cast<const bf16_t*>(bias);
   a.y = static_cast<bf16_t*>(y);
   if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
+  if (tile16_fits(K, (N + 15) / 16)) return launch_t16<EPI_STORE>(a, (N + 15) / 16, reinterpret_cast<hipStream_t>(stream));
   if ((st = bind_workspace(a, make_plan((N + 63) / 64, K), ws, ws_bytes)) != NS_OK) return st;
   return launch<EPI_STORE>(a, reinterpret_cast<hipStream_t>(stream));
 }
@@ -677,6 +929,7 @@ extern "C" int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out,
   GemmArgs a = base_args(x, w_gate_up, M, N2, K);
   a.y = static_cast<bf16_t*>(out);
   if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
+  if (tile16_fits(K, (N2 / 2 + 7) / 8)) return launch_t16<EPI_SILU>(a, (N2 / 2 + 7) / 8, reinterpret_cast<hipStream_t>(stream));
   if ((st = bind_workspace(a, make_plan((N2 / 2 + 31) / 32, K), ws, ws_bytes)) != NS_OK) return st;
   return launch<EPI_SILU>(a, reinterpret_cast<hipStream_t>(stream));
 }
@@ -693,6 +946,7 @@ extern "C" int ns_gemm_residual_norm_stats(const void* x, const void* w, const v
   a.residual = static_cast<const bf16_t*>(residual);
   a.res_out = static_cast<bf16_t*>(res_out);
   a.sumsq_out = row_sumsq;
+  if (tile16_fits(K, (N + 15) / 16)) return launch_t16<EPI_RESNORM>(a, (N + 15) / 16, reinterpret_cast<hipStream_t>(stream));
   if ((st = bind_workspace(a, make_plan((N + 63) / 64, K), ws, ws_bytes)) != NS_OK) return st;
   return launch<EPI_RESNORM>(a, reinterpret_cast<hipStream_t>(stream));
 }
@@ -742,6 +996,7 @@ extern "C" int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, 
   a.nkv = n_kv_heads;
   a.hd = head_dim;
   if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
+  if (tile16_fits(K, N / 16)) return launch_t16<EPI_ROPE>(a, N / 16, reinterpret_cast<hipStream_t>(stream));
   if ((st = bind_workspace(a, make_plan(N / 64, K), ws, ws_bytes)) != NS_OK) return st;
   return launch<EPI_ROPE>(a, reinterpret_cast<hipStream_t>(stream));
 }

@@ -8,7 +8,7 @@ ROCm) followed by the standalone HIP token-wise kernels. Both routes round where
 round, so they differ only in the fp32 summation order of the products.
 
 RMSNorm between projections is not a pass of its own on the skinny route: the projection that produces
-the residual stream also writes per-64-column row sums of its square, and the projection that consumes
+the residual stream also writes per-16-column row sums of its square, and the projection that consumes
 rms_norm(residual) normalises its input fragments as it loads them ("norm on load"). Such an input is a
 NormedRows (r, row_sumsq, weight, eps); NormedRows.tensor() materialises h with the same arithmetic.
 
@@ -29,7 +29,8 @@ from nanoserve_amd import _lib
 from nanoserve_amd.kernels.fused import rms_norm, rope_qkv, silu_mul
 
 SKINNY_MAX_M = 64
-NORM_TILE = 64   # columns per row-sum partial of a NormedRows
+NORM_COLS = 16   # columns per row-sum partial of a NormedRows
+NORM_ROWS = 64   # rows the row-sum buffer holds (the skinny GEMMs' largest M)
 
 _WS: dict[int, torch.Tensor] = {}
 _WS_RETIRED: list[torch.Tensor] = []   # superseded buffers stay alive: captured graphs may point at them
@@ -52,8 +53,8 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
 
 
 class NormedRows:
-    """rms_norm(r) held as r (bf16 [M, K]) plus the row statistics of r: sumsq (fp32 [ceil(K/64), 64],
-    column m = row m, each entry the sum of r^2 over 64 columns), the norm weight [K] and eps."""
+    """rms_norm(r) held as r (bf16 [M, K]) plus the row statistics of r: sumsq (fp32 [ceil(K/16), 64],
+    column m = row m, each entry the sum of r^2 over 16 columns), the norm weight [K] and eps."""
 
     def __init__(self, r: torch.Tensor, sumsq: torch.Tensor, weight: torch.Tensor, eps: float):
         self.r, self.sumsq, self.weight, self.eps = r, sumsq, weight, float(eps)
@@ -85,7 +86,7 @@ class NormedRows:
     def rows(self, idx: torch.Tensor) -> "NormedRows":
         """The rows idx (in that order) as a NormedRows."""
         n = idx.shape[0]
-        sq = torch.zeros(self.sumsq.shape[0], NORM_TILE, dtype=self.sumsq.dtype, device=self.sumsq.device)
+        sq = torch.zeros(self.sumsq.shape[0], NORM_ROWS, dtype=self.sumsq.dtype, device=self.sumsq.device)
         sq[:, :n] = self.sumsq[:, idx]
         return NormedRows(self.r[idx].contiguous(), sq, self.weight, self.eps)
 
@@ -153,7 +154,7 @@ def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.T
     M, K = x.shape
     N = w.shape[0]
     res_out = torch.empty(M, N, device=x.device, dtype=x.dtype)
-    sumsq = torch.empty(-(-N // NORM_TILE), NORM_TILE, device=x.device, dtype=torch.float32) if norm_w is not None else None
+    sumsq = torch.empty(-(-N // NORM_COLS), NORM_ROWS, device=x.device, dtype=torch.float32) if norm_w is not None else None
     wsp, wsn = _ws_args(x, N)
     _lib.check(_lib.lib().ns_gemm_residual_norm_stats(
         x.data_ptr(), w.data_ptr(), residual.data_ptr(), res_out.data_ptr(), _lib.ptr(sumsq), M, N, K, 1, wsp, wsn,
