@@ -30,6 +30,8 @@
 // it serves the fp32 correctness paths.
 #include "ns_common.h"
 
+#include <type_traits>
+
 namespace ns {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -327,6 +329,314 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
   }
 }
 
+// ---------------------------------------------------------------------------------------------------
+// Whole-row variant for token rows of 256 bytes (n_kv * head_dim = 128: hd 64 with 2 KV heads, or hd 128
+// with 1) and at most 16 query heads. One workgroup covers every KV head of one row's partition, so a
+// block's K (and V) is read as one contiguous 4 KB stretch, and the loads are row-contiguous (each
+// instruction reads 4 whole token rows) instead of 16 tokens x 64 bytes:
+//   * lane (c16, r4) loads, for token quad j, token 4j + r4's 16-byte chunk c16. K goes through a
+//     wave-private LDS page (chunks XOR-swizzled by the token) into MFMA A fragments; V stays in
+//     registers and is transposed as in the per-head kernel.
+//   * S^T rows are relabelled (row r = token 4(r & 3) + (r >> 2)) so S^T's output layout is again P^T's
+//     B layout and matches the V^T fragments' token order.
+//   * all KV heads accumulate into one 16-column S^T tile: head h's products see only its own query
+//     columns (the others multiply zeros), and O^T rows hold both heads' dims; each lane keeps the rows
+//     of its own query's head.
+//   * a wave walks PPW pages with D pages of loads in flight (register slot i % D holds page i), so the
+//     softmax and MFMA work of early pages overlaps the stream of later ones.
+//   * partitions of PART = 32 pages; a row with several merges as the per-head kernel does: 16-byte
+//     coherent (sc1) stores of (m, l, acc), a wait for them, the row's counter, and the last partition
+//     to arrive loads MB partitions per round trip and folds them in partition order.
+constexpr int ROWK_NW = 4, ROWK_PPW = 8, ROWK_D = 2, ROWK_PART = ROWK_NW * ROWK_PPW;
+constexpr int ROWK_MB = 8;
+constexpr int ROWK_MAX_PARTS = 32;
+typedef __attribute__((ext_vector_type(4))) unsigned int rk_u32x4_t;
+typedef __attribute__((ext_vector_type(2))) unsigned int rk_u32x2_t;
+
+template <int HD>
+__global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
+    const bf16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, const bf16_t* __restrict__ kp,
+    const bf16_t* __restrict__ vp, int64_t s_blk, const int32_t* __restrict__ bt, int64_t bt_sb,
+    const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G, int nq,
+    int max_blocks, int num_blocks, float scale_log2, unsigned* __restrict__ cnt, float* __restrict__ part_acc,
+    float* __restrict__ part_ml, int B, int n_parts) {
+  constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D, PART = ROWK_PART;
+  constexpr int RE = 128;            // elements of a token row (all KV heads)
+  constexpr int NKV = 128 / HD;
+  constexpr int KS = HD / 32;
+  constexpr int AROW = HD + 4;
+  constexpr int K_LDS = NW * 16 * 256;
+  constexpr int M_LDS = NW * 16 * AROW * 4;
+  __shared__ __align__(16) unsigned char lds[K_LDS > M_LDS ? K_LDS : M_LDS];
+  __shared__ float sm_m[NW][16], sm_l[NW][16];
+  __shared__ unsigned s_last;
+
+  // XCD-aware map as in the per-head kernel: a row's partitions rotate over the XCDs
+  const int L = blockIdx.x, part = L / B;
+  const int b = (L - part * B + part) % B;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c16 = lane & 15, r4 = lane >> 4;
+  const int p0 = part * PART;
+
+  // ctx, this wave's block ids (lane i < PPW holds page i's) and Q go out together
+  const int ctx = ctxl[b];
+  int blk_lane;
+  {
+    const int p = p0 + w + NW * (lane < PPW ? lane : 0);
+    blk_lane = p < max_blocks ? bt[int64_t(b) * bt_sb + p] : -1;
+  }
+  const bool qlive = c16 < nq;
+  const int gq = qlive ? c16 / G : NKV;   // KV head of this lane's query column
+  bf16x8_t qf[KS];
+  {
+    const bf16_t* qrow = q + int64_t(b) * q_sb + int64_t(qlive ? c16 : 0) * q_sh;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      rk_u32x4_t u = *reinterpret_cast<const rk_u32x4_t*>(qrow + 32 * s + 8 * r4);
+      if (!qlive) u = rk_u32x4_t{0u, 0u, 0u, 0u};
+      qf[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+  int n_pages = ctx > 0 ? (ctx + PAGE - 1) / PAGE : 0;
+  if (n_pages > max_blocks) n_pages = max_blocks;
+  if (ctx <= 0) {   // no keys: zeros
+    if (part == 0)
+      for (int i = tid; i < nq * HD; i += NW * 64) out[int64_t(b) * o_sb + int64_t(i / HD) * o_sh + (i % HD)] = bf16_t(0);
+    return;
+  }
+  if (p0 >= n_pages) return;
+  const int n_active = (n_pages + PART - 1) / PART;
+
+  // This wave's pages are p0 + w + NW i, i < PPW. Page i's K and V sit in register slot i % D; a slot is
+  // refilled with page i + D once page i is consumed. Pages past the row's end re-load the wave's first
+  // page (so every path issues the same loads) and skip the arithmetic.
+  int n_live = 0;
+#pragma unroll
+  for (int i = 0; i < PPW; ++i) n_live += (p0 + w + NW * i < n_pages) ? 1 : 0;
+  rk_u32x4_t kr[D][4], vr[D][4];
+  auto issue = [&](int i, auto sc) __attribute__((always_inline)) {
+    constexpr int sl = decltype(sc)::value;
+    const int bid = __builtin_amdgcn_readlane(blk_lane, i < n_live ? i : 0);
+    const bool ok = n_live > 0 && bid >= 0 && bid < num_blocks;
+    const int64_t base = int64_t(ok ? bid : 0) * s_blk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t off = base + int64_t(4 * j + r4) * RE + c16 * 8;
+      kr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(kp + off);
+      vr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(vp + off);
+    }
+  };
+  unsigned char* kpg = lds + w * (16 * 256);
+  float m_run = -INFINITY, l_run = 0.f;
+  float4_t acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const int tr = 4 * (c16 & 3) + (c16 >> 2);   // token of S^T row c16
+  auto page = [&](int i, auto sc) __attribute__((always_inline)) {
+    constexpr int sl = decltype(sc)::value;
+    const int p = p0 + w + NW * i;
+    const int bid = __builtin_amdgcn_readlane(blk_lane, i);
+    const bool okp = bid >= 0 && bid < num_blocks;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 4 * j + r4;
+      *reinterpret_cast<rk_u32x4_t*>(kpg + t * 256 + ((c16 ^ t) << 4)) = kr[sl][j];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): the page's K rows are in LDS
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    float4_t st = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < NKV; ++h)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int c = (h * HD + 32 * s + 8 * r4) >> 3;   // 16-byte chunk of the token row
+        const rk_u32x4_t a = *reinterpret_cast<const rk_u32x4_t*>(kpg + tr * 256 + ((c ^ tr) << 4));
+        const bf16x8_t bq = gq == h ? qf[s] : __builtin_bit_cast(bf16x8_t, rk_u32x4_t{0u, 0u, 0u, 0u});
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), bq, st, 0, 0, 0);
+      }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the next page's K writes stay behind these reads
+    // lane (c16, r4) holds rows 4 r4 + k = tokens 4k + r4 of the page
+    bool valid[4];
+    float sv[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      valid[k] = okp && (p * PAGE + 4 * k + r4) < ctx;
+      sv[k] = valid[k] ? st[k] * scale_log2 : -INFINITY;
+      mx = fmaxf(mx, sv[k]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    float pv[4], psum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      pv[k] = exp2f(sv[k] - m_use);
+      psum += pv[k];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    short4_t pb;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pb[k] = short(f32_to_bf16(pv[k]));
+    // V^T tile t: row c16 = 16-byte chunk c16 (dim 8 c16 + t of the row), k = token 4j + r4
+    const uint32_t m01 = (valid[0] ? 0x0000ffffu : 0u) | (valid[1] ? 0xffff0000u : 0u);
+    const uint32_t m23 = (valid[2] ? 0x0000ffffu : 0u) | (valid[3] ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int wd = t >> 1;
+      uint32_t lo, hi;
+      if ((t & 1) == 0) {
+        lo = pack_lo(vr[sl][0][wd], vr[sl][1][wd]);
+        hi = pack_lo(vr[sl][2][wd], vr[sl][3][wd]);
+      } else {
+        lo = pack_hi(vr[sl][0][wd], vr[sl][1][wd]);
+        hi = pack_hi(vr[sl][2][wd], vr[sl][3][wd]);
+      }
+      const short4_t va = __builtin_bit_cast(short4_t, make_uint2(lo & m01, hi & m23));
+      acc[t] *= alpha;
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+    }
+  };
+  using Z0 = std::integral_constant<int, 0>;
+  using Z1 = std::integral_constant<int, 1>;
+  static_assert(D == 2 && PPW % 2 == 0, "the page loop is unrolled for two slots");
+  issue(0, Z0{});
+  issue(1, Z1{});
+#pragma unroll
+  for (int i0 = 0; i0 < PPW; i0 += 2) {
+    if (i0 < n_live) page(i0, Z0{});       // wave-uniform
+    if (i0 + 2 < PPW) issue(i0 + 2, Z0{});
+    if (i0 + 1 < n_live) page(i0 + 1, Z1{});
+    if (i0 + 3 < PPW) issue(i0 + 3, Z1{});
+  }
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+
+  // ---- merge the waves through LDS: [wave][query][dim]; a lane keeps the O^T rows of its query's head
+  __syncthreads();   // every wave is done with its K page: the buffer is reused
+  float* sm_acc = reinterpret_cast<float*>(lds);
+  if (r4 == 0) {
+    sm_m[w][c16] = m_run;
+    sm_l[w][c16] = l_run;
+  }
+  {
+    const int head = NKV == 2 ? (r4 >> 1) : 0;   // rows 4 r4 + k are chunks of head (4 r4 + k) / (HD / 8)
+    if (head == gq) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) sm_acc[(w * 16 + c16) * AROW + ((8 * (4 * r4 + k) + t) & (HD - 1))] = acc[t][k];
+    }
+  }
+  __syncthreads();
+  auto part_state = [&](int h, int d4, float& M, float& Ls, float (&A)[4]) __attribute__((always_inline)) {
+    M = -INFINITY;
+#pragma unroll
+    for (int x = 0; x < NW; ++x) M = fmaxf(M, sm_m[x][h]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    Ls = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) A[e] = 0.f;
+#pragma unroll
+    for (int x = 0; x < NW; ++x) {
+      const float wgt = exp2f(sm_m[x][h] - Mu);   // waves without live pages: m = -inf -> weight 0
+      Ls += wgt * sm_l[x][h];
+      const float4_t v = *reinterpret_cast<const float4_t*>(sm_acc + (x * 16 + h) * AROW + 4 * d4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) A[e] += wgt * v[e];
+    }
+  };
+  auto store_out = [&](int h, int d4, float Ls, const float (&A)[4]) __attribute__((always_inline)) {
+    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+    const uint2 pk = make_uint2(uint32_t(f32_to_bf16(A[0] * inv)) | (uint32_t(f32_to_bf16(A[1] * inv)) << 16),
+                                uint32_t(f32_to_bf16(A[2] * inv)) | (uint32_t(f32_to_bf16(A[3] * inv)) << 16));
+    *reinterpret_cast<uint2*>(out + int64_t(b) * o_sb + int64_t(h) * o_sh + 4 * d4) = pk;
+  };
+  constexpr int ITEMS = (16 * (HD / 4) + NW * 64 - 1) / (NW * 64);
+  const int n_items = nq * (HD / 4);
+  if (n_active == 1) {
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int idx = tid + it * NW * 64;
+      if (idx < n_items) {
+        const int h = idx / (HD / 4), d4 = idx % (HD / 4);
+        float M, Ls, A[4];
+        part_state(h, d4, M, Ls, A);
+        store_out(h, d4, Ls, A);
+      }
+    }
+    return;
+  }
+  // publish (m, l, acc) with 16-byte coherent stores, wait for them, then the row's counter
+  const __amdgpu_buffer_rsrc_t racc =
+      __builtin_amdgcn_make_buffer_rsrc(part_acc + int64_t(b) * n_parts * (16 * HD), 0, n_parts * (16 * HD) * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rml =
+      __builtin_amdgcn_make_buffer_rsrc(part_ml + int64_t(b) * n_parts * 32, 0, n_parts * 32 * 4, 0x00020000);
+  constexpr int SC1 = 16;   // cache policy sc1: device-coherent, bypasses the XCD's L2
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int idx = tid + it * NW * 64;
+    if (idx < n_items) {
+      const int h = idx / (HD / 4), d4 = idx % (HD / 4);
+      float M, Ls, A[4];
+      part_state(h, d4, M, Ls, A);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          rk_u32x4_t{__float_as_uint(A[0]), __float_as_uint(A[1]), __float_as_uint(A[2]), __float_as_uint(A[3])}, racc,
+          ((part * 16 + h) * HD + 4 * d4) * 4, 0, SC1);
+      if (d4 == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(rk_u32x2_t{__float_as_uint(M), __float_as_uint(Ls)}, rml,
+                                              (part * 32 + 2 * h) * 4, 0, SC1);
+    }
+  }
+  publish_complete();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = publish_count(cnt + b);
+    const unsigned lst = prev == unsigned(n_active - 1);
+    if (lst) publish_reset(cnt + b);
+    s_last = lst;
+  }
+  __syncthreads();
+  if (s_last == 0u) return;
+  acquire_published();
+  // the last partition: MB partitions per round trip, folded in partition order with a running max
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int idx = tid + it * NW * 64;
+    if (idx < n_items) {
+      const int h = idx / (HD / 4), d4 = idx % (HD / 4);
+      float M = -INFINITY, Ls = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int x0 = 0; x0 < n_active; x0 += ROWK_MB) {
+        rk_u32x4_t ua[ROWK_MB];
+        rk_u32x2_t um[ROWK_MB];
+#pragma unroll
+        for (int e = 0; e < ROWK_MB; ++e) {
+          const int x = min(x0 + e, n_active - 1);
+          ua[e] = __builtin_amdgcn_raw_buffer_load_b128(racc, ((x * 16 + h) * HD + 4 * d4) * 4, 0, SC1);
+          um[e] = __builtin_amdgcn_raw_buffer_load_b64(rml, (x * 32 + 2 * h) * 4, 0, SC1);
+        }
+#pragma unroll
+        for (int e = 0; e < ROWK_MB; ++e) {
+          if (x0 + e < n_active) {
+            const float pm = __uint_as_float(um[e][0]), pl = __uint_as_float(um[e][1]);
+            const float Mn = fmaxf(M, pm);
+            const float a_old = M == -INFINITY ? 0.f : exp2f(M - Mn);
+            const float a_new = pm == -INFINITY ? 0.f : exp2f(pm - Mn);
+            Ls = Ls * a_old + pl * a_new;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) A[c] = A[c] * a_old + __uint_as_float(ua[e][c]) * a_new;
+            M = Mn;
+          }
+        }
+      }
+      store_out(h, d4, Ls, A);
+    }
+  }
+}
+
 // fp32: one wave per (row, KV head). Lane owns dims lane and lane + 64 (hd 128).
 template <int HD>
 __global__ __launch_bounds__(64) void paged_decode_f32_kernel(
@@ -396,16 +706,36 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 using namespace ns;
 
-// Workspace: [B * n_kv] arrival counters (zeroed once by the owner; every launch leaves them at zero),
-// then the partitions' (m, l) and accumulators.
-extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype) {
-  if (dtype != NS_DTYPE_BF16 || B <= 0 || n_kv_heads <= 0 || max_blocks <= 0) return 0;
-  if (head_dim != 64 && head_dim != 128) return 0;
+// Whole-row kernel: n_kv * head_dim == 128 (one 256-byte token row), <= 16 query heads, token rows
+// contiguous in the pool, and a table width its merge covers.
+static inline bool rows_kernel_fits(int n_heads, int n_kv_heads, int head_dim, int64_t kv_spos, int64_t kv_sh,
+                                    int max_blocks) {
+  return n_kv_heads * head_dim == 128 && n_heads <= 16 && kv_sh == head_dim && kv_spos == 128 &&
+         (max_blocks + ROWK_PART - 1) / ROWK_PART <= ROWK_MAX_PARTS;
+}
+static inline size_t per_head_ws_bytes(int B, int n_kv_heads, int head_dim, int max_blocks) {
   const size_t parts = size_t(decode_parts(head_dim, max_blocks));
   if (parts <= 1) return 0;
   const size_t rows = size_t(B) * n_kv_heads, slots = rows * parts;
   return align256(rows * sizeof(unsigned)) + align256(slots * 16 * 2 * sizeof(float)) +
          align256(slots * 16 * size_t(head_dim) * sizeof(float));
+}
+static inline size_t rows_ws_bytes(int B, int head_dim, int max_blocks) {
+  const size_t parts = size_t((max_blocks + ROWK_PART - 1) / ROWK_PART);
+  if (parts <= 1) return 0;
+  return align256(size_t(B) * sizeof(unsigned)) + align256(size_t(B) * parts * 32 * sizeof(float)) +
+         align256(size_t(B) * parts * 16 * size_t(head_dim) * sizeof(float));
+}
+
+// Workspace: arrival counters at offset 0 (zeroed once by the owner; every launch leaves them at zero),
+// then the partitions' (m, l) and accumulators. Sized for whichever kernel the shape takes; both follow
+// the same publish-then-count protocol, so one buffer may serve calls of either.
+extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype) {
+  if (dtype != NS_DTYPE_BF16 || B <= 0 || n_kv_heads <= 0 || max_blocks <= 0) return 0;
+  if (head_dim != 64 && head_dim != 128) return 0;
+  const size_t a = per_head_ws_bytes(B, n_kv_heads, head_dim, max_blocks);
+  const size_t r = n_kv_heads * head_dim == 128 ? rows_ws_bytes(B, head_dim, max_blocks) : 0;
+  return a > r ? a : r;
 }
 
 extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,
@@ -449,6 +779,42 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                      16 ==
                  0,
              "paged_attention_decode: q / k_pool / v_pool must be 16-byte aligned");
+  const float sl2 = scale * LOG2E;
+  if (rows_kernel_fits(n_heads, n_kv_heads, head_dim, kv_spos, kv_sh, max_blocks)) {
+    const int rparts = (max_blocks + ROWK_PART - 1) / ROWK_PART;
+    unsigned* rcnt = nullptr;
+    float* rml = nullptr;
+    float* racc = nullptr;
+    if (rparts > 1) {
+      const size_t need = ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype);
+      if (workspace == nullptr || workspace_bytes < need) {
+        set_error("paged_attention_decode: zero-initialised workspace of %zu bytes needed, got %zu", need,
+                  workspace == nullptr ? size_t(0) : workspace_bytes);
+        return NS_E_WORKSPACE;
+      }
+      NS_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+                 "paged_attention_decode: workspace not 256-byte aligned");
+      char* w = static_cast<char*>(workspace);
+      rcnt = reinterpret_cast<unsigned*>(w);
+      rml = reinterpret_cast<float*>(w + align256(size_t(B) * sizeof(unsigned)));
+      racc = reinterpret_cast<float*>(w + align256(size_t(B) * sizeof(unsigned)) +
+                                      align256(size_t(B) * rparts * 32 * sizeof(float)));
+    }
+    const dim3 rgrid(unsigned(rparts) * unsigned(B));
+    if (head_dim == 64)
+      hipLaunchKernelGGL(paged_decode_rows_bf16_kernel<64>, rgrid, dim3(ROWK_NW * 64), 0, s,
+                         static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
+                         static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
+                         static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
+                         rml, B, rparts);
+    else
+      hipLaunchKernelGGL(paged_decode_rows_bf16_kernel<128>, rgrid, dim3(ROWK_NW * 64), 0, s,
+                         static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
+                         static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
+                         static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
+                         rml, B, rparts);
+    return check_launch("paged_attention_decode(bf16 rows)");
+  }
   const int parts = decode_parts(head_dim, max_blocks);
   const int max_parts = head_dim == 64 ? MERGE_MAX_PARTS<64> : MERGE_MAX_PARTS<128>;
   NS_REQUIRE(parts <= max_parts, "paged_attention_decode: %d partitions (table width %d) exceed %d", parts, max_blocks,
@@ -457,7 +823,7 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
   float* ws_ml = nullptr;
   unsigned* ws_cnt = nullptr;
   if (parts > 1) {
-    const size_t need = ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype);
+    const size_t need = per_head_ws_bytes(B, n_kv_heads, head_dim, max_blocks);
     if (workspace == nullptr || workspace_bytes < need) {
       set_error("paged_attention_decode: zero-initialised workspace of %zu bytes needed, got %zu", need,
                 workspace == nullptr ? size_t(0) : workspace_bytes);
@@ -470,7 +836,6 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
     ws_ml = reinterpret_cast<float*>(w + align256(rows * sizeof(unsigned)));
     ws_acc = reinterpret_cast<float*>(w + align256(rows * sizeof(unsigned)) + align256(slots * 16 * 2 * sizeof(float)));
   }
-  const float sl2 = scale * LOG2E;
   const dim3 grid(unsigned(parts) * unsigned(n_kv_heads) * unsigned(B));
   if (head_dim == 64)
     hipLaunchKernelGGL(paged_decode_bf16_kernel<64>, grid, dim3(DecodeCfg<64>::NW * 64), 0, s,
