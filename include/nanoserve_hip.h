@@ -137,6 +137,19 @@ int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, void* q, void
                 int64_t n_tok, int n_heads, int n_kv_heads, int head_dim, int dtype, void* stream);
 
 /*
+ * The first ops of a forward step in one launch: x[i] = embed[token_ids[i]] ([vocab, hidden], row-major;
+ * an id outside [0, vocab) gives a zero row) and the RoPE tables cos/sin[i] = cat(f, f).cos() / .sin()
+ * rounded to the dtype, f = float(positions[i]) * inv_freq (fp32 [head_dim / 2]); x_out [n_tokens, hidden],
+ * cos/sin [n_tokens, head_dim]. row_sumsq (fp32 [ceil(hidden / 16)][64], may be NULL; n_tokens <= 64 then)
+ * receives the first RMSNorm's statistics in the layout ns_gemm_residual_norm_stats writes, so the first
+ * projection can normalise on load. hidden a multiple of 16.
+ * Replaces F.embedding (nanoserve/model.py:341) and Qwen2Model.rope (model.py:212-217).
+ */
+int ns_embed_rope(const int64_t* token_ids, const int64_t* positions, int64_t n_tokens, const void* embed,
+                  int64_t vocab, int hidden, const float* inv_freq, int head_dim, void* x_out, void* cos_out,
+                  void* sin_out, float* row_sumsq, int dtype, void* stream);
+
+/*
  * Skinny GEMMs of the decode step (bf16, 1 <= M <= 64, K a multiple of 32; W row-major [N, K], x [M, K],
  * outputs row-major, every pointer 16-byte aligned). They replace the F.linear calls of
  * nanoserve/model.py:231,256-257,362 for decode-sized batches: y = x W^T (+ bias) with fp32 accumulation

@@ -1,5 +1,5 @@
-// Token-wise fused kernels of the decode step for gfx950: RMSNorm (+ residual add), SiLU*mul, and
-// RoPE on the merged QKV projection with the paged KV write.
+// Token-wise fused kernels of the decode step for gfx950: RMSNorm (+ residual add), SiLU*mul, RoPE on the
+// merged QKV projection with the paged KV write, and the step's embedding + RoPE tables.
 //
 // Every kernel rounds to the tensor dtype exactly where PyTorch's unfused ops round, so bf16
 // outputs equal the unfused ops bit for bit apart from RMSNorm's fp32 sum order (<= 1 bf16 ulp).
@@ -172,6 +172,58 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(const T* __restrict__ qkv
   }
 }
 
+// ------------------------------------------------------------------------- embedding + RoPE tables
+// The first ops of a forward step in one launch (nanoserve/model.py:337-342 F.embedding and :212-217
+// rope): x[i] = embed[token_ids[i]]; cos/sin[i] = cat(f, f).cos()/.sin() rounded to the dtype with
+// f = float(positions[i]) * inv_freq (fp32). With row_sumsq given (decode batches, <= 64 rows) it also
+// writes the statistics the first RMSNorm takes on load: row_sumsq[p][i] = sum over columns 16p .. 16p+15
+// of x[i]^2. A token id outside [0, vocab) yields a zero row. One workgroup of 256 threads per token.
+template <typename T>
+__global__ __launch_bounds__(256) void embed_rope_kernel(const int64_t* __restrict__ ids, const int64_t* __restrict__ pos,
+                                                         const T* __restrict__ embed, int64_t vocab, int hidden,
+                                                         const float* __restrict__ inv_freq, int head_dim,
+                                                         T* __restrict__ x, T* __restrict__ cosb, T* __restrict__ sinb,
+                                                         float* __restrict__ row_sumsq) {
+  const int64_t i = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t id = ids[i];
+  const bool ok = id >= 0 && id < vocab;
+  const T* src = embed + (ok ? id : 0) * int64_t(hidden);
+  T* dst = x + i * int64_t(hidden);
+  constexpr int VEC = 16 / sizeof(T);   // elements per 16-byte chunk
+  // 16-column groups are VEC == 8 ? two threads : four threads; the group's sum is formed by shuffles
+  constexpr int TPG = 16 / VEC;
+  for (int c0 = 0; c0 < hidden; c0 += 256 * VEC) {
+    const int c = c0 + tid * VEC;
+    float ss = 0.f;
+    if (c < hidden) {
+      uint4 u = *reinterpret_cast<const uint4*>(src + c);
+      if (!ok) u = make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4*>(dst + c) = u;
+      const T* e = reinterpret_cast<const T*>(&u);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) {
+        const float f = io<T>::ld(e + q);
+        ss += f * f;
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < TPG; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    if (row_sumsq != nullptr && c < hidden && (tid % TPG) == 0) row_sumsq[int64_t(c / 16) * 64 + i] = ss;
+  }
+  const int half = head_dim >> 1;
+  if (tid < half) {
+    const float f = float(pos[i]) * inv_freq[tid];
+    const float cv = cosf(f), sv = sinf(f);
+    T* cr = cosb + i * int64_t(head_dim);
+    T* sr = sinb + i * int64_t(head_dim);
+    io<T>::st(cr + tid, cv);
+    io<T>::st(cr + half + tid, cv);
+    io<T>::st(sr + tid, sv);
+    io<T>::st(sr + half + tid, sv);
+  }
+}
+
 }  // namespace ns
 
 using namespace ns;
@@ -244,4 +296,30 @@ extern "C" int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, vo
                        static_cast<float*>(k_cache), static_cast<float*>(v_cache), slots, n_heads, n_kv_heads,
                        head_dim);
   return check_launch("rope_qkv");
+}
+
+extern "C" int ns_embed_rope(const int64_t* token_ids, const int64_t* positions, int64_t n_tokens, const void* embed,
+                             int64_t vocab, int hidden, const float* inv_freq, int head_dim, void* x_out, void* cos_out,
+                             void* sin_out, float* row_sumsq, int dtype, void* stream) {
+  NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "embed_rope: dtype %d not supported", dtype);
+  const int vec = dtype == NS_DTYPE_BF16 ? 8 : 4;
+  NS_REQUIRE(hidden > 0 && hidden % 16 == 0, "embed_rope: hidden %d must be a positive multiple of 16", hidden);
+  NS_REQUIRE(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 512, "embed_rope: head_dim %d (even, <= 512)", head_dim);
+  NS_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t(1) << 31), "embed_rope: n_tokens %lld", (long long)n_tokens);
+  NS_REQUIRE(row_sumsq == nullptr || n_tokens <= 64, "embed_rope: row statistics need <= 64 tokens, got %lld",
+             (long long)n_tokens);
+  NS_REQUIRE((reinterpret_cast<uintptr_t>(embed) | reinterpret_cast<uintptr_t>(x_out)) % 16 == 0,
+             "embed_rope: embed and x_out must be 16-byte aligned");
+  (void)vec;
+  if (n_tokens == 0) return NS_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == NS_DTYPE_BF16)
+    hipLaunchKernelGGL(embed_rope_kernel<bf16_t>, dim3(unsigned(n_tokens)), dim3(256), 0, s, token_ids, positions,
+                       static_cast<const bf16_t*>(embed), vocab, hidden, inv_freq, head_dim, static_cast<bf16_t*>(x_out),
+                       static_cast<bf16_t*>(cos_out), static_cast<bf16_t*>(sin_out), row_sumsq);
+  else
+    hipLaunchKernelGGL(embed_rope_kernel<float>, dim3(unsigned(n_tokens)), dim3(256), 0, s, token_ids, positions,
+                       static_cast<const float*>(embed), vocab, hidden, inv_freq, head_dim, static_cast<float*>(x_out),
+                       static_cast<float*>(cos_out), static_cast<float*>(sin_out), row_sumsq);
+  return check_launch("embed_rope");
 }

@@ -2,8 +2,9 @@
 // `logits.argmax(-1)`). Semantics of torch.argmax: the index of the first maximal value, NaN counting
 // as larger than every number (the first NaN wins).
 //
-// One workgroup per row, each thread scans a strided part of the row with 16-byte loads (8 bf16), keeps
-// (value, index) with first-index tie breaking, then a wave64 shuffle reduction and a cross-wave step.
+// One workgroup per row, each thread scans a strided part of the row with 16-byte loads (8 bf16, eight
+// loads in flight), keeps (value, index) with first-index tie breaking, then a wave64 shuffle reduction
+// and a cross-wave step.
 #include "ns_common.h"
 
 namespace ns {
@@ -32,16 +33,32 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__
   constexpr int VEC = 16 / sizeof(T);
   const bool vec_ok = (reinterpret_cast<uintptr_t>(r) % 16) == 0;
   const int nv = vec_ok ? n / VEC : 0;
-  for (int v = threadIdx.x; v < nv; v += blockDim.x) {
-    const uint4 u = reinterpret_cast<const uint4*>(r)[v];
-    const T* e = reinterpret_cast<const T*>(&u);
+  // U vectors in flight per thread: a row is one workgroup's, so its bandwidth comes from memory-level
+  // parallelism inside the workgroup, not from more workgroups. Indices still rise within each thread,
+  // so first-index tie breaking is kept.
+  constexpr int U = 8;
+  const int stride = int(blockDim.x);
+  for (int v0 = threadIdx.x; v0 < nv; v0 += U * stride) {
+    uint4 u[U];
 #pragma unroll
-    for (int q = 0; q < VEC; ++q) {
-      float f;
-      if constexpr (sizeof(T) == 2) f = bf16_to_f32(reinterpret_cast<const bf16_t*>(e)[q]);
-      else f = reinterpret_cast<const float*>(e)[q];
-      const int i = v * VEC + q;
-      if (better(f, i, bv, bi)) { bv = f; bi = i; }
+    for (int k = 0; k < U; ++k) {
+      const int v = v0 + k * stride;
+      u[k] = v < nv ? reinterpret_cast<const uint4*>(r)[v] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int v = v0 + k * stride;
+      if (v < nv) {
+        const T* e = reinterpret_cast<const T*>(&u[k]);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          float f;
+          if constexpr (sizeof(T) == 2) f = bf16_to_f32(reinterpret_cast<const bf16_t*>(e)[q]);
+          else f = reinterpret_cast<const float*>(e)[q];
+          const int i = v * VEC + q;
+          if (better(f, i, bv, bi)) { bv = f; bi = i; }
+        }
+      }
     }
   }
   for (int i = nv * VEC + threadIdx.x; i < n; i += blockDim.x) {

@@ -7,6 +7,10 @@ Same entry points, argument meaning and return values as nanoserve/kernels/fused
     rope_qkv(qkv, cos, sin, n_heads, n_kv_heads, head_dim,
              k_cache=None, v_cache=None, slots=None) -> (q, k, v)             (fused.py:156-175)
 
+and the step's first ops in one launch (F.embedding + Qwen2Model.rope, nanoserve/model.py:341,212-217):
+
+    embed_rope(token_ids, positions, embed, inv_freq, head_dim, row_stats=False) -> (x, cos, sin, sumsq)
+
 Each kernel rounds to the model dtype where PyTorch's unfused ops round, so bf16 results equal the
 unfused ops bit for bit except for RMSNorm's fp32 summation order (then at most 1 bf16 ulp apart).
 Outputs are allocated here with torch (inside a graph capture they come from the graph's pool).
@@ -80,3 +84,25 @@ def rope_qkv(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_heads: i
         _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(slots) if write else None,
         N, n_heads, n_kv_heads, head_dim, _lib.dtype_code(qkv), _lib.stream_of(qkv)), "rope_qkv")
     return q, k, v
+
+
+def embed_rope(token_ids: torch.Tensor, positions: torch.Tensor, embed: torch.Tensor, inv_freq: torch.Tensor,
+               head_dim: int, row_stats: bool = False):
+    """x = embed[token_ids] [N, H]; cos/sin [N, head_dim] (cat(f, f).cos()/.sin() in the embedding dtype,
+    f = positions.float() * inv_freq); with row_stats (N <= 64) also the first RMSNorm's row statistics
+    sumsq (fp32 [ceil(H / 16), 64]) for a NormedRows, else None."""
+    N = token_ids.shape[0]
+    V, H = embed.shape
+    assert token_ids.dtype == torch.int64 and positions.dtype == torch.int64 and positions.shape == (N,)
+    assert token_ids.is_contiguous() and positions.is_contiguous() and embed.is_contiguous()
+    assert inv_freq.dtype == torch.float32 and inv_freq.shape == (head_dim // 2,) and inv_freq.is_contiguous()
+    _lib.require_gpu(token_ids, positions, embed, inv_freq)
+    dev, dt = embed.device, embed.dtype
+    x = torch.empty(N, H, device=dev, dtype=dt)
+    cos = torch.empty(N, head_dim, device=dev, dtype=dt)
+    sin = torch.empty(N, head_dim, device=dev, dtype=dt)
+    sumsq = torch.empty(-(-H // 16), 64, device=dev, dtype=torch.float32) if row_stats else None
+    _lib.check(_lib.lib().ns_embed_rope(token_ids.data_ptr(), positions.data_ptr(), N, embed.data_ptr(), V, H,
+                                        inv_freq.data_ptr(), head_dim, x.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                        _lib.ptr(sumsq), _lib.dtype_code(embed), _lib.stream_of(embed)), "embed_rope")
+    return x, cos, sin, sumsq

@@ -370,11 +370,16 @@ class Qwen2Model:
             raise ValueError("the HIP path needs the paged KV cache (`paged` + `slot_mapping`)")
         assert sum(s.n_tokens for s in seqs) == token_ids.shape[0], "seqs must cover token_ids exactly"
         self._rows_cache = None
-        from nanoserve_amd.kernels.fused import rms_norm
+        from nanoserve_amd.kernels.fused import embed_rope, rms_norm
+        from nanoserve_amd.kernels.linear import SKINNY_MAX_M, NormedRows
         L, eps = self.cfg.n_layers, self.cfg.rms_norm_eps
-        x = F.embedding(token_ids, self.embed)
-        cos, sin = self.rope(positions)
-        h = rms_norm(x, self.layers[0].ln1, eps)
+        # embedding rows and RoPE tables in one launch; a decode-sized bf16 batch also gets the first
+        # RMSNorm's row statistics, so layer 0's QKV projection normalises on load like every later layer
+        stats = self.dtype == torch.bfloat16 and token_ids.shape[0] <= SKINNY_MAX_M
+        x, cos, sin, sumsq = embed_rope(token_ids.contiguous(), positions.contiguous(), self.embed, self.inv_freq,
+                                        self.cfg.head_dim, row_stats=stats)
+        cos, sin = cos[None], sin[None]
+        h = NormedRows(x, sumsq, self.layers[0].ln1, eps) if stats else rms_norm(x, self.layers[0].ln1, eps)
         for i in range(L):
             q, k, v = self._qkv(i, h, cos, sin, paged, slot_mapping)
             o = self._attend(i, q, k, v, seqs, paged, decode_meta, slot_mapping=slot_mapping)[0]

@@ -95,3 +95,42 @@ def test_rope_without_cache(hiplib):
     check(q, q0, torch.bfloat16)
     check(k, k0, torch.bfloat16)
     assert torch.equal(v.cpu(), v0)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("H,hd,N", [(1536, 128, 32), (896, 64, 5), (2048, 128, 64), (256, 64, 200)])
+def test_embed_rope(hiplib, dtype, H, hd, N):
+    """x = embedding rows exactly; cos/sin equal the oracle's RoPE tables (HF order: fp32 positions *
+    inv_freq, cat, cos/sin, cast) to the check's gate; the row statistics are the 16-column sums of x^2
+    (fp64 closed form), and the norm they feed equals the oracle's rms_norm of x."""
+    from nanoserve_amd.kernels.fused import embed_rope
+    from nanoserve_amd.kernels.linear import NormedRows
+    g = cpu_gen(11)
+    V = 1000
+    embed = (torch.randn(V, H, generator=g) * 0.5).to(dtype)
+    ids = torch.randint(0, V, (N,), generator=g)
+    pos = torch.randint(0, 40000, (N,), generator=g)
+    inv = 1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float) / hd))
+    stats = dtype == torch.bfloat16 and N <= 64
+    x, cos, sin, sq = embed_rope(ids.cuda(), pos.cuda(), embed.cuda(), inv.cuda(), hd, row_stats=stats)
+    assert torch.equal(x.cpu(), embed[ids])
+    c_ref, s_ref = ops.rope_tables(pos, hd, 1e6, dtype)
+    check(cos, c_ref, dtype)
+    check(sin, s_ref, dtype)
+    if stats:
+        ref = (embed[ids].double() ** 2).view(N, H // 16, 16).sum(-1).T
+        torch.testing.assert_close(sq[:, :N].cpu().double(), ref, rtol=1e-5, atol=1e-6)
+        w = (1 + 0.1 * torch.randn(H, generator=g)).to(dtype)
+        h = NormedRows(x, sq, w.cuda(), 1e-6).tensor()
+        check(h, ops.rms_norm(embed[ids], w, 1e-6), dtype)
+    else:
+        assert sq is None
+
+
+def test_embed_rope_out_of_range_id_gives_a_zero_row(hiplib):
+    from nanoserve_amd.kernels.fused import embed_rope
+    embed = torch.randn(10, 64).to(torch.bfloat16).cuda()
+    ids = torch.tensor([3, 10, -1, 9]).cuda()
+    x, _, _, _ = embed_rope(ids, torch.arange(4).cuda(), embed, torch.ones(32).cuda(), 64)
+    assert torch.equal(x[0], embed[3]) and torch.equal(x[3], embed[9])
+    assert not x[1].any() and not x[2].any()
