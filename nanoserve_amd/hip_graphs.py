@@ -4,7 +4,8 @@ DecodeGraphRunner — one graph per batch bucket for pure-decode steps; contract
 nanoserve/cuda_graphs.py:42-126:
   * buckets (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128); a batch of n replays the smallest bucket >= n;
   * inputs live in static device buffers overwritten before each replay (tokens, positions, slots int64;
-    block tables int32 [Bmax, W]; context lengths int32), W = ceil(max_seq_len / block_size);
+    block tables int32 [B, W]; context lengths int32), W = ceil(max_seq_len / block_size); here each bucket
+    packs them into one buffer with a pinned host twin, so staging a step is one H2D copy;
   * padding rows use token 0, slot garbage_block * block_size, table row [garbage_block, 0, ...] and
     ctx 1: they write and read only the reserved garbage block;
   * capture is lazy (first use of a bucket) after two eager warm-ups on a shared side stream, and every
@@ -48,50 +49,63 @@ class DecodeGraphRunner:
         self.max_blocks = math.ceil(max_seq_len / pool.block_size)
         self.garbage_block = pool.allocator.allocate()
         dev, mb = model.device, self.max_bucket
-        self.tokens = torch.zeros(mb, dtype=torch.long, device=dev)
-        self.positions = torch.zeros(mb, dtype=torch.long, device=dev)
-        self.slots = torch.zeros(mb, dtype=torch.long, device=dev)
-        self.block_tables = torch.zeros(mb, self.max_blocks, dtype=torch.int32, device=dev)
-        self.context_lens = torch.ones(mb, dtype=torch.int32, device=dev)
         self.token_idx = torch.arange(mb, device=dev)
-        # pinned host staging: one H2D copy per buffer per step
-        self._h_tokens = torch.zeros(mb, dtype=torch.long, pin_memory=True)
-        self._h_positions = torch.zeros(mb, dtype=torch.long, pin_memory=True)
-        self._h_slots = torch.zeros(mb, dtype=torch.long, pin_memory=True)
-        self._h_tables = torch.zeros(mb, self.max_blocks, dtype=torch.int32, pin_memory=True)
-        self._h_lens = torch.ones(mb, dtype=torch.int32, pin_memory=True)
+        self.inputs: dict[int, tuple] = {}     # bucket -> (device buffer, pinned twin, device views, host views)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.outputs: dict[int, torch.Tensor] = {}
         self.greedy: dict[int, torch.Tensor] = {}    # in-graph argmax of each row's logits (int64)
         self.mempool = None
-        self._reset_to_padding()
 
     @property
     def captured_buckets(self) -> list[int]:
         return sorted(self.graphs)
 
+    def _views(self, buf: torch.Tensor, B: int):
+        """tokens, positions, slots (int64 [B]); context lengths (int32 [B]); block tables (int32 [B, W])."""
+        o1, o2, o3, o4 = 8 * B, 16 * B, 24 * B, 28 * B
+        return (buf[0:o1].view(torch.int64), buf[o1:o2].view(torch.int64), buf[o2:o3].view(torch.int64),
+                buf[o3:o4].view(torch.int32), buf[o4:].view(torch.int32).view(B, self.max_blocks))
+
+    def _buffers(self, B: int) -> tuple:
+        """Bucket B's static inputs: one packed device buffer with a pinned host twin, so a step's inputs
+        arrive in a single H2D copy of 28 B + 4 B W bytes."""
+        if B not in self.inputs:
+            n = 28 * B + 4 * B * self.max_blocks
+            dev = torch.zeros(n, dtype=torch.uint8, device=self.model.device)
+            host = torch.zeros(n, dtype=torch.uint8, pin_memory=True)
+            self.inputs[B] = (dev, host, self._views(dev, B), self._views(host, B))
+        return self.inputs[B]
+
     def bucket_for(self, n: int) -> int | None:
         return next((b for b in self.buckets if b >= n), None)
 
-    def _reset_to_padding(self) -> None:
-        self.tokens.zero_()
-        self.positions.zero_()
-        self.slots.fill_(self.garbage_block * self.pool.block_size)
-        self.block_tables.zero_()
-        self.block_tables[:, 0] = self.garbage_block
-        self.context_lens.fill_(1)
+    def _fill_padding(self, views, lo: int) -> None:
+        """Rows lo.. of the (host) views become padding rows."""
+        tokens, positions, slots, lens, tables = views
+        tokens[lo:] = 0
+        positions[lo:] = 0
+        slots[lo:] = self.garbage_block * self.pool.block_size
+        lens[lo:] = 1
+        tables[lo:] = 0
+        tables[lo:, 0] = self.garbage_block
+
+    def _reset_to_padding(self, B: int) -> None:
+        dev, host, _, hv = self._buffers(B)
+        self._fill_padding(hv, 0)
+        dev.copy_(host)
 
     def _forward(self, B: int) -> tuple[torch.Tensor, torch.Tensor]:
         from nanoserve_amd.kernels.sampling import argmax_rows
-        meta = DecodeMeta(self.token_idx[:B], self.block_tables[:B], self.context_lens[:B], all_rows=True)
+        tokens, positions, slots, lens, tables = self._buffers(B)[2]
+        meta = DecodeMeta(self.token_idx[:B], tables, lens, all_rows=True)
         seqs = [SeqInput(1, ctx_len=1, use_kernel=True)] * B
-        logits = self.model.forward_batch(self.tokens[:B], self.positions[:B], seqs, logits="all", paged=self.pool,
-                                          slot_mapping=self.slots[:B], decode_meta=meta)
+        logits = self.model.forward_batch(tokens, positions, seqs, logits="all", paged=self.pool,
+                                          slot_mapping=slots, decode_meta=meta)
         return logits, argmax_rows(logits)
 
     def _capture(self, B: int) -> None:
         # warm-up and capture run on padding inputs only, so they cannot overwrite real K/V
-        self._reset_to_padding()
+        self._reset_to_padding(B)
         side = _capture_stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -114,23 +128,17 @@ class DecodeGraphRunner:
         if B is None:
             raise ValueError(f"batch of {n} exceeds the largest graph bucket ({self.max_bucket})")
         W = self.max_blocks
-        g = self.garbage_block
-        pad = B - n
         for t in block_tables:
             if len(t) > W:
                 raise ValueError(f"block table of {len(t)} blocks exceeds the graph width {W} (max_seq_len)")
-        ht, hp, hs, hb, hl = self._h_tokens, self._h_positions, self._h_slots, self._h_tables, self._h_lens
-        ht[:B] = torch.tensor(tokens + [0] * pad, dtype=torch.long)
-        hp[:B] = torch.tensor(positions + [0] * pad, dtype=torch.long)
-        hs[:B] = torch.tensor(slots + [g * self.pool.block_size] * pad, dtype=torch.long)
-        hl[:B] = torch.tensor(context_lens + [1] * pad, dtype=torch.int32)
-        pad_row = [g] + [0] * (W - 1)
-        hb[:B] = torch.tensor([t + [0] * (W - len(t)) for t in block_tables] + [pad_row] * pad, dtype=torch.int32)
-        self.tokens[:B].copy_(ht[:B], non_blocking=True)
-        self.positions[:B].copy_(hp[:B], non_blocking=True)
-        self.slots[:B].copy_(hs[:B], non_blocking=True)
-        self.block_tables[:B].copy_(hb[:B], non_blocking=True)
-        self.context_lens[:B].copy_(hl[:B], non_blocking=True)
+        dev, host, _, (ht, hp, hs, hl, hb) = self._buffers(B)
+        ht[:n] = torch.tensor(tokens, dtype=torch.long)
+        hp[:n] = torch.tensor(positions, dtype=torch.long)
+        hs[:n] = torch.tensor(slots, dtype=torch.long)
+        hl[:n] = torch.tensor(context_lens, dtype=torch.int32)
+        hb[:n] = torch.tensor([t + [0] * (W - len(t)) for t in block_tables], dtype=torch.int32)
+        self._fill_padding((ht, hp, hs, hl, hb), n)
+        dev.copy_(host, non_blocking=True)
         return B
 
     @torch.inference_mode()
