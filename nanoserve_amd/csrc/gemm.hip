@@ -60,6 +60,7 @@ constexpr int G_STAGE = G_TN * G_NTB;
 constexpr int G_RED = 65;          // floats per tile row in the cross-wave reduction (64 + 1 pad)
 constexpr int G_MAX_M = 64;
 constexpr int G_NORM_COLS = 16;   // columns per row-sum partial of the RMSNorm statistics
+constexpr int G_NX_MAX_K = 4096;  // longest normalised input the 64-row kernel stages its norm weight for
 // The arrival counters sit at the start of every workspace, in a region no other data ever uses, so the
 // "all counters are zero between calls" invariant holds whatever shapes share the buffer.
 constexpr int G_MAX_TILES = 8191;
@@ -191,8 +192,24 @@ constexpr int g_items4() { return (16 * TM * 4 + G_WAVES * 64 - 1) / (G_WAVES * 
 // in flight, the compiler's wait counts for the prefetched slots are exact again.
 __device__ __forceinline__ void drain_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// RESNORM's residual fragments of this thread's epilogue items (row m, 8 columns), loaded at kernel start
+// with clamped addresses, so the epilogue waits for no round trip of its own.
 template <int TM, int EPI>
-__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSource& src, int t) {
+__device__ __forceinline__ void res_prefetch(const GemmArgs& a, int t, g_u32x4_t (&pre)[g_items8<4>()]) {
+  if constexpr (EPI == EPI_RESNORM) {
+#pragma unroll
+    for (int it = 0; it < g_items8<TM>(); ++it) {
+      const int idx = threadIdx.x + it * G_WAVES * 64;
+      const int m = min(idx >> 3, a.M - 1), n0 = min(t * 64 + 8 * (idx & 7), a.N - 8);
+      pre[it] = *reinterpret_cast<const g_u32x4_t*>(a.residual + int64_t(m) * a.N + n0);
+    }
+  }
+}
+
+// pre: RESNORM's residual fragments of this thread's items, loaded at kernel start (res_prefetch)
+template <int TM, int EPI>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSource& src, int t,
+                                              const g_u32x4_t (&pre)[g_items8<4>()]) {
   const int tid = threadIdx.x, M = a.M;
   if constexpr (EPI == EPI_STORE) {
 #pragma unroll
@@ -308,7 +325,11 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSourc
       if (live && n0 < N) {
         float o[8], rs[8], r[8];
         tile_values(src, m, 8 * cq, o);
-        load_bf16x8(a.residual + int64_t(m) * N + n0, rs);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          rs[2 * e] = __uint_as_float(pre[it][e] << 16);
+          rs[2 * e + 1] = __uint_as_float(pre[it][e] & 0xffff0000u);
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           r[e] = round_bf16(rs[e] + round_bf16(o[e]));
@@ -340,27 +361,30 @@ __device__ __forceinline__ float rms_norm_row_inv(const float* sumsq, int ptiles
   return rsqrtf(part / float(K) + eps);
 }
 
-// inv of rows 0 .. M-1 into s_inv (LDS), for a whole workgroup at once: thread (row, g) = (tid / 4, tid % 4)
-// adds the partials p = g, g + 4, g + 8, ... in increasing p, then the four combine as (g0 + g1) + (g2 + g3)
-// -- the same operations in the same order as rms_norm_row_inv, so the bits agree. All loads of a thread
-// are issued together (one round trip for K <= 2048). Every thread calls it; the caller synchronises before
-// reading s_inv.
-__device__ __forceinline__ void block_row_inv(const float* sumsq, int ptiles, int M, int K, float eps, float* s_inv) {
+// inv of rows 0 .. M-1 into s_inv (LDS), for a whole workgroup, in two steps, so that the loads go out
+// ahead of the kernel's weight stream and waiting for them never waits for it (vector loads complete in
+// issue order). Thread (row, g) = (tid / 4, tid % 4) of the first ceil(M / 16) waves adds the partials
+// p = g, g + 4, g + 8, ... in increasing p, then the four combine as (g0 + g1) + (g2 + g3) -- the same
+// operations in the same order as rms_norm_row_inv, so the bits agree. row_stats_issue loads the thread's
+// first RS_PRE partials (all of them for K <= 2048) with clamped, branch-free addresses; row_stats_finish
+// adds them (and, for longer rows, the rest) and writes s_inv; the caller synchronises before reading it.
+constexpr int RS_PRE = 32;
+__device__ __forceinline__ void row_stats_issue(const float* sumsq, int ptiles, int M, float (&v)[RS_PRE]) {
+  const int tid = threadIdx.x, m = min(tid >> 2, M - 1), g = tid & 3;
+#pragma unroll
+  for (int e = 0; e < RS_PRE; ++e) v[e] = sumsq[int64_t(min(g + 4 * e, ptiles - 1)) * G_MAX_M + m];
+}
+__device__ __forceinline__ void row_stats_finish(const float* sumsq, int ptiles, int M, int K, float eps,
+                                                 const float (&v)[RS_PRE], float* s_inv) {
   const int tid = threadIdx.x, m = tid >> 2, g = tid & 3;
-  const bool live = m < M;
-  constexpr int B = 32;
   float part = 0.f;
-  for (int p0 = g; p0 < ptiles; p0 += 4 * B) {
-    float v[B];
 #pragma unroll
-    for (int e = 0; e < B; ++e) v[e] = live && p0 + 4 * e < ptiles ? sumsq[int64_t(p0 + 4 * e) * G_MAX_M + m] : 0.f;
-#pragma unroll
-    for (int e = 0; e < B; ++e)
-      if (p0 + 4 * e < ptiles) part += v[e];
-  }
+  for (int e = 0; e < RS_PRE; ++e)
+    if (g + 4 * e < ptiles) part += v[e];
+  for (int p = g + 4 * RS_PRE; p < ptiles; p += 4) part += sumsq[int64_t(p) * G_MAX_M + min(m, M - 1)];
   part += __shfl_xor(part, 1, 64);
   part += __shfl_xor(part, 2, 64);
-  if (live && g == 0) s_inv[m] = rsqrtf(part / float(K) + eps);
+  if (m < M && g == 0) s_inv[m] = rsqrtf(part / float(K) + eps);
 }
 
 // 8 bf16 of r (one X fragment) -> 8 bf16 of h = round(w * round(r * inv))
@@ -418,9 +442,25 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   // in flight, and a slot is refilled with chunk c + D as soon as its chunk has been staged. Refills past
   // the segment re-load its last chunk (an L2 hit), so every path issues the same load sequence and the
   // compiler's wait counts stay exact (vmcnt leaves the other slots' loads in flight).
+  // Epilogue operands and row statistics go out before the weight stream (waiting for them never waits
+  // for it); a normalised input's norm weight is staged through LDS once (a per-fragment load would cost a
+  // 1 KB wave access for 64 distinct bytes).
+  g_u32x4_t pre[g_items8<4>()];
+  res_prefetch<TM, EPI>(a, t, pre);
+  const bool stat_wave = wv < TM;   // threads 0 .. 64 TM - 1 hold the (row, group) pairs
+  const int ptiles = (K + G_NORM_COLS - 1) / G_NORM_COLS;
+  float rs[RS_PRE];
+  constexpr int NW_PER_THREAD = G_NX_MAX_K / 2 / (G_WAVES * 64);
+  uint32_t nw_word[NW_PER_THREAD];
+  if constexpr (NX) {
+    if (stat_wave) row_stats_issue(a.xsq, ptiles, a.M, rs);
+#pragma unroll
+    for (int j = 0; j < NW_PER_THREAD; ++j)
+      nw_word[j] = reinterpret_cast<const uint32_t*>(a.xnw)[min(tid + j * G_WAVES * 64, (K >> 1) - 1)];
+  }
   constexpr int D = (TM <= 2 && !NX) ? 3 : 2;
   g_u32x4_t wr[D][8], xf[D][2][TM];
-  g_u32x4_t xw[D][2];   // normalised input: norm-weight fragments of the lane's k range
+  __shared__ __align__(16) uint32_t s_nw[NX ? G_NX_MAX_K / 2 : 4];
   const int clast = c1 - 1;
   auto load_w = [&](auto qc, int c) __attribute__((always_inline)) {
     constexpr int q = decltype(qc)::value;
@@ -436,7 +476,6 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
       const int k = min(kc + 32 * (2 * wv + h), K - 32);
 #pragma unroll
       for (int i = 0; i < TM; ++i) xf[q][h][i] = *reinterpret_cast<const g_u32x4_t*>(xrow[i] + k);
-      if constexpr (NX) xw[q][h] = *reinterpret_cast<const g_u32x4_t*>(a.xnw + k + 8 * r4);
     }
   };
   int buf = 0;
@@ -452,6 +491,8 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
     for (int h = 0; h < 2; ++h) {
       const int kstep = 2 * wv + h;
       if (kc + 32 * kstep < K) {   // uniform
+        g_u32x4_t w8;
+        if constexpr (NX) w8 = *reinterpret_cast<const g_u32x4_t*>(s_nw + ((kc + 32 * kstep + 8 * r4) >> 1));
         g_bf16x8_t bfr[G_TN];
 #pragma unroll
         for (int j = 0; j < G_TN; ++j)
@@ -459,7 +500,7 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
           g_u32x4_t xa = xf[q][h][i];
-          if constexpr (NX) xa = norm_fragment(xa, xw[q][h], xinv[i]);
+          if constexpr (NX) xa = norm_fragment(xa, w8, xinv[i]);
 #pragma unroll
           for (int j = 0; j < G_TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, xa), bfr[j], acc[i][j], 0,
@@ -481,9 +522,12 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
     load_w(Q2{}, min(c0 + 2, clast));
     load_x(Q2{}, min(c0 + 2, clast));
   }
-  if constexpr (NX) {   // the row statistics' round trip overlaps the first chunks' loads
+  if constexpr (NX) {   // the statistics' and norm weight's round trip overlaps the first chunks' loads
     __shared__ float s_inv[G_MAX_M];
-    block_row_inv(a.xsq, (K + G_NORM_COLS - 1) / G_NORM_COLS, a.M, K, a.xeps, s_inv);
+    if (stat_wave) row_stats_finish(a.xsq, ptiles, a.M, K, a.xeps, rs, s_inv);
+#pragma unroll
+    for (int j = 0; j < NW_PER_THREAD; ++j)
+      if (tid + j * G_WAVES * 64 < (K >> 1)) s_nw[tid + j * G_WAVES * 64] = nw_word[j];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < TM; ++i) xinv[i] = s_inv[min(16 * i + c16, a.M - 1)];
@@ -510,7 +554,7 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   __syncthreads();
   TileSource src{red, R, false, ks, nullptr};
   if (ks == 1) {
-    tile_epilogue<TM, EPI>(a, src, t);
+    tile_epilogue<TM, EPI>(a, src, t, pre);
     return;
   }
   // sliced tile: publish this slice's partial; the last slice to arrive sums all of them in slice order
@@ -540,7 +584,7 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   acquire_published();
   src.from_parts = true;
   src.part = tile_part;
-  tile_epilogue<TM, EPI>(a, src, t);
+  tile_epilogue<TM, EPI>(a, src, t, pre);
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -584,57 +628,87 @@ __global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a)
   const int c16 = lane & 15, r4 = lane >> 4;
   const int rowb = 2 * K;   // bytes of a weight row = LDS pitch
 
-  // weight row wv of the tile, 16 bytes per lane per 1 KB piece
-  g_u32x4_t wr[T16_MAX_K * 2 / 1024];
-  {
-    const unsigned char* src = reinterpret_cast<const unsigned char*>(a.w + int64_t(t16_row<EPI>(a, t, wv)) * K);
-#pragma unroll
-    for (int j = 0; j < T16_MAX_K * 2 / 1024; ++j)
-      if (j * 1024 + lane * 16 < rowb) wr[j] = *reinterpret_cast<const g_u32x4_t*>(src + j * 1024 + lane * 16);
-  }
-  // X fragments (and norm weights) of this wave's k-steps
-  const int nks = K >> 5;
-  const int ks0 = wv * nks / T16_WAVES, ks1 = (wv + 1) * nks / T16_WAVES;
-  g_u32x4_t xr[T16_KSW][TM];
-  g_u32x4_t xw[T16_KSW];
-#pragma unroll
-  for (int s = 0; s < T16_KSW; ++s) {
-    const int k = 32 * max(min(ks0 + s, ks1 - 1), 0) + 8 * r4;   // past the wave's range: an in-bounds re-read
-#pragma unroll
-    for (int i = 0; i < TM; ++i) xr[s][i] = *reinterpret_cast<const g_u32x4_t*>(a.x + int64_t(min(16 * i + c16, M - 1)) * K + k);
-    if constexpr (NX) xw[s] = *reinterpret_cast<const g_u32x4_t*>(a.xnw + k);
-  }
-  __shared__ float s_inv[G_MAX_M];
-  if constexpr (NX) block_row_inv(a.xsq, (K + G_NORM_COLS - 1) / G_NORM_COLS, M, K, a.xeps, s_inv);
-  // epilogue operands of this thread's output(s): thread (m, n) for STORE / RESNORM, (m, j) for the pairs
+  // Epilogue operands (raw bits) and the row statistics go out first, with branch-free addresses (a
+  // missing operand reads a harmless in-bounds word instead): they return before the weights, waiting for
+  // them never waits for the weight stream, and nothing is converted until the epilogue.
   constexpr int PAIR = (EPI == EPI_SILU || EPI == EPI_ROPE) ? 1 : 0;
   const int em = PAIR ? (tid >> 3) : (tid >> 4);
   const int en = PAIR ? (tid & 7) : (tid & 15);
   const bool elive = em < M && tid < TM * 16 * (PAIR ? 8 : 16);
   const int emc = min(em, M - 1);
-  float e_bias0 = 0.f, e_bias1 = 0.f, e_res = 0.f, e_cl = 0.f, e_ch = 0.f, e_sl = 0.f, e_sh = 0.f;
+  bf16_t r_b0 = 0, r_b1 = 0, r_cl = 0, r_ch = 0, r_sl = 0, r_sh = 0, r_res = 0;
   int64_t e_slot = 0;
-  int col = 0;
+  const bf16_t* bias_src = a.bias != nullptr ? a.bias : a.w;
   if constexpr (EPI == EPI_STORE) {
-    col = min(16 * t + en, a.N - 1);
-    if (a.bias != nullptr) e_bias0 = bf16_to_f32(a.bias[col]);
+    r_b0 = bias_src[min(16 * t + en, a.N - 1)];
   } else if constexpr (EPI == EPI_RESNORM) {
-    col = min(16 * t + en, a.N - 1);
-    e_res = bf16_to_f32(a.residual[int64_t(emc) * a.N + col]);
+    r_res = a.residual[int64_t(emc) * a.N + min(16 * t + en, a.N - 1)];
   } else if constexpr (EPI == EPI_ROPE) {
     const int tph = a.hd >> 4, head = t / tph, f = t - head * tph, hh = a.hd >> 1;
     const int d = 8 * f + en;
-    if (a.bias != nullptr) {
-      e_bias0 = bf16_to_f32(a.bias[head * a.hd + d]);
-      e_bias1 = bf16_to_f32(a.bias[head * a.hd + hh + d]);
+    r_b0 = bias_src[head * a.hd + d];
+    r_b1 = bias_src[head * a.hd + hh + d];
+    r_cl = a.cosb[int64_t(emc) * a.hd + d];
+    r_ch = a.cosb[int64_t(emc) * a.hd + hh + d];
+    r_sl = a.sinb[int64_t(emc) * a.hd + d];
+    r_sh = a.sinb[int64_t(emc) * a.hd + hh + d];
+    e_slot = (a.slots != nullptr ? a.slots : reinterpret_cast<const int64_t*>(a.w))[emc];
+  }
+  const bool stat_wave = wv < TM;   // threads 0 .. 64 TM - 1 hold the (row, group) pairs
+  const int ptiles = (K + G_NORM_COLS - 1) / G_NORM_COLS;
+  float rs[RS_PRE];
+  uint32_t nw_word = 0;
+  if constexpr (NX) {
+    if (stat_wave) row_stats_issue(a.xsq, ptiles, M, rs);
+    // the norm weight, one 4-byte word per thread (K <= 2048), staged through LDS: a per-fragment load would
+    // cost a 1 KB wave access for 64 distinct bytes
+    nw_word = reinterpret_cast<const uint32_t*>(a.xnw)[min(tid, (K >> 1) - 1)];
+  }
+  // X fragments of this wave's k-steps and weight row wv of the tile (16 bytes per lane per 1 KB piece). A
+  // normalised input's fragments go out first: they arrive first and are normalised while the weight rows
+  // are still in flight; a plain input's go out after the weights, which the workgroup waits for first.
+  const int nks = K >> 5;
+  const int ks0 = wv * nks / T16_WAVES, ks1 = (wv + 1) * nks / T16_WAVES;
+  g_u32x4_t xr[T16_KSW][TM];
+  g_u32x4_t wr[T16_MAX_K * 2 / 1024];
+  auto load_x = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < T16_KSW; ++s) {
+      const int k = 32 * max(min(ks0 + s, ks1 - 1), 0) + 8 * r4;   // past the wave's range: an in-bounds re-read
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        xr[s][i] = *reinterpret_cast<const g_u32x4_t*>(a.x + int64_t(min(16 * i + c16, M - 1)) * K + k);
     }
-    if (head < a.nh + a.nkv) {
-      e_cl = bf16_to_f32(a.cosb[int64_t(emc) * a.hd + d]);
-      e_ch = bf16_to_f32(a.cosb[int64_t(emc) * a.hd + hh + d]);
-      e_sl = bf16_to_f32(a.sinb[int64_t(emc) * a.hd + d]);
-      e_sh = bf16_to_f32(a.sinb[int64_t(emc) * a.hd + hh + d]);
-    }
-    if (head >= a.nh && a.kc != nullptr) e_slot = a.slots[emc];
+  };
+  auto load_w = [&]() __attribute__((always_inline)) {
+    const unsigned char* src = reinterpret_cast<const unsigned char*>(a.w + int64_t(t16_row<EPI>(a, t, wv)) * K);
+#pragma unroll
+    for (int j = 0; j < T16_MAX_K * 2 / 1024; ++j)
+      if (j * 1024 + lane * 16 < rowb) wr[j] = *reinterpret_cast<const g_u32x4_t*>(src + j * 1024 + lane * 16);
+  };
+  if constexpr (NX) {
+    load_x();
+    load_w();
+  } else {
+    load_w();
+    load_x();
+  }
+  if constexpr (NX) {
+    __shared__ float s_inv[G_MAX_M];
+    __shared__ __align__(16) uint32_t s_nw[T16_MAX_K / 2];
+    if (stat_wave) row_stats_finish(a.xsq, ptiles, M, K, a.xeps, rs, s_inv);
+    if (tid < (K >> 1)) s_nw[tid] = nw_word;
+    __syncthreads();   // every row's inv and the norm weight are in LDS
+    float xinv[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xinv[i] = s_inv[min(16 * i + c16, M - 1)];
+#pragma unroll
+    for (int s = 0; s < T16_KSW; ++s)
+      if (ks0 + s < ks1) {
+        const g_u32x4_t w8 = *reinterpret_cast<const g_u32x4_t*>(s_nw + 16 * (ks0 + s) + 4 * r4);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xr[s][i] = norm_fragment(xr[s][i], w8, xinv[i]);
+      }
   }
 
   // weight row -> LDS: chunk q of row wv at (q & ~15) | ((q ^ wv) & 15)
@@ -644,10 +718,6 @@ __global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a)
     if (q * 16 < rowb) *reinterpret_cast<g_u32x4_t*>(lds + wv * rowb + (((q & ~15) | ((q ^ wv) & 15)) << 4)) = wr[j];
   }
   __syncthreads();
-  float xinv[TM];
-  if constexpr (NX)
-#pragma unroll
-    for (int i = 0; i < TM; ++i) xinv[i] = s_inv[min(16 * i + c16, M - 1)];
   g_float4_t acc[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) acc[i] = g_float4_t{0.f, 0.f, 0.f, 0.f};
@@ -659,11 +729,8 @@ __global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a)
       const g_bf16x8_t b = __builtin_bit_cast(
           g_bf16x8_t, *reinterpret_cast<const g_u32x4_t*>(lds + c16 * rowb + (((q & ~15) | ((q ^ c16) & 15)) << 4)));
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        g_u32x4_t xa = xr[s][i];
-        if constexpr (NX) xa = norm_fragment(xa, xw[s], xinv[i]);
-        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, xa), b, acc[i], 0, 0, 0);
-      }
+      for (int i = 0; i < TM; ++i)
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, xr[s][i]), b, acc[i], 0, 0, 0);
     }
   }
   __syncthreads();   // every wave is done with the weight tile: the LDS now takes the partial tiles
@@ -679,12 +746,13 @@ __global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a)
     for (int w = 0; w < T16_WAVES; ++w) v += red[(w * TM * 16 + m) * 16 + n];
     return v;
   };
+  const float e_bias0 = a.bias != nullptr ? bf16_to_f32(r_b0) : 0.f, e_bias1 = a.bias != nullptr ? bf16_to_f32(r_b1) : 0.f;
   if constexpr (EPI == EPI_STORE) {
     if (elive && 16 * t + en < a.N) a.y[int64_t(em) * a.N + 16 * t + en] = f32_to_bf16(value(em, en) + e_bias0);
   } else if constexpr (EPI == EPI_RESNORM) {
     float ss = 0.f;
     if (tid < TM * 256) {
-      const float r = round_bf16(e_res + round_bf16(value(em, en)));
+      const float r = round_bf16(bf16_to_f32(r_res) + round_bf16(value(em, en)));
       if (elive && 16 * t + en < a.N) a.res_out[int64_t(em) * a.N + 16 * t + en] = f32_to_bf16(r);
       ss = 16 * t + en < a.N ? r * r : 0.f;
     }
@@ -707,6 +775,7 @@ __global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a)
       const float xl = round_bf16(value(em, en) + e_bias0), xh = round_bf16(value(em, en + 8) + e_bias1);
       float lo = xl, hi = xh;
       if (head < a.nh + a.nkv) {
+        const float e_cl = bf16_to_f32(r_cl), e_ch = bf16_to_f32(r_ch), e_sl = bf16_to_f32(r_sl), e_sh = bf16_to_f32(r_sh);
         lo = round_bf16(xl * e_cl) - round_bf16(xh * e_sl);
         hi = round_bf16(xh * e_ch) + round_bf16(xl * e_sh);
       }
@@ -874,8 +943,9 @@ static int launch(const GemmArgs& a, hipStream_t st) {
 // Optional normalised input (x holds r; see the file comment): sumsq NULL = plain x.
 static int bind_xnorm(GemmArgs& a, const float* x_sumsq, const void* x_norm_w, float x_eps) {
   NS_REQUIRE(x_sumsq == nullptr || (x_norm_w != nullptr && reinterpret_cast<uintptr_t>(x_norm_w) % 16 == 0 &&
-                                     a.K % 8 == 0),
-             "skinny gemm: a normalised input needs a 16-byte aligned norm weight and K %% 8 == 0");
+                                     a.K % 8 == 0 && a.K <= G_NX_MAX_K),
+             "skinny gemm: a normalised input needs a 16-byte aligned norm weight, K %% 8 == 0 and K <= %d (K=%d)",
+             G_NX_MAX_K, a.K);
   a.xsq = x_sumsq;
   a.xnw = static_cast<const bf16_t*>(x_norm_w);
   a.xeps = x_eps;

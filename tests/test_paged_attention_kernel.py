@@ -5,8 +5,9 @@ Qwen2.5-0.5B / 1.5B / 3B, context lengths {1, 15, 16, 17, 100, 333, 700}, fragme
 block tables; fp32 max|diff| <= 1e-5; bf16 max|diff| <= 1e-2 against the fp32 oracle on the same bf16
 inputs; ctx=1 returns that token's value for every head of the group. Inputs are drawn on the CPU with a
 seeded generator so the oracle and the GPU see identical values. Added: the BASELINE config-2 shape (B=32,
-ctx U[512, 4096], 64k-block pool), split-K counter reset across calls, NaN poison in padding table entries
-and past-ctx tokens, and hipGraph replay against eager calls.
+ctx U[512, 4096], 64k-block pool), split-K state carried across calls (counters back at zero, merge words
+of earlier calls never taken), NaN poison in padding table entries and past-ctx tokens, and hipGraph replay
+against eager calls.
 """
 import math
 
@@ -93,6 +94,32 @@ def test_config2_shape_split_k(hiplib, n_heads, n_kv, hd):
     print(f"config-2 shape ({n_heads},{n_kv},{hd}) max|diff| = {err:.2e}")
     assert err <= 1e-2
     assert torch.equal(out1, out2)
+
+
+def test_merge_words_of_earlier_calls_are_never_taken(hiplib):
+    """Several calls of one shape share the split-K workspace while each row's partition count changes
+    (1 .. 8 partitions of 32 pages, table width 256): a merger must fold only this call's partials, never
+    words an earlier call left in the same slots. Every call is checked against the oracle and against a
+    second call with the same inputs."""
+    from nanoserve_amd.kernels.paged_attention import paged_attention_decode
+    B, W, nh, nkv, hd = 8, 256, 14, 2, 64
+    g = cpu_gen(21)
+    q, k, v, _, _ = make_case(nh, nkv, hd, [4096] * B, torch.bfloat16, seed=21, extra_blocks=8, width=W)
+    dk, dv = k.cuda(), v.cuda()
+    schedule = [[4096, 600, 1, 2000, 513, 4000, 100, 3000],     # partitions 8 2 1 4 2 8 1 6
+                [300, 4096, 2048, 1, 512, 4096, 700, 1000],     #            1 8 4 1 1 8 2 2
+                [4096, 513, 2049, 3000, 4096, 1, 4096, 4096]]   #            8 2 5 6 8 1 8 8
+    for it, ctx in enumerate(schedule + [torch.randint(1, W * 16 + 1, (B,), generator=g).tolist()]):
+        qq = torch.randn(B, nh, hd, generator=g).to(torch.bfloat16)
+        perm = torch.randperm(k.shape[0], generator=g)[:B * W].view(B, W).int()
+        lens = torch.tensor(ctx, dtype=torch.int32)
+        out1 = paged_attention_decode(qq.cuda(), dk, dv, perm.cuda(), lens.cuda(), hd ** -0.5).cpu()
+        out2 = paged_attention_decode(qq.cuda(), dk, dv, perm.cuda(), lens.cuda(), hd ** -0.5).cpu()
+        ref = paged_attention_reference(qq.float(), k.float(), v.float(), perm, lens, hd ** -0.5)
+        err = (out1.float() - ref).abs().max().item()
+        print(f"call {it}: ctx {ctx} max|diff| {err:.2e}")
+        assert err <= 1e-2
+        assert torch.equal(out1, out2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
