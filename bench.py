@@ -21,6 +21,9 @@ new K/V and the logits) over the measured step time.
 mixed_step: BASELINE config 4 (one 1536-token chunk on 512 cached tokens + 16 decode rows, eager) --
 step time and algorithmic TFLOP/s against the bf16 MFMA peak, and the chunked-prefill attention kernel
 alone at that shape (FLOPs = sum_j (512 + j + 1) * n_heads * hd * 4 per layer).
+fused_ops: the standalone RMSNorm+residual, SiLU*mul and RoPE+KV-write kernels at 32 and 1552 rows of the
+1.5B shapes: algorithmic HBM bytes per launch over the HIP-event time (`--ops-only` runs these and the
+chunked-prefill kernel alone, for rocprofv3 --pmc passes).
 prefix_sharing: BASELINE config 5 (3B shape, a 1024-token prefix shared by 32 requests through the prefix
 cache, 211-token suffixes): decode tokens/s and the step's HBM roofline, logical (a shared block counted
 once per row that reads it) and unique bytes.
@@ -289,6 +292,77 @@ def mixed_step_bench(model, cfg, reps: int = 5) -> dict:
                                   "flop_per_launch": int(pf_flops), "us_per_launch": round(pf_ms * 1e3, 2)}}
 
 
+def fused_ops_bench(reps: int = 100) -> dict:
+    """The standalone token-wise kernels -- RMSNorm with the residual add, SiLU*mul, RoPE with the paged KV
+    write (the reference's fused.py entry points) -- on the 1.5B shapes at the config-3 decode row count (32)
+    and the config-4 step's row count (1552). Algorithmic HBM bytes per launch (every input read once, every
+    output written once) over the HIP-event time of `reps` back-to-back launches cycling over 8 input sets
+    (the 1552-row sets total 0.2-0.9 GB, beyond the 256 MB Infinity Cache). In the decode step these ops run
+    inside the GEMM epilogues; these are the drop-in entry points' own numbers."""
+    from nanoserve_amd.kernels.fused import rms_norm, rope_qkv, silu_mul
+    dev, bf = "cuda", torch.bfloat16
+    H, I, NH, NKV, HD, R = 1536, 8960, 12, 2, 128, 8
+    g = torch.Generator().manual_seed(3)
+    out = {}
+    for rows in (32, 1552):
+        xs = [torch.randn(rows, H, generator=g).to(dev, bf) for _ in range(R)]
+        rs = [torch.randn(rows, H, generator=g).to(dev, bf) for _ in range(R)]
+        w = torch.ones(H, device=dev, dtype=bf)
+        gus = [torch.randn(rows, 2 * I, generator=g).to(dev, bf) for _ in range(R)]
+        qkvs = [torch.randn(rows, (NH + 2 * NKV) * HD, generator=g).to(dev, bf) for _ in range(R)]
+        cos = torch.randn(rows, HD, generator=g).to(dev, bf)
+        sin = torch.randn(rows, HD, generator=g).to(dev, bf)
+        kc = torch.zeros(rows // 16 + 8, 16, NKV, HD, device=dev, dtype=bf)
+        vc = torch.zeros_like(kc)
+        slots = torch.randperm(kc.shape[0] * 16, generator=g)[:rows].to(dev)
+        it = iter(range(10 ** 9))
+        cases = {
+            "rms_norm_residual": (lambda: rms_norm(xs[next(it) % R], w, 1e-6, residual=rs[0]),
+                                  (4 * rows * H + H) * 2),
+            "silu_mul": (lambda: silu_mul(gus[next(it) % R]), 3 * rows * I * 2),
+            "rope_qkv_kv_write": (lambda: rope_qkv(qkvs[next(it) % R], cos, sin, NH, NKV, HD, kc, vc, slots),
+                                  2 * rows * (NH + 2 * NKV) * HD * 2 + 2 * rows * HD * 2 + 2 * rows * NKV * HD * 2
+                                  + 8 * rows),
+        }
+        for name, (fn, nbytes) in cases.items():
+            for _ in range(2 * R):
+                fn()
+            us = gated_region_time(fn, reps) / reps * 1e3
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out[f"{name}_{rows}rows"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                         "bytes_per_launch": int(nbytes), "us_per_launch": round(us, 2)}
+        del xs, rs, gus, qkvs
+    return out
+
+
+def prefill_attention_bench(reps: int = 50) -> dict:
+    """The chunked-prefill attention kernel alone at BASELINE config 4's shape with synthetic pages: one
+    sequence, a 1536-token chunk on 512 cached tokens (2048 keys), 12 q / 2 kv heads, hd 128, its 128 blocks
+    scattered by a random permutation over a 4096-block pool. FLOPs = sum_j (512 + j + 1) * n_heads * hd * 4
+    (QK^T and PV, causal) against the bf16 MFMA peak."""
+    from nanoserve_amd.kernels.paged_attention import paged_attention_prefill, prefill_seq_info
+    dev, bf = "cuda", torch.bfloat16
+    T, C, NH, NKV, HD, NB = 1536, 512, 12, 2, 128, 4096
+    g = torch.Generator().manual_seed(4)
+    k = torch.randn(NB, 16, NKV, HD, generator=g).to(dev, bf)
+    v = torch.randn(NB, 16, NKV, HD, generator=g).to(dev, bf)
+    q = torch.randn(T, NH, HD, generator=g).to(dev, bf)
+    tab = torch.randperm(NB, generator=g)[:(T + C) // 16].int().view(1, -1).to(dev)
+    info = prefill_seq_info([0], [T], [C], dev)
+    out = torch.empty_like(q)
+
+    def pf():
+        paged_attention_prefill(q, k, v, tab, info, T, C + T, HD ** -0.5, out=out)
+    for _ in range(3):
+        pf()
+    us = gated_region_time(pf, reps) / reps * 1e3
+    flops = sum(C + j + 1 for j in range(T)) * NH * HD * 4
+    tf = flops / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_launch": int(flops), "us_per_launch": round(us, 2)}
+
+
 def copy_calibration(nbytes: int = 512 << 20, reps: int = 4) -> float:
     """A plain device copy of known size (nbytes read + nbytes written per launch): under rocprofv3 --pmc its
     FETCH_SIZE / WRITE_SIZE per dispatch give the scale from counter units to bytes. Returns GB/s."""
@@ -353,6 +427,9 @@ def main() -> int:
     ap.add_argument("--no-prefix-sharing", action="store_true", help="skip the config-5 prefix-sharing decode run")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the paged-attention roofline and the copy calibration (for rocprofv3 --pmc passes)")
+    ap.add_argument("--ops-only", action="store_true",
+                    help="only the fused token-wise ops, the chunked-prefill kernel alone and the copy calibration "
+                         "(for rocprofv3 --pmc passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (data-parallel replicas would "
@@ -364,6 +441,13 @@ def main() -> int:
         log(f"paged attention: {roof['us_per_launch']} us/call, {roof['achieved']} GB/s")
         log(f"copy calibration: {copy_calibration():.0f} GB/s")
         print(json.dumps({"roofline": roof}), flush=True)
+        return 0
+    if args.ops_only:
+        ops = fused_ops_bench()
+        pfa = prefill_attention_bench()
+        log(f"prefill attention alone: {pfa['us_per_launch']} us/launch, {pfa['achieved']} TFLOP/s")
+        log(f"copy calibration: {copy_calibration():.0f} GB/s")
+        print(json.dumps({"fused_ops": ops, "prefill_attention": pfa}), flush=True)
         return 0
     from nanoserve_amd.model import QWEN25_1_5B, QWEN25_3B, Qwen2Model, random_state_dict
 
@@ -389,6 +473,8 @@ def main() -> int:
     log("paged-attention roofline (config 2 shape)")
     roof = paged_attention_roofline()
     log(f"paged attention: {roof['us_per_launch']} us/call, {roof['achieved']} GB/s")
+    log("fused token-wise ops alone (32 and 1552 rows)")
+    ops = fused_ops_bench()
 
     prefix = None
     if not args.no_prefix_sharing:
@@ -419,6 +505,7 @@ def main() -> int:
                           "frac": round(step_gbs / PEAK_HBM_GBS, 4), "bytes_per_step": int(step_bytes),
                           "roofline_tok_s": round(B / (step_bytes / (PEAK_HBM_GBS * 1e9)), 1)},
         "mixed_step": mixed,
+        "fused_ops": ops,
         "prefix_sharing": prefix,
         "cpu_baseline": cpu,
     }

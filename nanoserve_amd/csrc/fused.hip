@@ -72,6 +72,78 @@ __global__ __launch_bounds__(RMS_THREADS) void rms_norm_kernel(const T* __restri
   }
 }
 
+// bf16 rows with n % 8 == 0 and 16-byte aligned operands: one wave per row, 8 consecutive elements (16 bytes)
+// per lane per pass, every pass's loads issued before any arithmetic. The sum of squares is the lane's
+// elements in pass order, then a butterfly over the wave. Same roundings as rms_norm_kernel.
+constexpr int RMSV_MAX_PASS = 8;   // n <= 8 * 512
+typedef __attribute__((ext_vector_type(4))) unsigned int f_u32x4_t;
+
+__device__ __forceinline__ void unpack8(const f_u32x4_t& u, float (&f)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(u[e] << 16);
+    f[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ f_u32x4_t pack8(const float (&f)[8]) {
+  f_u32x4_t u;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) u[e] = uint32_t(f32_to_bf16(f[2 * e])) | (uint32_t(f32_to_bf16(f[2 * e + 1])) << 16);
+  return u;
+}
+
+__global__ __launch_bounds__(256) void rms_norm_bf16_rows_kernel(const bf16_t* __restrict__ x,
+                                                                 const bf16_t* __restrict__ res,
+                                                                 const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
+                                                                 bf16_t* __restrict__ res_out, int64_t rows, int n,
+                                                                 float eps) {
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;   // wave-uniform, and nothing below synchronises the workgroup
+  const int lane = threadIdx.x & 63;
+  const bf16_t* xr = x + row * n;
+  f_u32x4_t xv[RMSV_MAX_PASS], rv[RMSV_MAX_PASS], wv[RMSV_MAX_PASS];
+#pragma unroll
+  for (int p = 0; p < RMSV_MAX_PASS; ++p) {
+    const int c = p * 512 + lane * 8;
+    if (c < n) {
+      xv[p] = *reinterpret_cast<const f_u32x4_t*>(xr + c);
+      if (res != nullptr) rv[p] = *reinterpret_cast<const f_u32x4_t*>(res + row * n + c);
+      wv[p] = *reinterpret_cast<const f_u32x4_t*>(w + c);
+    }
+  }
+  float v[RMSV_MAX_PASS][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < RMSV_MAX_PASS; ++p) {
+    const int c = p * 512 + lane * 8;
+    if (c < n) {
+      unpack8(xv[p], v[p]);
+      if (res != nullptr) {
+        float r[8];
+        unpack8(rv[p], r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[p][e] = round_bf16(r[e] + v[p][e]);   // residual + x, rounded
+        *reinterpret_cast<f_u32x4_t*>(res_out + row * n + c) = pack8(v[p]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[p][e] * v[p][e];
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / float(n) + eps);
+#pragma unroll
+  for (int p = 0; p < RMSV_MAX_PASS; ++p) {
+    const int c = p * 512 + lane * 8;
+    if (c < n) {
+      float wf[8], o[8];
+      unpack8(wv[p], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = wf[e] * round_bf16(v[p][e] * inv);   // cast back before the weight
+      *reinterpret_cast<f_u32x4_t*>(out + row * n + c) = pack8(o);
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------ SiLU*mul
 // Elementwise over [rows, n] outputs; each thread produces 8 consecutive outputs when n % 8 == 0.
 template <typename T>
@@ -172,6 +244,64 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(const T* __restrict__ qkv
   }
 }
 
+// bf16 with head_dim % 16 == 0 and 16-byte aligned operands: one workgroup per token, a thread's item is 8 dims
+// of a rotated head's low half with their rotate-half partners (16-byte loads and stores), or 8 dims of a
+// value head -- one pass for up to 256 items (the 1.5B and 3B shapes have 144 and 176). Same roundings as
+// rope_qkv_kernel.
+__global__ __launch_bounds__(256) void rope_qkv_bf16x8_kernel(const bf16_t* __restrict__ qkv,
+                                                              const bf16_t* __restrict__ cosb,
+                                                              const bf16_t* __restrict__ sinb, bf16_t* __restrict__ q,
+                                                              bf16_t* __restrict__ k, bf16_t* __restrict__ v,
+                                                              bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
+                                                              const int64_t* __restrict__ slots, int nh, int nkv,
+                                                              int hd) {
+  const int64_t t = blockIdx.x;
+  const int half = hd >> 1, per_head = half >> 3;
+  const bf16_t* row = qkv + t * int64_t((nh + 2 * nkv) * hd);
+  const bf16_t* cr = cosb + t * hd;
+  const bf16_t* sr = sinb + t * hd;
+  const int64_t slot = kc != nullptr ? slots[t] : 0;
+  const int n_rot = (nh + nkv) * per_head, n_v = nkv * (hd >> 3);
+  for (int i = threadIdx.x; i < n_rot + n_v; i += 256) {
+    if (i < n_rot) {
+      const int head = i / per_head, d0 = (i - head * per_head) * 8;
+      float xl[8], xh[8], cl[8], ch[8], sl[8], sh[8], lo[8], hi[8];
+      unpack8(*reinterpret_cast<const f_u32x4_t*>(row + head * hd + d0), xl);
+      unpack8(*reinterpret_cast<const f_u32x4_t*>(row + head * hd + half + d0), xh);
+      unpack8(*reinterpret_cast<const f_u32x4_t*>(cr + d0), cl);
+      unpack8(*reinterpret_cast<const f_u32x4_t*>(cr + half + d0), ch);
+      unpack8(*reinterpret_cast<const f_u32x4_t*>(sr + d0), sl);
+      unpack8(*reinterpret_cast<const f_u32x4_t*>(sr + half + d0), sh);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        lo[e] = round_bf16(xl[e] * cl[e]) - round_bf16(xh[e] * sl[e]);
+        hi[e] = round_bf16(xh[e] * ch[e]) + round_bf16(xl[e] * sh[e]);
+      }
+      const f_u32x4_t plo = pack8(lo), phi = pack8(hi);
+      bf16_t* dst;
+      bf16_t* cd = nullptr;
+      if (head < nh) {
+        dst = q + (t * nh + head) * hd;
+      } else {
+        const int kh = head - nh;
+        dst = k + (t * nkv + kh) * hd;
+        if (kc != nullptr) cd = kc + (slot * nkv + kh) * hd;
+      }
+      *reinterpret_cast<f_u32x4_t*>(dst + d0) = plo;
+      *reinterpret_cast<f_u32x4_t*>(dst + half + d0) = phi;
+      if (cd != nullptr) {
+        *reinterpret_cast<f_u32x4_t*>(cd + d0) = plo;
+        *reinterpret_cast<f_u32x4_t*>(cd + half + d0) = phi;
+      }
+    } else {
+      const int c = (i - n_rot) * 8;   // element of the row's value heads
+      const f_u32x4_t val = *reinterpret_cast<const f_u32x4_t*>(row + (nh + nkv) * hd + c);
+      *reinterpret_cast<f_u32x4_t*>(v + t * (nkv * hd) + c) = val;
+      if (vc != nullptr) *reinterpret_cast<f_u32x4_t*>(vc + slot * (nkv * hd) + c) = val;
+    }
+  }
+}
+
 // ------------------------------------------------------------------------- embedding + RoPE tables
 // The first ops of a forward step in one launch (nanoserve/model.py:337-342 F.embedding and :212-217
 // rope): x[i] = embed[token_ids[i]]; cos/sin[i] = cat(f, f).cos()/.sin() rounded to the dtype with
@@ -237,7 +367,16 @@ extern "C" int ns_rms_norm(const void* x, const void* residual, const void* weig
   NS_REQUIRE(rows >= 0 && rows < (int64_t(1) << 31), "rms_norm: rows %lld out of range", (long long)rows);
   if (rows == 0) return NS_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == NS_DTYPE_BF16)
+  const bool vec = dtype == NS_DTYPE_BF16 && n % 8 == 0 && n <= RMSV_MAX_PASS * 512 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
+                     reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(out) |
+                     reinterpret_cast<uintptr_t>(res_out)) % 16) == 0;
+  if (vec)
+    hipLaunchKernelGGL(rms_norm_bf16_rows_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, s,
+                       static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(residual),
+                       static_cast<const bf16_t*>(weight), static_cast<bf16_t*>(out), static_cast<bf16_t*>(res_out),
+                       rows, n, eps);
+  else if (dtype == NS_DTYPE_BF16)
     hipLaunchKernelGGL(rms_norm_kernel<bf16_t>, dim3(unsigned(rows)), dim3(RMS_THREADS), 0, s,
                        static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(residual),
                        static_cast<const bf16_t*>(weight), static_cast<bf16_t*>(out), static_cast<bf16_t*>(res_out),
@@ -283,7 +422,18 @@ extern "C" int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, vo
   NS_REQUIRE(n_tok >= 0 && n_tok < (int64_t(1) << 31), "rope_qkv: n_tok %lld out of range", (long long)n_tok);
   if (n_tok == 0) return NS_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == NS_DTYPE_BF16)
+  const bool vec = dtype == NS_DTYPE_BF16 && head_dim % 16 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(cos) |
+                     reinterpret_cast<uintptr_t>(sin) | reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                     reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(k_cache) |
+                     reinterpret_cast<uintptr_t>(v_cache)) % 16) == 0;
+  if (vec)
+    hipLaunchKernelGGL(rope_qkv_bf16x8_kernel, dim3(unsigned(n_tok)), dim3(256), 0, s,
+                       static_cast<const bf16_t*>(qkv), static_cast<const bf16_t*>(cos),
+                       static_cast<const bf16_t*>(sin), static_cast<bf16_t*>(q), static_cast<bf16_t*>(k),
+                       static_cast<bf16_t*>(v), static_cast<bf16_t*>(k_cache), static_cast<bf16_t*>(v_cache), slots,
+                       n_heads, n_kv_heads, head_dim);
+  else if (dtype == NS_DTYPE_BF16)
     hipLaunchKernelGGL(rope_qkv_kernel<bf16_t>, dim3(unsigned(n_tok)), dim3(256), 0, s,
                        static_cast<const bf16_t*>(qkv), static_cast<const bf16_t*>(cos),
                        static_cast<const bf16_t*>(sin), static_cast<bf16_t*>(q), static_cast<bf16_t*>(k),
