@@ -353,15 +353,18 @@ constexpr int ROWK_MAX_PARTS = 32;
 typedef __attribute__((ext_vector_type(4))) unsigned int rk_u32x4_t;
 typedef __attribute__((ext_vector_type(2))) unsigned int rk_u32x2_t;
 
-template <int HD>
+// PH: each KV head is a workgroup row of its own (hd 128, several KV heads); otherwise a row is a token's
+// whole 256-byte K row.
+template <int HD, bool PH>
 __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const bf16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, const bf16_t* __restrict__ kp,
     const bf16_t* __restrict__ vp, int64_t s_blk, const int32_t* __restrict__ bt, int64_t bt_sb,
     const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G, int nq,
     int max_blocks, int num_blocks, float scale_log2, unsigned* __restrict__ cnt, float* __restrict__ part_acc,
-    float* __restrict__ part_ml, int B, int n_parts) {
+    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h) {
   constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D, PART = ROWK_PART;
-  constexpr int RE = 128;            // elements of a token row (all KV heads)
+  // A workgroup's token row: 128 elements (256 bytes) -- all KV heads of a token (nkv_grid == 1), or one
+  // KV head of hd 128 when each KV head is a row of its own (nkv_grid == n_kv, token stride s_tok).
   constexpr int NKV = 128 / HD;
   constexpr int KS = HD / 32;
   constexpr int AROW = HD + 4;
@@ -372,8 +375,13 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   __shared__ unsigned s_last;
 
   // XCD-aware map as in the per-head kernel: a row's partitions rotate over the XCDs
-  const int L = blockIdx.x, part = L / B;
-  const int b = (L - part * B + part) % B;
+  const int nkv_grid = PH ? nkv_grid_arg : 1;
+  const int64_t s_tok = PH ? s_tok_arg : 128;
+  const int R = B * nkv_grid;
+  const int L = blockIdx.x, part = L / R;
+  const int row = (L - part * R + part) % R;
+  const int b = row / nkv_grid, g = row - b * nkv_grid;
+  const int nq_w = nkv_grid > 1 ? G : nq;   // query heads of this workgroup: heads g G .. g G + nq_w - 1
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
   const int p0 = part * PART;
@@ -385,11 +393,11 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const int p = p0 + w + NW * (lane < PPW ? lane : 0);
     blk_lane = p < max_blocks ? bt[int64_t(b) * bt_sb + p] : -1;
   }
-  const bool qlive = c16 < nq;
-  const int gq = qlive ? c16 / G : NKV;   // KV head of this lane's query column
+  const bool qlive = c16 < nq_w;
+  const int gq = qlive ? c16 / G : NKV;   // KV head (within the token row) of this lane's query column
   bf16x8_t qf[KS];
   {
-    const bf16_t* qrow = q + int64_t(b) * q_sb + int64_t(qlive ? c16 : 0) * q_sh;
+    const bf16_t* qrow = q + int64_t(b) * q_sb + int64_t(g * G + (qlive ? c16 : 0)) * q_sh;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       rk_u32x4_t u = *reinterpret_cast<const rk_u32x4_t*>(qrow + 32 * s + 8 * r4);
@@ -401,7 +409,8 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   if (n_pages > max_blocks) n_pages = max_blocks;
   if (ctx <= 0) {   // no keys: zeros
     if (part == 0)
-      for (int i = tid; i < nq * HD; i += NW * 64) out[int64_t(b) * o_sb + int64_t(i / HD) * o_sh + (i % HD)] = bf16_t(0);
+      for (int i = tid; i < nq_w * HD; i += NW * 64)
+        out[int64_t(b) * o_sb + int64_t(g * G + i / HD) * o_sh + (i % HD)] = bf16_t(0);
     return;
   }
   if (p0 >= n_pages) return;
@@ -418,10 +427,10 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     constexpr int sl = decltype(sc)::value;
     const int bid = __builtin_amdgcn_readlane(blk_lane, i < n_live ? i : 0);
     const bool ok = n_live > 0 && bid >= 0 && bid < num_blocks;
-    const int64_t base = int64_t(ok ? bid : 0) * s_blk;
+    const int64_t base = int64_t(ok ? bid : 0) * s_blk + (PH ? int64_t(g) * s_h : 0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int64_t off = base + int64_t(4 * j + r4) * RE + c16 * 8;
+      const int64_t off = base + int64_t(4 * j + r4) * s_tok + c16 * 8;
       kr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(kp + off);
       vr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(vp + off);
     }
@@ -553,10 +562,10 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
     const uint2 pk = make_uint2(uint32_t(f32_to_bf16(A[0] * inv)) | (uint32_t(f32_to_bf16(A[1] * inv)) << 16),
                                 uint32_t(f32_to_bf16(A[2] * inv)) | (uint32_t(f32_to_bf16(A[3] * inv)) << 16));
-    *reinterpret_cast<uint2*>(out + int64_t(b) * o_sb + int64_t(h) * o_sh + 4 * d4) = pk;
+    *reinterpret_cast<uint2*>(out + int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + 4 * d4) = pk;
   };
   constexpr int ITEMS = (16 * (HD / 4) + NW * 64 - 1) / (NW * 64);
-  const int n_items = nq * (HD / 4);
+  const int n_items = nq_w * (HD / 4);
   if (n_active == 1) {
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
@@ -572,9 +581,9 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   }
   // publish (m, l, acc) with 16-byte coherent stores, wait for them, then the row's counter
   const __amdgpu_buffer_rsrc_t racc =
-      __builtin_amdgcn_make_buffer_rsrc(part_acc + int64_t(b) * n_parts * (16 * HD), 0, n_parts * (16 * HD) * 4, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(part_acc + int64_t(row) * n_parts * (16 * HD), 0, n_parts * (16 * HD) * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t rml =
-      __builtin_amdgcn_make_buffer_rsrc(part_ml + int64_t(b) * n_parts * 32, 0, n_parts * 32 * 4, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(part_ml + int64_t(row) * n_parts * 32, 0, n_parts * 32 * 4, 0x00020000);
   constexpr int SC1 = 16;   // cache policy sc1: device-coherent, bypasses the XCD's L2
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
@@ -594,9 +603,9 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   publish_complete();
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = publish_count(cnt + b);
+    const unsigned prev = publish_count(cnt + row);
     const unsigned lst = prev == unsigned(n_active - 1);
-    if (lst) publish_reset(cnt + b);
+    if (lst) publish_reset(cnt + row);
     s_last = lst;
   }
   __syncthreads();
@@ -708,10 +717,16 @@ using namespace ns;
 
 // Whole-row kernel: n_kv * head_dim == 128 (one 256-byte token row), <= 16 query heads, token rows
 // contiguous in the pool, and a table width its merge covers.
-static inline bool rows_kernel_fits(int n_heads, int n_kv_heads, int head_dim, int64_t kv_spos, int64_t kv_sh,
-                                    int max_blocks) {
-  return n_kv_heads * head_dim == 128 && n_heads <= 16 && kv_sh == head_dim && kv_spos == 128 &&
-         (max_blocks + ROWK_PART - 1) / ROWK_PART <= ROWK_MAX_PARTS;
+// KV heads that are workgroup rows of their own: 1 when a token's K row (all KV heads) is 256 bytes
+// (n_kv * head_dim == 128, token rows contiguous), n_kv for hd 128 with several KV heads (one head's 256
+// bytes per workgroup row, tokens kv_spos apart); 0 when the whole-row kernel does not apply.
+static inline int rows_kernel_grid_heads(int n_heads, int n_kv_heads, int head_dim, int64_t kv_spos, int64_t kv_sh,
+                                         int max_blocks) {
+  if ((max_blocks + ROWK_PART - 1) / ROWK_PART > ROWK_MAX_PARTS) return 0;
+  if (n_kv_heads * head_dim == 128 && n_heads <= 16 && kv_sh == head_dim && kv_spos == 128) return 1;
+  if (head_dim == 128 && n_kv_heads > 1 && n_heads / n_kv_heads <= 16 && kv_sh == 128 && kv_spos % 8 == 0)
+    return n_kv_heads;
+  return 0;
 }
 static inline size_t per_head_ws_bytes(int B, int n_kv_heads, int head_dim, int max_blocks) {
   const size_t parts = size_t(decode_parts(head_dim, max_blocks));
@@ -734,7 +749,8 @@ extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim,
   if (dtype != NS_DTYPE_BF16 || B <= 0 || n_kv_heads <= 0 || max_blocks <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
   const size_t a = per_head_ws_bytes(B, n_kv_heads, head_dim, max_blocks);
-  const size_t r = n_kv_heads * head_dim == 128 ? rows_ws_bytes(B, head_dim, max_blocks) : 0;
+  const int rows_per_b = n_kv_heads * head_dim == 128 ? 1 : (head_dim == 128 ? n_kv_heads : 0);
+  const size_t r = rows_per_b > 0 ? rows_ws_bytes(B * rows_per_b, head_dim, max_blocks) : 0;
   return a > r ? a : r;
 }
 
@@ -780,8 +796,10 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                  0,
              "paged_attention_decode: q / k_pool / v_pool must be 16-byte aligned");
   const float sl2 = scale * LOG2E;
-  if (rows_kernel_fits(n_heads, n_kv_heads, head_dim, kv_spos, kv_sh, max_blocks)) {
+  const int rgh = rows_kernel_grid_heads(n_heads, n_kv_heads, head_dim, kv_spos, kv_sh, max_blocks);
+  if (rgh > 0) {
     const int rparts = (max_blocks + ROWK_PART - 1) / ROWK_PART;
+    const int rrows = B * rgh;
     unsigned* rcnt = nullptr;
     float* rml = nullptr;
     float* racc = nullptr;
@@ -796,23 +814,29 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                  "paged_attention_decode: workspace not 256-byte aligned");
       char* w = static_cast<char*>(workspace);
       rcnt = reinterpret_cast<unsigned*>(w);
-      rml = reinterpret_cast<float*>(w + align256(size_t(B) * sizeof(unsigned)));
-      racc = reinterpret_cast<float*>(w + align256(size_t(B) * sizeof(unsigned)) +
-                                      align256(size_t(B) * rparts * 32 * sizeof(float)));
+      rml = reinterpret_cast<float*>(w + align256(size_t(rrows) * sizeof(unsigned)));
+      racc = reinterpret_cast<float*>(w + align256(size_t(rrows) * sizeof(unsigned)) +
+                                      align256(size_t(rrows) * rparts * 32 * sizeof(float)));
     }
-    const dim3 rgrid(unsigned(rparts) * unsigned(B));
-    if (head_dim == 64)
-      hipLaunchKernelGGL(paged_decode_rows_bf16_kernel<64>, rgrid, dim3(ROWK_NW * 64), 0, s,
+    const dim3 rgrid(unsigned(rparts) * unsigned(rrows));
+    if (rgh > 1)
+      hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts);
+                         rml, B, rparts, rgh, kv_spos, kv_sh);
+    else if (head_dim == 64)
+      hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
+                         static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
+                         static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
+                         static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
+                         rml, B, rparts, 1, int64_t(128), kv_sh);
     else
-      hipLaunchKernelGGL(paged_decode_rows_bf16_kernel<128>, rgrid, dim3(ROWK_NW * 64), 0, s,
+      hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts);
+                         rml, B, rparts, 1, int64_t(128), kv_sh);
     return check_launch("paged_attention_decode(bf16 rows)");
   }
   const int parts = decode_parts(head_dim, max_blocks);

@@ -122,6 +122,18 @@ def test_merge_words_of_earlier_calls_are_never_taken(hiplib):
         assert torch.equal(out1, out2)
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hd", [(12, 2, 128), (14, 2, 64)])
+def test_per_head_kernel_for_tables_wider_than_the_row_merge(hiplib, n_heads, n_kv, hd):
+    """A table of 1100 pages (more partitions than the whole-row kernel merges) takes the per-head kernel;
+    contexts up to 1100 pages."""
+    g = cpu_gen(22)
+    ctx = [1, 700, 17600, 9000, 333]
+    q, k, v, tables, lens = make_case(n_heads, n_kv, hd, ctx, torch.bfloat16, seed=22, extra_blocks=4, width=1100)
+    out = run(q, k, v, tables, lens, hd ** -0.5)
+    ref = paged_attention_reference(q.float(), k.float(), v.float(), tables, lens, hd ** -0.5)
+    assert (out.float() - ref).abs().max().item() <= 1e-2
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_padding_entries_and_past_ctx_tokens_are_never_used(hiplib, dtype):
     """Padding table entries point at a NaN-filled block and the unused tail of each last page is NaN:
