@@ -223,8 +223,13 @@ int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void*
  * Greedy selection: out[r] = index of the first maximal element of row r of x (rows x n, row stride
  * ld elements); NaN ranks above every number (torch.argmax semantics). int64 output.
  * Replaces logits.argmax(-1) of nanoserve/engine.py:239 / sampling.py:59-60.
+ * workspace (optional, zero-initialised once by the caller, 256-byte aligned, at least
+ * ns_argmax_workspace_bytes(rows, n) bytes): rows are split over several workgroups merged in the same
+ * launch; every call leaves the workspace's counters at zero. NULL: one workgroup per row.
  */
-int ns_argmax_rows(const void* x, int64_t ld, int64_t rows, int n, int dtype, int64_t* out, void* stream);
+size_t ns_argmax_workspace_bytes(int64_t rows, int n);
+int ns_argmax_rows(const void* x, int64_t ld, int64_t rows, int n, int dtype, int64_t* out, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

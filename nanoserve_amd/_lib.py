@@ -49,7 +49,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "ns_silu_mul": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "ns_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                              _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp]),
-    "ns_argmax_rows": (_c_int, [_c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
+    "ns_argmax_workspace_bytes": (_c_sz, [_c_i64, _c_int]),
+    "ns_argmax_rows": (_c_int, [_c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_vp, _c_sz, _c_vp]),
     "ns_embed_rope": (_c_int, [_c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp, _c_int,   # ids pos n embed V H inv hd
                                _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_vp]),                 # x cos sin sumsq dtype stream
     "ns_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),

@@ -7,6 +7,23 @@ import torch
 from nanoserve_amd import _lib
 
 
+_WS: dict[int, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """A zero-filled workspace per device, grown (never shrunk) outside graph capture; the split kernel leaves
+    its counters at zero, so one buffer serves every call. None when capture would need a larger one (the
+    single-workgroup-per-row path needs none)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WS.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _WS[idx] = ws
+    return ws
+
+
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """logits [R, V] (last dim contiguous) -> int64 [R]."""
     assert logits.dim() == 2 and logits.stride(1) == 1
@@ -15,6 +32,8 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     if out is None:
         out = torch.empty(R, dtype=torch.int64, device=logits.device)
     assert out.dtype == torch.int64 and out.shape == (R,) and out.is_contiguous()
+    ws = _workspace(logits.device, _lib.lib().ns_argmax_workspace_bytes(R, V)) if R > 0 else None
     _lib.check(_lib.lib().ns_argmax_rows(logits.data_ptr(), logits.stride(0), R, V, _lib.dtype_code(logits),
-                                         out.data_ptr(), _lib.stream_of(logits)), "argmax_rows")
+                                         out.data_ptr(), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+                                         _lib.stream_of(logits)), "argmax_rows")
     return out

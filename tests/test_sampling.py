@@ -47,6 +47,36 @@ def test_argmax_rows_matches_torch(hiplib, dtype, V):
     x[6, :] = float("-inf")
     ref = x.argmax(-1)
     assert torch.equal(argmax_rows(x.cuda()).cpu(), ref)
+    assert torch.equal(argmax_rows(x.cuda()).cpu(), ref)     # the split path's counters are back at zero
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_argmax_rows_split_boundaries(hiplib, dtype):
+    """Row splits: maxima placed on every split boundary, ties across splits (the first index wins), NaN in
+    the last split, a row of one value, and the same call without a workspace (one workgroup per row)."""
+    from nanoserve_amd import _lib
+    from nanoserve_amd.kernels.sampling import argmax_rows
+    g = cpu_gen(5)
+    R, V = 32, 151936
+    x = torch.randn(R, V, generator=g).to(dtype)
+    vec = 8 if dtype == torch.bfloat16 else 4
+    splits = min(512 // R, V // 2048, 64)
+    bounds = [((k * (V // vec)) // splits) * vec for k in range(1, splits)]
+    for r, bnd in enumerate(bounds[: R // 2]):
+        x[r, bnd - 1] = 10.0 + r                  # last element of split k-1 ...
+        x[r, bnd] = 10.0 + r                      # ... ties with the first of split k: the earlier wins
+    x[20, -1] = float("nan")
+    x[21, :] = 3.0
+    x[22, 5] = 50.0
+    x[22, V - 5] = 50.0
+    ref = x.argmax(-1)
+    xd = x.cuda()
+    assert torch.equal(argmax_rows(xd).cpu(), ref)
+    out = torch.empty(R, dtype=torch.int64, device="cuda")
+    assert _lib.lib().ns_argmax_rows(xd.data_ptr(), xd.stride(0), R, V, _lib.dtype_code(xd), out.data_ptr(), None, 0,
+                                     _lib.stream_of(xd)) == 0
+    assert torch.equal(out.cpu(), ref)
 
 
 @pytest.mark.gpu
