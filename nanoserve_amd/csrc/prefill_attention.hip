@@ -45,6 +45,7 @@ namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 pf_bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float pf_float4_t;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
 constexpr float PF_LOG2E = 1.4426950408889634f;
 constexpr int PF_PAGE = 16;
@@ -70,6 +71,10 @@ struct PfLds {
   // K rows are stored with their 16-byte chunks XOR-swizzled by the row, so the 16 rows one fragment
   // read touches land in 16 different bank groups: logical chunk c of stage row t sits at c ^ key(t).
   static __device__ __forceinline__ int key(int t) { return HD == 128 ? (t & 15) : ((t >> 1) & 7); }
+  // V rows likewise, by an even key from the row's low bits: a transpose read takes a 32-byte chunk pair
+  // (2 chunks) from each of four consecutive rows, and XOR by even values moves whole pairs, so the four
+  // rows' pairs land in four different bank groups.
+  static __device__ __forceinline__ int vkey(int t) { return (t & (CH / 2 - 1)) << 1; }
 };
 static_assert(PF_NP == PF_WAVES, "each wave stages one page of a stage");
 
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
       __builtin_amdgcn_global_load_lds(
           (__attribute__((address_space(1))) void*)(a.kp + row + 8 * (cp ^ L::key(t))),
           (__attribute__((address_space(3))) void*)(kd + 1024 * i), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(a.vp + row + 8 * cp),
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(a.vp + row + 8 * (cp ^ L::vkey(t))),
                                        (__attribute__((address_space(3))) void*)(vd + 1024 * i), 16, 0, 0);
     }
   };
@@ -262,29 +267,18 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
       }
     }
     // ---- P.V over two 32-key steps: k-slots 0..3 = page 2*ks2 keys 4*r4 + e, 4..7 = page 2*ks2 + 1.
-    // V^T fragments are built once per step and feed both query tiles.
+    // V^T fragments come straight from LDS by transpose reads (ds_read_b64_tr_b16): within each group of
+    // 16 lanes, lane j addresses 4 dims (16t + 4 (j % 4) ..) of key row kb + j / 4, and lane i receives
+    // dim 16t + i of keys kb .. kb + 3 -- its A-operand slots for one page. Built once per step, they feed
+    // every query tile.
 #pragma unroll
     for (int ks2 = 0; ks2 < 2; ++ks2) {
-      uint32_t va[2][NT][2];
+      v4i16_t va[2][NT];
 #pragma unroll
       for (int hp = 0; hp < 2; ++hp) {
         const int pp = 2 * ks2 + hp;
-        const unsigned char* vrow = st + L::K_BYTES + (PF_PAGE * pp + 4 * r4) * L::ROW + NT * 2 * c16;
-        uint32_t vw[4][VW];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (VW == 4) {
-            const uint4 u = *reinterpret_cast<const uint4*>(vrow + e * L::ROW);
-            vw[e][0] = u.x;
-            vw[e][1] = u.y;
-            vw[e][2] = u.z;
-            vw[e][3] = u.w;
-          } else {
-            const uint2 u = *reinterpret_cast<const uint2*>(vrow + e * L::ROW);
-            vw[e][0] = u.x;
-            vw[e][1] = u.y;
-          }
-        }
+        const int vr = PF_PAGE * pp + 4 * r4 + (c16 >> 2);   // the key row this lane addresses
+        const unsigned char* vrow = st + L::K_BYTES + vr * L::ROW;
         uint32_t m01 = 0xffffffffu, m23 = 0xffffffffu;
         if constexpr (MASK) {   // keys that do not exist read as 0
           const int key0 = kb0 + PF_PAGE * pp + 4 * r4;
@@ -294,14 +288,17 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const int wd = t >> 1;
-          if ((t & 1) == 0) {
-            va[hp][t][0] = pf_pack_lo(vw[0][wd], vw[1][wd]) & m01;
-            va[hp][t][1] = pf_pack_lo(vw[2][wd], vw[3][wd]) & m23;
-          } else {
-            va[hp][t][0] = pf_pack_hi(vw[0][wd], vw[1][wd]) & m01;
-            va[hp][t][1] = pf_pack_hi(vw[2][wd], vw[3][wd]) & m23;
+          const int dim = 16 * t + 4 * (c16 & 3);
+          const int chunk = dim >> 3;
+          const unsigned char* src = vrow + 16 * (chunk ^ L::vkey(vr)) + 2 * (dim & 7);
+          v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)(src));
+          if constexpr (MASK) {
+            uint2 u = __builtin_bit_cast(uint2, v);
+            u.x &= m01;
+            u.y &= m23;
+            v = __builtin_bit_cast(v4i16_t, u);
           }
+          va[hp][t] = v;
         }
       }
 #pragma unroll
@@ -310,8 +307,8 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
             pf_bf16x8_t, make_uint4(pb[rt][2 * ks2][0], pb[rt][2 * ks2][1], pb[rt][2 * ks2 + 1][0], pb[rt][2 * ks2 + 1][1]));
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const pf_bf16x8_t vav =
-              __builtin_bit_cast(pf_bf16x8_t, make_uint4(va[0][t][0], va[0][t][1], va[1][t][0], va[1][t][1]));
+          const uint2 lo = __builtin_bit_cast(uint2, va[0][t]), hi = __builtin_bit_cast(uint2, va[1][t]);
+          const pf_bf16x8_t vav = __builtin_bit_cast(pf_bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
           acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vav, pbv, acc[rt][t], 0, 0, 0);
         }
       }
@@ -360,22 +357,14 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     l_run[rt] += __shfl_xor(l_run[rt], 16, 64);
     l_run[rt] += __shfl_xor(l_run[rt], 32, 64);
   }
-  // lane holds, for query tile rt, tile t and r = 0..3, query c16 at dim NT*(4*r4 + r) + t
+  // lane holds, for query tile rt, tile t and r = 0..3, query c16 at dim 16 t + 4 r4 + r
   auto write_out = [&](int rt, const pf_float4_t (&o)[NT], float inv) __attribute__((always_inline)) {
     if (jq[rt] >= T) return;
     bf16_t* orow = a.out + int64_t(q_start + jq[rt]) * a.o_st + int64_t(h) * a.o_sh;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      uint32_t pk[VW];
-#pragma unroll
-      for (int t2 = 0; t2 < VW; ++t2)
-        pk[t2] = uint32_t(f32_to_bf16(o[2 * t2][r] * inv)) | (uint32_t(f32_to_bf16(o[2 * t2 + 1][r] * inv)) << 16);
-      bf16_t* dst = orow + NT * (4 * r4 + r);
-      if constexpr (VW == 4)
-        *reinterpret_cast<uint4*>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-      else
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pk[0], pk[1]);
-    }
+    for (int t = 0; t < NT; ++t)
+      *reinterpret_cast<uint2*>(orow + 16 * t + 4 * r4) =
+          make_uint2(pf_bf16x2(o[t][0] * inv, o[t][1] * inv), pf_bf16x2(o[t][2] * inv, o[t][3] * inv));
   };
   if (n_parts == 1) {
 #pragma unroll
