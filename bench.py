@@ -24,6 +24,8 @@ alone at that shape (FLOPs = sum_j (512 + j + 1) * n_heads * hd * 4 per layer).
 fused_ops: the standalone RMSNorm+residual, SiLU*mul and RoPE+KV-write kernels at 32 and 1552 rows of the
 1.5B shapes: algorithmic HBM bytes per launch over the HIP-event time (`--ops-only` runs these and the
 chunked-prefill kernel alone, for rocprofv3 --pmc passes).
+spec_verify: speculative verification through the decode graph -- k + 1 rows per sequence sharing its
+block table (k = 2: 32 sequences, k = 4: 24 sequences, 1024-token contexts): ms per verify step.
 prefix_sharing: BASELINE config 5 (3B shape, a 1024-token prefix shared by 32 requests through the prefix
 cache, 211-token suffixes): decode tokens/s and the step's HBM roofline, logical (a shared block counted
 once per row that reads it) and unique bytes.
@@ -336,6 +338,49 @@ def fused_ops_bench(reps: int = 100) -> dict:
     return out
 
 
+def spec_verify_bench(model, cfg, ctx: int = 1024, reps: int = 20) -> dict:
+    """Speculative verification through the decode graph (nanoserve/speculative.py:193-211): each sequence's
+    k draft tokens plus its last accepted token are k + 1 decode rows sharing the sequence's block table, with
+    context lengths ctx + 1 .. ctx + k + 1, in one graph replay. 1.5B shape, bf16, `ctx`-token contexts of
+    random K/V; k = 2 with 32 sequences (96 rows) and k = 4 with 24 sequences (120 rows, the largest bucket
+    that holds them). Returns ms per verify step and rows (tokens checked) per second."""
+    from nanoserve_amd.hip_graphs import DecodeGraphRunner
+    from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
+    out = {}
+    for k, nseq in ((2, 32), (4, 24)):
+        k1 = k + 1
+        pool = PagedKVCache.from_token_budget(cfg, nseq * (ctx + k1 + 16) + 64, 16, "cuda", torch.bfloat16)
+        g = torch.Generator(device="cuda").manual_seed(5)
+        pool.k.normal_(generator=g)
+        pool.v.normal_(generator=g)
+        runner = DecodeGraphRunner(model, pool, max_seq_len=ctx + k1 + 16)
+        tables = []
+        for _ in range(nseq):
+            t = BlockTable(16)
+            t.reserve(ctx + k1, pool.allocator)
+            t.commit(ctx)
+            tables.append(t)
+        gt = torch.Generator().manual_seed(6)
+        toks = torch.randint(0, cfg.vocab_size, (nseq * k1,), generator=gt).tolist()
+        args = dict(tokens=toks, positions=[ctx + j for _ in tables for j in range(k1)],
+                    slots=[x for t in tables for x in t.slots(k1)],
+                    block_tables=[t.blocks for t in tables for _ in range(k1)],
+                    context_lens=[ctx + j + 1 for _ in tables for j in range(k1)])
+        for _ in range(3):
+            runner.run(**args)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            runner.run(**args)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / reps * 1e3
+        out[f"k{k}"] = {"sequences": nseq, "rows": nseq * k1, "ctx": ctx, "ms_per_verify_step": round(ms, 3),
+                        "rows_per_s": round(nseq * k1 / (ms * 1e-3), 1)}
+        del runner, pool
+        torch.cuda.empty_cache()
+    return out
+
+
 def prefill_attention_bench(reps: int = 50) -> dict:
     """The chunked-prefill attention kernel alone at BASELINE config 4's shape with synthetic pages: one
     sequence, a 1536-token chunk on 512 cached tokens (2048 keys), 12 q / 2 kv heads, hd 128, its 128 blocks
@@ -463,6 +508,11 @@ def main() -> int:
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"decode: {tok_s:.0f} tok/s, {ms_step:.3f} ms/step, {step_gbs:.0f} GB/s algorithmic")
 
+    log("speculative verification rows (k = 2, 4)")
+    spec = spec_verify_bench(model, cfg)
+    log(f"verify steps: k=2 {spec['k2']['ms_per_verify_step']} ms ({spec['k2']['rows']} rows), "
+        f"k=4 {spec['k4']['ms_per_verify_step']} ms ({spec['k4']['rows']} rows)")
+
     mixed = None
     if not args.no_mixed_step:
         log("mixed step (config 4 shape)")
@@ -506,6 +556,7 @@ def main() -> int:
                           "roofline_tok_s": round(B / (step_bytes / (PEAK_HBM_GBS * 1e9)), 1)},
         "mixed_step": mixed,
         "fused_ops": ops,
+        "spec_verify": spec,
         "prefix_sharing": prefix,
         "cpu_baseline": cpu,
     }

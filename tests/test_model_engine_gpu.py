@@ -261,6 +261,54 @@ def test_graph_step_bitwise_equals_eager_at_bucket_size(hiplib):
     assert len(changed) <= 3
 
 
+def test_speculative_verify_rows_match_token_by_token_decode(hiplib):
+    """Speculative verification through the decode graph (nanoserve/speculative.py:193-211): each of k + 1
+    new tokens of a sequence is its own decode row with the sequence's block table and context length
+    ctx + j + 1, all written and attended in one step. Its logits must equal decoding the same tokens one
+    step at a time (eager decode rows), row for row, and pick the same argmax."""
+    from nanoserve_amd.hip_graphs import DecodeGraphRunner
+    from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
+    model, _ = gpu_model(SMALL128, torch.bfloat16)
+    pool = PagedKVCache.from_token_budget(SMALL128, 8192, 16, "cuda", torch.bfloat16)
+    runner = DecodeGraphRunner(model, pool, max_seq_len=1024, max_batch=16)
+    k1 = 4                                                   # k = 3 draft tokens + the last accepted one
+    tables, ctxs = [], []
+    for i, ids in enumerate(prompts(4, 300, SMALL128.vocab_size, seed=7)):
+        ids = ids[:150 + 37 * i]
+        t = BlockTable(16)
+        t.reserve(len(ids) + k1, pool.allocator)
+        model.forward_batch(torch.tensor(ids, device="cuda"), torch.arange(len(ids), device="cuda"),
+                            [SeqInput(len(ids))], paged=pool, slot_mapping=torch.tensor(t.slots(len(ids)), device="cuda"))
+        t.commit(len(ids))
+        tables.append(t)
+        ctxs.append(len(ids))
+    drafts = [torch.randint(0, SMALL128.vocab_size, (k1,), generator=torch.Generator().manual_seed(30 + i)).tolist()
+              for i in range(4)]
+    slots = [t.slots(k1) for t in tables]                    # the k1 slots after each context
+    # token by token: step j feeds token j of every sequence as one eager decode row each
+    seq = torch.empty(4, k1, SMALL128.vocab_size, dtype=torch.bfloat16)
+    width = max(len(t.blocks) for t in tables)
+    bt = torch.tensor([t.blocks + [0] * (width - len(t.blocks)) for t in tables], dtype=torch.int32, device="cuda")
+    for j in range(k1):
+        meta = DecodeMeta(token_idx=torch.arange(4, device="cuda"), block_tables=bt,
+                          context_lens=torch.tensor([c + j + 1 for c in ctxs], dtype=torch.int32, device="cuda"))
+        lg = model.forward_batch(torch.tensor([d[j] for d in drafts], device="cuda"),
+                                 torch.tensor([c + j for c in ctxs], device="cuda"),
+                                 [SeqInput(1, ctx_len=c + j, use_kernel=True) for c in ctxs], logits="all", paged=pool,
+                                 slot_mapping=torch.tensor([s[j] for s in slots], device="cuda"), decode_meta=meta)
+        seq[:, j] = lg.cpu()
+    # one verify step: 16 rows, rows of a sequence sharing its table
+    out = runner.run(tokens=[x for d in drafts for x in d],
+                     positions=[c + j for c in ctxs for j in range(k1)],
+                     slots=[x for s in slots for x in s],
+                     block_tables=[t.blocks for t in tables for _ in range(k1)],
+                     context_lens=[c + j + 1 for c in ctxs for j in range(k1)]).cpu().view(4, k1, -1)
+    diff = (out.float() - seq.float()).abs().max().item()
+    print(f"verify rows vs token by token: max|diff| {diff:.3e}, bitwise equal {torch.equal(out, seq)}")
+    assert diff <= 1e-2
+    assert torch.equal(out.float().argmax(-1), seq.float().argmax(-1))
+
+
 def oracle_streams(cfg, sd, reqs):
     """Greedy tokens (and logits) of each request generated alone by the CPU oracle."""
     orc = OracleModel(cfg, {k: v.cpu() for k, v in sd.items()})
