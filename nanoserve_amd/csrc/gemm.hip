@@ -588,6 +588,164 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------
+// Persistent 64-row GEMM for wide STORE projections (the tied LM head: ~2,400 tiles of 64 vocabulary rows)
+// with M <= 32 and K <= 2048. Launched one workgroup per tile, every workgroup re-reads the whole activation
+// block (96 KB at M = 32, K = 1536) for its 196 KB of weights. Here about two workgroups per CU stay
+// resident and walk tiles blockIdx.x, blockIdx.x + G, ...: each wave loads the activation fragments of its
+// k-steps (2 wv, 2 wv + 1 of every 256-k chunk) once -- normalised once for a normalised input -- and keeps
+// them in registers, so the weights are the only stream. A workgroup's (tile, chunk) sequence is one
+// rolling pipeline (two chunks of weight loads in flight, staged through LDS exactly as in the 64-row
+// kernel), so the next tile's first chunks are in flight while a tile's partial sums are reduced and
+// stored; the reduction reuses the stage buffer of the tile's last chunk. CP: chunks per tile rounded up to
+// even (a padding chunk re-reads the last one and multiplies nothing).
+template <int TM, bool NX, int CP>
+__global__ __launch_bounds__(G_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void persist_gemm_kernel(GemmArgs a) {
+  static_assert(TM <= 2 && CP % 2 == 0 && CP <= 8, "reduction in one stage buffer; K <= 2048");
+  __shared__ __align__(16) unsigned char lds[2 * G_STAGE];
+  constexpr int R = 16 * TM;
+  const int G = gridDim.x, K = a.K, N = a.N;
+  const int n_my = (a.tiles - int(blockIdx.x) + G - 1) / G;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c16 = lane & 15, r4 = lane >> 4;
+  const int half_sel = lane >> 5, col16 = lane & 31;
+  const int st_off = wv * G_NTB + half_sel * 512 + col16 * 16;        // + p * G_PAIR
+  const int fr_off = (c16 & 7) * G_PAIR + (c16 >> 3) * 512 + r4 * 16;   // + j * G_NTB + kstep * 64
+
+  // (normalised input) statistics and norm weight first, so waiting for them waits for nothing else
+  const bool stat_wave = wv < TM;
+  const int ptiles = (K + G_NORM_COLS - 1) / G_NORM_COLS;
+  float rs[RS_PRE];
+  constexpr int NWT = 2048 / 2 / (G_WAVES * 64);   // norm-weight words per thread (K <= 2048)
+  uint32_t nw_word[NWT];
+  if constexpr (NX) {
+    if (stat_wave) row_stats_issue(a.xsq, ptiles, a.M, rs);
+#pragma unroll
+    for (int j = 0; j < NWT; ++j)
+      nw_word[j] = reinterpret_cast<const uint32_t*>(a.xnw)[min(tid + j * G_WAVES * 64, (K >> 1) - 1)];
+  }
+  // this wave's activation fragments of every chunk
+  g_u32x4_t xa[CP][2][TM];
+#pragma unroll
+  for (int c = 0; c < CP; ++c)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = min(c * G_KC + 32 * (2 * wv + h), K - 32) + 8 * r4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        xa[c][h][i] = *reinterpret_cast<const g_u32x4_t*>(a.x + int64_t(min(16 * i + c16, a.M - 1)) * K + k);
+    }
+  // weights: stream position (tile i of this workgroup, chunk c); past the end it re-reads the last one
+  g_u32x4_t wr[2][8];
+  auto load_w = [&](auto qc, int i, int c) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    if (c >= CP) {
+      c -= CP;
+      ++i;
+    }
+    if (i >= n_my) {
+      i = n_my - 1;
+      c = CP - 1;
+    }
+    const int t = int(blockIdx.x) + i * G;
+    const int kc = min(c * G_KC, K - 8 * col16 - 8);   // k beyond K: a clamped in-bounds address, not multiplied
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int row = min(t * 64 + 16 * wv + p + 8 * half_sel, N - 1);
+      wr[q][p] = *reinterpret_cast<const g_u32x4_t*>(a.w + int64_t(row) * K + 8 * col16 + kc);
+    }
+  };
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
+  load_w(Q0{}, 0, 0);
+  load_w(Q1{}, 0, 1);
+  if constexpr (NX) {
+    __shared__ float s_inv[G_MAX_M];
+    __shared__ __align__(16) uint32_t s_nw[1024];
+    if (stat_wave) row_stats_finish(a.xsq, ptiles, a.M, K, a.xeps, rs, s_inv);
+#pragma unroll
+    for (int j = 0; j < NWT; ++j)
+      if (tid + j * G_WAVES * 64 < (K >> 1)) s_nw[tid + j * G_WAVES * 64] = nw_word[j];
+    __syncthreads();
+    float xinv[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xinv[i] = s_inv[min(16 * i + c16, a.M - 1)];
+#pragma unroll
+    for (int c = 0; c < CP; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k0 = c * G_KC + 32 * (2 * wv + h);
+        if (k0 < K) {
+          const g_u32x4_t w8 = *reinterpret_cast<const g_u32x4_t*>(s_nw + ((k0 + 8 * r4) >> 1));
+#pragma unroll
+          for (int i = 0; i < TM; ++i) xa[c][h][i] = norm_fragment(xa[c][h][i], w8, xinv[i]);
+        }
+      }
+  }
+  g_float4_t acc[TM][G_TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < G_TN; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
+  int buf = 0;
+  auto step = [&](auto qc, auto cc, int i) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value, c = decltype(cc)::value;
+    unsigned char* stage = lds + buf * G_STAGE;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) *reinterpret_cast<g_u32x4_t*>(stage + st_off + p * G_PAIR) = wr[q][p];
+    load_w(qc, i, c + 2);
+    __syncthreads();   // the chunk's 64 rows are in this buffer; every wave is done with the other one
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kstep = 2 * wv + h;
+      if (c * G_KC + 32 * kstep < K) {   // uniform
+        g_bf16x8_t bfr[G_TN];
+#pragma unroll
+        for (int j = 0; j < G_TN; ++j)
+          bfr[j] = __builtin_bit_cast(g_bf16x8_t, *reinterpret_cast<const g_u32x4_t*>(stage + j * G_NTB + kstep * 64 + fr_off));
+#pragma unroll
+        for (int ii = 0; ii < TM; ++ii)
+#pragma unroll
+          for (int j = 0; j < G_TN; ++j)
+            acc[ii][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, xa[c][h][ii]), bfr[j],
+                                                                 acc[ii][j], 0, 0, 0);
+      }
+    }
+    buf ^= 1;
+  };
+  const g_u32x4_t none[g_items8<4>()] = {};
+  for (int i = 0; i < n_my; ++i) {
+    step(Q0{}, std::integral_constant<int, 0>{}, i);
+    step(Q1{}, std::integral_constant<int, 1>{}, i);
+    if constexpr (CP > 2) {
+      step(Q0{}, std::integral_constant<int, 2>{}, i);
+      step(Q1{}, std::integral_constant<int, 3>{}, i);
+    }
+    if constexpr (CP > 4) {
+      step(Q0{}, std::integral_constant<int, 4>{}, i);
+      step(Q1{}, std::integral_constant<int, 5>{}, i);
+    }
+    if constexpr (CP > 6) {
+      step(Q0{}, std::integral_constant<int, 6>{}, i);
+      step(Q1{}, std::integral_constant<int, 7>{}, i);
+    }
+    // tile done: the waves' partial tiles are summed through the buffer of the last chunk (wave order)
+    float* red = reinterpret_cast<float*>(lds + (buf ^ 1) * G_STAGE);
+    __syncthreads();   // every wave is done multiplying out of that buffer
+#pragma unroll
+    for (int ii = 0; ii < TM; ++ii)
+#pragma unroll
+      for (int j = 0; j < G_TN; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wv * R + 16 * ii + 4 * r4 + r) * G_RED + 16 * j + c16] = acc[ii][j][r];
+        acc[ii][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    __syncthreads();
+    TileSource src{red, R, false, 1, nullptr};
+    tile_epilogue<TM, EPI_STORE>(a, src, int(blockIdx.x) + i * G, none);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------
 // Tile-16 GEMM for projections with few weight rows (QKV, O: N in the low thousands, K <= 2048). A split-K
 // plan would need a cross-workgroup merge whose round trips (publish, counter, reload) cost more than the
 // few microseconds these projections stream for, so here one workgroup owns 16 weight rows over the whole
@@ -927,6 +1085,41 @@ static int launch_t16(const GemmArgs& a, int tiles, hipStream_t st) {
   return check_launch("skinny_gemm(tile16)");
 }
 
+// The persistent kernel takes wide STORE projections without bias: M <= 32, K <= 2048, at least four tiles
+// per CU (the LM head).
+static bool persist_fits(int M, int K, int tiles, const void* bias) {
+  return M <= 32 && K <= 2048 && tiles >= 4 * target_workgroups() && bias == nullptr;
+}
+template <bool NX, int CP>
+static void launch_persist_cp(const GemmArgs& a, int grid, hipStream_t st) {
+  if (a.M <= 16)
+    hipLaunchKernelGGL((persist_gemm_kernel<1, NX, CP>), dim3(unsigned(grid)), dim3(G_WAVES * 64), 0, st, a);
+  else
+    hipLaunchKernelGGL((persist_gemm_kernel<2, NX, CP>), dim3(unsigned(grid)), dim3(G_WAVES * 64), 0, st, a);
+}
+template <bool NX>
+static void launch_persist_nx(const GemmArgs& a, int grid, hipStream_t st) {
+  switch ((a.chunks + 1) & ~1) {
+    case 2: launch_persist_cp<NX, 2>(a, grid, st); break;
+    case 4: launch_persist_cp<NX, 4>(a, grid, st); break;
+    case 6: launch_persist_cp<NX, 6>(a, grid, st); break;
+    default: launch_persist_cp<NX, 8>(a, grid, st); break;
+  }
+}
+// Two resident workgroups per CU, each with the same number of tiles (the last one fewer).
+static int launch_persist(GemmArgs a, int tiles, hipStream_t st) {
+  a.tiles = tiles;
+  a.chunks = (a.K + G_KC - 1) / G_KC;
+  const int T = 2 * target_workgroups();
+  const int per = (tiles + T - 1) / T;
+  const int grid = (tiles + per - 1) / per;
+  if (a.xsq != nullptr)
+    launch_persist_nx<true>(a, grid, st);
+  else
+    launch_persist_nx<false>(a, grid, st);
+  return check_launch("gemm(persistent)");
+}
+
 template <int EPI>
 static int launch(const GemmArgs& a, hipStream_t st) {
   if constexpr (EPI == EPI_RESNORM) {
@@ -985,6 +1178,7 @@ extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, 
   a.y = static_cast<bf16_t*>(y);
   if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
   if (tile16_fits(K, (N + 15) / 16)) return launch_t16<EPI_STORE>(a, (N + 15) / 16, reinterpret_cast<hipStream_t>(stream));
+  if (persist_fits(M, K, (N + 63) / 64, bias)) return launch_persist(a, (N + 63) / 64, reinterpret_cast<hipStream_t>(stream));
   if ((st = bind_workspace(a, make_plan((N + 63) / 64, K), ws, ws_bytes)) != NS_OK) return st;
   return launch<EPI_STORE>(a, reinterpret_cast<hipStream_t>(stream));
 }

@@ -402,9 +402,14 @@ class Qwen2Model:
             idx = ends
         if idx is not None:
             x = x.rows(idx) if isinstance(x, NormedRows) else x[idx]
-        # The LM head streams 2,374 whole tiles, one per workgroup: normalising on load would repeat the
-        # row-statistics prologue in every one of them, so the final norm is materialised once instead.
-        return linear(x.tensor() if isinstance(x, NormedRows) else x.contiguous(), self.lm_head)
+        # Up to 32 rows (K <= 2048) the wide LM head runs on persistent workgroups that normalise their
+        # activation fragments once, so it takes the NormedRows itself; beyond that every 64-row tile would
+        # repeat the row-statistics prologue, so the final norm is materialised once instead.
+        if isinstance(x, NormedRows):
+            if x.r.shape[0] > 32 or x.r.shape[1] > 2048:
+                x = x.tensor()
+            return linear(x, self.lm_head)
+        return linear(x.contiguous(), self.lm_head)
 
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, cache=None, logits: str = "last"):
         raise NotImplementedError("the single-sequence contiguous-cache API (M1) is not part of the HIP path; "

@@ -77,6 +77,26 @@ def test_lm_head_shape(hiplib):
     bf16_check(linear(x.cuda(), w.cuda()), ref_linear(x, w), "lm head 32x151936x1536", dot_bound(x, w))
 
 
+@pytest.mark.parametrize("M", [1, 16, 32])
+@pytest.mark.parametrize("K", [896, 1280, 2048])
+def test_wide_projection_persistent_kernel(hiplib, M, K):
+    """Wide projections without bias (at least four 64-row tiles per CU, M <= 32, K <= 2048: the LM head) run
+    on persistent workgroups that keep their activation fragments in registers across tiles. N = 65573 (a
+    partial last tile), K with a partial and a padding chunk; a normalised input equals its materialised
+    norm bitwise here too."""
+    from nanoserve_amd.kernels.linear import linear, linear_residual_rms_norm
+    N = 65536 + 37
+    x, w = operands(M, N, K, seed=M + K)
+    wd = w.cuda()
+    bf16_check(linear(x.cuda(), wd), ref_linear(x, w), f"wide M={M} N={N} K={K}", dot_bound(x, w))
+    if M == 32:
+        x0, w0 = operands(M, K, 512, seed=40)
+        res = torch.randn(M, K, generator=cpu_gen(41)).to(BF).cuda()
+        nw = (1 + 0.1 * torch.randn(K, generator=cpu_gen(42))).to(BF).cuda()
+        hn, _ = linear_residual_rms_norm(x0.cuda(), w0.cuda(), res, nw, 1e-6)
+        assert torch.equal(linear(hn, wd), linear(hn.tensor(), wd))
+
+
 @pytest.mark.parametrize("M", [1, 24, 32, 64])
 @pytest.mark.parametrize("I,K", [(8960, 1536), (4864, 896), (11008, 2048)])
 def test_linear_silu_mul(hiplib, M, I, K):
