@@ -781,7 +781,34 @@ __device__ __forceinline__ int t16_row(const GemmArgs& a, int t, int r) {
 template <int TM, int EPI, bool NX>
 __global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a) {
   __shared__ __align__(16) unsigned char lds[16 * 2 * T16_MAX_K];   // weight tile, then the partial tiles
-  const int t = blockIdx.x, M = a.M, K = a.K;
+  // Token-split launch (TM = 1 with M > 16, gridDim.x = tiles * ceil(M / 16)): workgroup mb * tiles + t
+  // computes tokens [16 mb, 16 mb + 16) of tile t over all of K. The token blocks of a tile share its weight
+  // rows through L2 (same XCD when tiles % 8 == 0) and each workgroup reads half the activations.
+  int t = blockIdx.x;
+  if (TM == 1 && a.M > 16) {
+    const int mbs = (a.M + 15) >> 4, tiles = int(gridDim.x) / mbs, mb = t / tiles, m0 = 16 * mb;
+    t -= mb * tiles;
+    a.M = min(16, a.M - m0);
+    a.x += int64_t(m0) * a.K;
+    if constexpr (NX) a.xsq += m0;
+    if constexpr (EPI == EPI_STORE) {
+      a.y += int64_t(m0) * a.N;
+    } else if constexpr (EPI == EPI_RESNORM) {
+      a.residual += int64_t(m0) * a.N;
+      a.res_out += int64_t(m0) * a.N;
+      if (a.sumsq_out != nullptr) a.sumsq_out += m0;
+    } else if constexpr (EPI == EPI_SILU) {
+      a.y += int64_t(m0) * (a.N >> 1);
+    } else {
+      a.cosb += int64_t(m0) * a.hd;
+      a.sinb += int64_t(m0) * a.hd;
+      if (a.slots != nullptr) a.slots += m0;
+      a.q += int64_t(m0) * a.nh * a.hd;
+      a.k += int64_t(m0) * a.nkv * a.hd;
+      a.v += int64_t(m0) * a.nkv * a.hd;
+    }
+  }
+  const int M = a.M, K = a.K;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
   const int rowb = 2 * K;   // bytes of a weight row = LDS pitch
@@ -1062,9 +1089,23 @@ static void launch_nx(const GemmArgs& a, hipStream_t st) {
 constexpr int T16_MAX_TILES = 512;
 static bool tile16_fits(int K, int tiles) { return K <= T16_MAX_K && tiles <= T16_MAX_TILES; }
 
+// Token split: with at most T16_MAX_TILES workgroups in all, each tile's tokens are cut into blocks of 16,
+// one workgroup each (NS_T16_MSPLIT=0 turns it off, for experiments).
+static bool t16_token_split(int M, int tiles) {
+  static const bool on = [] {
+    const char* e = getenv("NS_T16_MSPLIT");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on && M > 16 && tiles * ((M + 15) / 16) <= T16_MAX_TILES;
+}
 template <int EPI, bool NX>
 static void launch_t16_nx(const GemmArgs& a, int tiles, hipStream_t st) {
-  const dim3 grid{unsigned(tiles)}, block{unsigned(T16_WAVES * 64)};
+  const dim3 block{unsigned(T16_WAVES * 64)};
+  if (t16_token_split(a.M, tiles)) {
+    hipLaunchKernelGGL((tile16_gemm_kernel<1, EPI, NX>), dim3(unsigned(tiles * ((a.M + 15) / 16))), block, 0, st, a);
+    return;
+  }
+  const dim3 grid{unsigned(tiles)};
   if (a.M <= 16)
     hipLaunchKernelGGL((tile16_gemm_kernel<1, EPI, NX>), grid, block, 0, st, a);
   else if (a.M <= 32)

@@ -111,7 +111,7 @@ def test_linear_silu_mul(hiplib, M, I, K):
     bf16_check(linear_silu_mul(x.cuda(), w.cuda()), ops.silu_mul(gu), f"silu_mul M={M} I={I}", 2 * bound)
 
 
-@pytest.mark.parametrize("M", [1, 32, 64])
+@pytest.mark.parametrize("M", [1, 20, 32, 64])
 @pytest.mark.parametrize("N,K,norm", [(1536, 1536, True), (1536, 8960, True), (896, 4864, False), (2048, 11008, True)])
 def test_linear_residual_rms_norm(hiplib, M, N, K, norm):
     from nanoserve_amd.kernels.linear import linear_residual_rms_norm
@@ -136,7 +136,7 @@ def test_linear_residual_rms_norm(hiplib, M, N, K, norm):
         assert h is None
 
 
-@pytest.mark.parametrize("M", [1, 32, 64])
+@pytest.mark.parametrize("M", [1, 20, 32, 64])
 @pytest.mark.parametrize("nh,nkv,hd,K", [(12, 2, 128, 1536), (14, 2, 64, 896), (16, 2, 128, 2048)])
 def test_linear_rope_qkv_and_cache_write(hiplib, M, nh, nkv, hd, K):
     from nanoserve_amd.kernels.linear import linear_rope_qkv
