@@ -361,8 +361,8 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const bf16_t* __restrict__ vp, int64_t s_blk, const int32_t* __restrict__ bt, int64_t bt_sb,
     const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G, int nq,
     int max_blocks, int num_blocks, float scale_log2, unsigned* __restrict__ cnt, float* __restrict__ part_acc,
-    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h) {
-  constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D, PART = ROWK_PART;
+    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h, int pp) {
+  constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D;
   // A workgroup's token row: 128 elements (256 bytes) -- all KV heads of a token (nkv_grid == 1), or one
   // KV head of hd 128 when each KV head is a row of its own (nkv_grid == n_kv, token stride s_tok).
   constexpr int NKV = 128 / HD;
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   const int nq_w = nkv_grid > 1 ? G : nq;   // query heads of this workgroup: heads g G .. g G + nq_w - 1
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
-  const int p0 = part * PART;
+  const int p0 = part * pp;   // pp <= NW PPW pages per partition
 
   // ctx, this wave's block ids (lane i < PPW holds page i's) and Q go out together
   const int ctx = ctxl[b];
@@ -414,14 +414,15 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     return;
   }
   if (p0 >= n_pages) return;
-  const int n_active = (n_pages + PART - 1) / PART;
+  const int n_active = (n_pages + pp - 1) / pp;
+  const int p_end = min(n_pages, p0 + pp);
 
   // This wave's pages are p0 + w + NW i, i < PPW. Page i's K and V sit in register slot i % D; a slot is
   // refilled with page i + D once page i is consumed. Pages past the row's end re-load the wave's first
   // page (so every path issues the same loads) and skip the arithmetic.
   int n_live = 0;
 #pragma unroll
-  for (int i = 0; i < PPW; ++i) n_live += (p0 + w + NW * i < n_pages) ? 1 : 0;
+  for (int i = 0; i < PPW; ++i) n_live += (p0 + w + NW * i < p_end) ? 1 : 0;
   rk_u32x4_t kr[D][4], vr[D][4];
   auto issue = [&](int i, auto sc) __attribute__((always_inline)) {
     constexpr int sl = decltype(sc)::value;
@@ -735,8 +736,16 @@ static inline size_t per_head_ws_bytes(int B, int n_kv_heads, int head_dim, int 
   return align256(rows * sizeof(unsigned)) + align256(slots * 16 * 2 * sizeof(float)) +
          align256(slots * 16 * size_t(head_dim) * sizeof(float));
 }
+// Pages per partition of the whole-row kernel: the fewest partitions of at most ROWK_PART pages that cover
+// the table width, made equal, so rows near the width end in partitions of one size (a 73-page table: 25,
+// 25, 23 instead of 32, 32, 9) and the longest partition, which sets the kernel's time, is as short as it
+// can be without adding partitions.
+static inline int rows_pages_per_part(int max_blocks) {
+  const int n = (max_blocks + ROWK_PART - 1) / ROWK_PART;
+  return n > 0 ? (max_blocks + n - 1) / n : ROWK_PART;
+}
 static inline size_t rows_ws_bytes(int B, int head_dim, int max_blocks) {
-  const size_t parts = size_t((max_blocks + ROWK_PART - 1) / ROWK_PART);
+  const size_t parts = size_t((max_blocks + rows_pages_per_part(max_blocks) - 1) / rows_pages_per_part(max_blocks));
   if (parts <= 1) return 0;
   return align256(size_t(B) * sizeof(unsigned)) + align256(size_t(B) * parts * 32 * sizeof(float)) +
          align256(size_t(B) * parts * 16 * size_t(head_dim) * sizeof(float));
@@ -798,7 +807,8 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
   const float sl2 = scale * LOG2E;
   const int rgh = rows_kernel_grid_heads(n_heads, n_kv_heads, head_dim, kv_spos, kv_sh, max_blocks);
   if (rgh > 0) {
-    const int rparts = (max_blocks + ROWK_PART - 1) / ROWK_PART;
+    const int rpp = rows_pages_per_part(max_blocks);
+    const int rparts = (max_blocks + rpp - 1) / rpp;
     const int rrows = B * rgh;
     unsigned* rcnt = nullptr;
     float* rml = nullptr;
@@ -824,19 +834,19 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, rgh, kv_spos, kv_sh);
+                         rml, B, rparts, rgh, kv_spos, kv_sh, rpp);
     else if (head_dim == 64)
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh);
+                         rml, B, rparts, 1, int64_t(128), kv_sh, rpp);
     else
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh);
+                         rml, B, rparts, 1, int64_t(128), kv_sh, rpp);
     return check_launch("paged_attention_decode(bf16 rows)");
   }
   const int parts = decode_parts(head_dim, max_blocks);
