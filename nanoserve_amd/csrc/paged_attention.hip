@@ -344,7 +344,8 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
 //     of its own query's head.
 //   * a wave walks PPW pages with D pages of loads in flight (register slot i % D holds page i), so the
 //     softmax and MFMA work of early pages overlaps the stream of later ones.
-//   * partitions of PART = 32 pages; a row with several merges as the per-head kernel does: 16-byte
+//   * partitions of at most PART = 32 pages, equal for the table width (pp pages each: the fewest such
+//     partitions that cover it); a row with several merges as the per-head kernel does: 16-byte
 //     coherent (sc1) stores of (m, l, acc), a wait for them, the row's counter, and the last partition
 //     to arrive loads MB partitions per round trip and folds them in partition order.
 constexpr int ROWK_NW = 4, ROWK_PPW = 8, ROWK_D = 2, ROWK_PART = ROWK_NW * ROWK_PPW;
