@@ -1023,7 +1023,9 @@ static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 // tiles: 64-row tiles of the weight (SILU: 32 gate + 32 up rows, i.e. 32 output columns).
 // Many tiles: one workgroup per tile. Fewer than twice the target: the target's worth of whole tiles,
 // and the rest cut into K slices so that the last round is spread over the GPU too. Fewer tiles than
-// the target: every tile cut into up to `chunks` slices.
+// the target: every tile cut into up to `chunks` slices. At most G_MAXC slices per tile, so the last
+// slice loads all partials in one round trip (the down projection: 8 slices of 24 tiles, 12.5 us, against
+// 13.4 us with 10 slices and 14.2 with 6).
 static Plan make_plan(int tiles, int K) {
   Plan p;
   const int T = target_workgroups();
@@ -1037,6 +1039,7 @@ static Plan make_plan(int tiles, int K) {
     const int rest = tiles - p.whole;
     const int ks = rest > 0 ? T / rest : 1;   // the sliced round fits the target (never a partial extra wave)
     p.ks = ks < 1 ? 1 : (ks > p.chunks ? p.chunks : ks);
+    if (p.ks > G_MAXC) p.ks = G_MAXC;   // the last slice loads every partial in one round trip
   }
   if (p.ks == 1) p.whole = tiles;
   p.grid = p.whole + (tiles - p.whole) * p.ks;
