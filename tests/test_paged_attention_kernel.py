@@ -96,6 +96,27 @@ def test_config2_shape_split_k(hiplib, n_heads, n_kv, hd):
     assert torch.equal(out1, out2)
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hd", [(12, 2, 128), (14, 2, 64)])
+def test_equal_partitions_of_a_73_page_table(hiplib, n_heads, n_kv, hd):
+    """BASELINE config 3's table width (73 pages): the whole-row kernel cuts it into three equal partitions
+    of 25 pages, so rows end in ragged partitions at other places than with 32-page ones. Context lengths
+    sit on and next to the 25-page (400-token) partition boundaries, inside the last page and at the full
+    width."""
+    ctx = [1, 16, 17, 399, 400, 401, 799, 800, 801, 1025, 1100, 1151, 1152, 1160, 1168, 73 * 16]
+    ctx = ctx + [1025 + 9 * i for i in range(16)]
+    q, k, v, tables, lens = make_case(n_heads, n_kv, hd, ctx, torch.bfloat16, seed=31, extra_blocks=16, width=73)
+    scale = hd ** -0.5
+    from nanoserve_amd.kernels.paged_attention import paged_attention_decode
+    dq, dk, dv, dt, dl = q.cuda(), k.cuda(), v.cuda(), tables.cuda(), lens.cuda()
+    out1 = paged_attention_decode(dq, dk, dv, dt, dl, scale).cpu()
+    out2 = paged_attention_decode(dq, dk, dv, dt, dl, scale).cpu()
+    ref = paged_attention_reference(q.float(), k.float(), v.float(), tables, lens, scale)
+    err = (out1.float() - ref).abs().max().item()
+    print(f"73-page table ({n_heads},{n_kv},{hd}) max|diff| = {err:.2e}")
+    assert err <= 1e-2
+    assert torch.equal(out1, out2)
+
+
 def test_merge_words_of_earlier_calls_are_never_taken(hiplib):
     """Several calls of one shape share the split-K workspace while each row's partition count changes
     (1 .. 8 partitions of 32 pages, table width 256): a merger must fold only this call's partials, never
