@@ -53,7 +53,11 @@ class DecodeGraphRunner:
         self.inputs: dict[int, tuple] = {}     # bucket -> (device buffer, pinned twin, device views, host views)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.outputs: dict[int, torch.Tensor] = {}
-        self.greedy: dict[int, torch.Tensor] = {}    # in-graph argmax of each row's logits (int64)
+        self._np: dict[int, tuple] = {}                # numpy views of the pinned host inputs
+        self._staged_rows: dict[int, list] = {}        # per bucket row: (block list, entries staged)
+        # in-graph argmax of each row's logits (int64), written by the kernel straight into pinned host
+        # memory: reading it after the step's synchronisation needs no device-to-host copy
+        self.greedy: dict[int, torch.Tensor] = {}
         self.mempool = None
 
     @property
@@ -92,7 +96,15 @@ class DecodeGraphRunner:
     def _reset_to_padding(self, B: int) -> None:
         dev, host, _, hv = self._buffers(B)
         self._fill_padding(hv, 0)
+        self._staged_rows[B] = [None] * B
         dev.copy_(host)
+
+    def _host_np(self, B: int) -> tuple:
+        """numpy views of bucket B's pinned host inputs (list assignment into them skips torch.tensor)."""
+        if B not in self._np:
+            self._np[B] = tuple(v.numpy() for v in self._buffers(B)[3])
+            self._staged_rows.setdefault(B, [None] * B)
+        return self._np[B]
 
     def _forward(self, B: int) -> tuple[torch.Tensor, torch.Tensor]:
         from nanoserve_amd.kernels.sampling import argmax_rows
@@ -101,7 +113,9 @@ class DecodeGraphRunner:
         seqs = [SeqInput(1, ctx_len=1, use_kernel=True)] * B
         logits = self.model.forward_batch(tokens, positions, seqs, logits="all", paged=self.pool,
                                           slot_mapping=slots, decode_meta=meta)
-        return logits, argmax_rows(logits)
+        if B not in self.greedy:
+            self.greedy[B] = torch.empty(B, dtype=torch.int64, pin_memory=True)
+        return logits, argmax_rows(logits, self.greedy[B])
 
     def _capture(self, B: int) -> None:
         # warm-up and capture run on padding inputs only, so they cannot overwrite real K/V
@@ -116,8 +130,8 @@ class DecodeGraphRunner:
             self.mempool = torch.cuda.graph_pool_handle()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self.mempool):
-            out, greedy = self._forward(B)
-        self.graphs[B], self.outputs[B], self.greedy[B] = graph, out, greedy
+            out, _ = self._forward(B)
+        self.graphs[B], self.outputs[B] = graph, out
 
     def stage(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
               context_lens: list[int]) -> int:
@@ -131,12 +145,26 @@ class DecodeGraphRunner:
         for t in block_tables:
             if len(t) > W:
                 raise ValueError(f"block table of {len(t)} blocks exceeds the graph width {W} (max_seq_len)")
-        dev, host, _, (ht, hp, hs, hl, hb) = self._buffers(B)
-        ht[:n] = torch.tensor(tokens, dtype=torch.long)
-        hp[:n] = torch.tensor(positions, dtype=torch.long)
-        hs[:n] = torch.tensor(slots, dtype=torch.long)
-        hl[:n] = torch.tensor(context_lens, dtype=torch.int32)
-        hb[:n] = torch.tensor([t + [0] * (W - len(t)) for t in block_tables], dtype=torch.int32)
+        dev, host, _, _ = self._buffers(B)
+        ht, hp, hs, hl, hb = self._host_np(B)
+        ht[:n] = tokens
+        hp[:n] = positions
+        hs[:n] = slots
+        hl[:n] = context_lens
+        # Table rows: a block list only grows between steps (every other change rebinds the sequence's
+        # list), so a row whose list is the one staged last time needs only its new tail written.
+        staged = self._staged_rows[B]
+        for i, t in enumerate(block_tables):
+            c, L = staged[i], len(t)
+            if c is not None and c[0] is t and c[1] <= L:
+                if c[1] < L:
+                    hb[i, c[1]:L] = t[c[1]:L]
+            else:
+                hb[i, :L] = t
+                hb[i, L:] = 0
+            staged[i] = (t, L)
+        for i in range(n, B):
+            staged[i] = None
         self._fill_padding((ht, hp, hs, hl, hb), n)
         dev.copy_(host, non_blocking=True)
         return B
@@ -159,7 +187,9 @@ class DecodeGraphRunner:
         return self.outputs[B][:n]
 
     def greedy_tokens(self, n: int) -> list[int]:
-        """Argmax of the first n rows of the last replay (computed inside the graph): one 8n-byte copy."""
+        """Argmax of the first n rows of the last replay (computed inside the graph into pinned host memory):
+        waits for the replay, then reads the host buffer."""
+        torch.cuda.current_stream().synchronize()
         return self.greedy[self.last_bucket][:n].tolist()
 
     @torch.inference_mode()

@@ -25,7 +25,8 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
 
 
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """logits [R, V] (last dim contiguous) -> int64 [R]."""
+    """logits [R, V] (last dim contiguous) -> int64 [R]. `out` may be pinned host memory (the kernel writes
+    it over the bus; read it after synchronising the stream)."""
     assert logits.dim() == 2 and logits.stride(1) == 1
     _lib.require_gpu(logits)
     R, V = logits.shape
