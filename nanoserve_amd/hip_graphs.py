@@ -53,8 +53,11 @@ class DecodeGraphRunner:
         self.inputs: dict[int, tuple] = {}     # bucket -> (device buffer, pinned twin, device views, host views)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.outputs: dict[int, torch.Tensor] = {}
-        self._np: dict[int, tuple] = {}                # numpy views of the pinned host inputs
-        self._staged_rows: dict[int, list] = {}        # per bucket row: (block list, entries staged)
+        self._np: dict[tuple, tuple] = {}              # numpy views of the pinned host inputs
+        self._staged_rows: dict[tuple, list] = {}      # per (bucket, buffer) row: (block list, entries staged)
+        self._host2: dict[int, torch.Tensor] = {}      # second pinned host buffer per bucket
+        self._par: dict[int, int] = {}                 # host buffer of the bucket's last staged step
+        self._pending = None                           # (bucket, buffer, rows) of a prestaged step
         # in-graph argmax of each row's logits (int64), written by the kernel straight into pinned host
         # memory: reading it after the step's synchronisation needs no device-to-host copy
         self.greedy: dict[int, torch.Tensor] = {}
@@ -96,15 +99,24 @@ class DecodeGraphRunner:
     def _reset_to_padding(self, B: int) -> None:
         dev, host, _, hv = self._buffers(B)
         self._fill_padding(hv, 0)
-        self._staged_rows[B] = [None] * B
+        self._staged_rows[(B, 0)] = [None] * B
         dev.copy_(host)
 
-    def _host_np(self, B: int) -> tuple:
-        """numpy views of bucket B's pinned host inputs (list assignment into them skips torch.tensor)."""
-        if B not in self._np:
-            self._np[B] = tuple(v.numpy() for v in self._buffers(B)[3])
-            self._staged_rows.setdefault(B, [None] * B)
-        return self._np[B]
+    def _host_buf(self, B: int, par: int) -> torch.Tensor:
+        """Pinned host buffer `par` (0 or 1) of bucket B."""
+        if par == 0:
+            return self._buffers(B)[1]
+        if B not in self._host2:
+            self._host2[B] = torch.zeros_like(self._buffers(B)[1], pin_memory=True)
+            self._fill_padding(self._views(self._host2[B], B), 0)
+        return self._host2[B]
+
+    def _host_np(self, B: int, par: int = 0) -> tuple:
+        """numpy views of bucket B's pinned host buffer `par` (list assignment into them skips torch.tensor)."""
+        if (B, par) not in self._np:
+            self._np[(B, par)] = tuple(v.numpy() for v in self._views(self._host_buf(B, par), B))
+            self._staged_rows.setdefault((B, par), [None] * B)
+        return self._np[(B, par)]
 
     def _forward(self, B: int) -> tuple[torch.Tensor, torch.Tensor]:
         from nanoserve_amd.kernels.sampling import argmax_rows
@@ -133,27 +145,23 @@ class DecodeGraphRunner:
             out, _ = self._forward(B)
         self.graphs[B], self.outputs[B] = graph, out
 
-    def stage(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
-              context_lens: list[int]) -> int:
-        """Write one step's inputs into the static buffers (padding rows point at the garbage block);
-        returns the bucket."""
-        n = len(tokens)
-        B = self.bucket_for(n)
-        if B is None:
-            raise ValueError(f"batch of {n} exceeds the largest graph bucket ({self.max_bucket})")
+    def _stage_host(self, B: int, par: int, tokens: list[int] | None, positions: list[int], slots: list[int],
+                    block_tables: list[list[int]], context_lens: list[int]) -> None:
+        """Write one step's inputs into pinned host buffer `par` of bucket B (tokens None: left for later)."""
+        n = len(positions)
         W = self.max_blocks
         for t in block_tables:
             if len(t) > W:
                 raise ValueError(f"block table of {len(t)} blocks exceeds the graph width {W} (max_seq_len)")
-        dev, host, _, _ = self._buffers(B)
-        ht, hp, hs, hl, hb = self._host_np(B)
-        ht[:n] = tokens
+        ht, hp, hs, hl, hb = self._host_np(B, par)
+        if tokens is not None:
+            ht[:n] = tokens
         hp[:n] = positions
         hs[:n] = slots
         hl[:n] = context_lens
         # Table rows: a block list only grows between steps (every other change rebinds the sequence's
         # list), so a row whose list is the one staged last time needs only its new tail written.
-        staged = self._staged_rows[B]
+        staged = self._staged_rows[(B, par)]
         for i, t in enumerate(block_tables):
             c, L = staged[i], len(t)
             if c is not None and c[0] is t and c[1] <= L:
@@ -166,8 +174,48 @@ class DecodeGraphRunner:
         for i in range(n, B):
             staged[i] = None
         self._fill_padding((ht, hp, hs, hl, hb), n)
-        dev.copy_(host, non_blocking=True)
+
+    def _bucket(self, n: int) -> int:
+        B = self.bucket_for(n)
+        if B is None:
+            raise ValueError(f"batch of {n} exceeds the largest graph bucket ({self.max_bucket})")
         return B
+
+    def stage(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
+              context_lens: list[int]) -> int:
+        """Write one step's inputs into the static buffers (padding rows point at the garbage block);
+        returns the bucket. The pinned host side alternates between two buffers, so a step can be staged
+        while the previous step's copy may still be reading the other one."""
+        B = self._bucket(len(tokens))
+        par = self._par.get(B, 1) ^ 1
+        self._par[B] = par
+        self._stage_host(B, par, tokens, positions, slots, block_tables, context_lens)
+        self._buffers(B)[0].copy_(self._host_buf(B, par), non_blocking=True)
+        return B
+
+    def prestage(self, positions: list[int], slots: list[int], block_tables: list[list[int]],
+                 context_lens: list[int]) -> int:
+        """Stage the next step's inputs except its tokens (unknown until the running step ends) into the
+        host buffer the running step does not use; launch_prestaged() adds the tokens and replays."""
+        B = self._bucket(len(positions))
+        par = self._par.get(B, 1) ^ 1
+        self._stage_host(B, par, None, positions, slots, block_tables, context_lens)
+        self._pending = (B, par, len(positions))
+        return B
+
+    @torch.inference_mode()
+    def launch_prestaged(self, tokens: list[int]) -> torch.Tensor:
+        """Complete the prestaged step with its tokens, copy it in and replay its bucket's graph (the caller
+        has waited for the previous step); returns the logits view as run() does."""
+        B, par, n = self._pending
+        self._pending = None
+        assert len(tokens) == n and B in self.graphs
+        self._host_np(B, par)[0][:n] = tokens
+        self._par[B] = par
+        self._buffers(B)[0].copy_(self._host_buf(B, par), non_blocking=True)
+        self.graphs[B].replay()
+        self.last_bucket = B
+        return self.outputs[B][:n]
 
     @torch.inference_mode()
     def run(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
@@ -180,7 +228,7 @@ class DecodeGraphRunner:
             raise ValueError(f"batch of {n} exceeds the largest graph bucket ({self.max_bucket})")
         if B not in self.graphs:
             self._capture(B)
-        torch.cuda.current_stream().synchronize()   # the pinned staging buffers are reused every step
+        torch.cuda.current_stream().synchronize()   # a pinned staging buffer is reused every other step
         self.stage(tokens, positions, slots, block_tables, context_lens)
         self.graphs[B].replay()
         self.last_bucket = B

@@ -393,3 +393,50 @@ def test_engine_rejects_the_oracle_only_backends(hiplib):
     for kw in ({"attn_backend": "sdpa"}, {"fused_ops": False}, {"kv_cache": "contiguous"}):
         with pytest.raises(ValueError):
             LLMEngine(model, [], max_seq_len=256, kv_cache_tokens=1024, **kw)
+
+
+def test_overlapped_host_staging_matches_plain_steps(hiplib):
+    """Steady greedy decode stages the next step while the current one runs and relaunches the graph right
+    after the wait. Every request's tokens and finish must equal the engine's with that off: requests
+    finishing by length at different steps, one finishing on an EOS token, one aborted while a prelaunched
+    step is in flight, and a request arriving mid-run (admitted at most one step later: the step already in
+    flight when it arrives runs first). Until that arrival the outputs agree step for step."""
+    model, _ = gpu_model(SMALL, torch.bfloat16, seed=7)
+    ps = prompts(6, 40, SMALL.vocab_size, seed=8)
+
+    def drive(overlap: bool, eos: list[int]):
+        from nanoserve_amd.engine import LLMEngine
+        eng = LLMEngine(model, eos, max_seq_len=256, max_num_seqs=8, batch_wait_s=0.0, kv_cache_tokens=8192)
+        eng.overlap_host = overlap
+        ids = [eng.add_request(p, n, ignore_eos=(i != 2)) for i, (p, n) in enumerate(zip(ps[:5], [30, 12, 40, 25, 33]))]
+        log, prelaunched, steps = [], 0, 0
+        while eng.has_unfinished():
+            if steps == 9:
+                eng.abort(ids[3])
+            if steps == 15:
+                ids.append(eng.add_request(ps[5], 10, ignore_eos=True))
+            log.append([(o.seq_id, o.token, o.finished) for o in eng.step()])
+            prelaunched += eng._pre is not None
+            steps += 1
+        assert eng.kv.num_free_blocks == eng.kv.alloc.num_free and not eng.sequences
+        return log, prelaunched
+
+    plain, _ = drive(False, [])
+    # an EOS id request 2 produces at its 20th token (it alone does not ignore EOS)
+    out2 = [t for step in plain for (sid, t, _) in step if sid == 2]
+    eos = [out2[19]] if len(out2) > 19 and out2[19] not in out2[:19] else []
+    plain, n0 = drive(False, eos)
+    fast, n1 = drive(True, eos)
+    assert n0 == 0 and n1 > 10
+    assert fast[:15] == plain[:15]
+
+    def streams(log):
+        toks, fin = {}, {}
+        for k, step in enumerate(log):
+            for sid, t, f in step:
+                toks.setdefault(sid, []).append(t)
+                fin.setdefault(sid, (k, f)) if f else None
+        return toks, fin
+    (ta, fa), (tb, fb) = streams(fast), streams(plain)
+    assert ta == tb and fa.keys() == fb.keys()
+    assert all(0 <= fa[s][0] - fb[s][0] <= 1 for s in fa)
