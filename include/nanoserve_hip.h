@@ -28,6 +28,11 @@ extern "C" {
 #define NS_DTYPE_F32 0
 #define NS_DTYPE_BF16 1
 
+/* Split-K workspaces (ns_paged_attn_decode, ns_paged_attn_prefill, ns_argmax_rows) begin with this many
+ * bytes of arrival counters. Every call leaves them at zero and nothing else is ever stored there, so one
+ * zero-filled workspace may serve calls of any shape, in any order, on one stream. */
+#define NS_WS_COUNTER_BYTES (256u << 10)
+
 #define NS_OK 0
 #define NS_E_INVALID 1      /* argument outside what the kernels support (message says which) */
 #define NS_E_WORKSPACE 2    /* workspace pointer missing or smaller than ns_decode_workspace_bytes */
@@ -54,9 +59,11 @@ const char* ns_version(void);
  * Long contexts are split into partitions that run in parallel (split-K); in the same launch the last
  * partition of a row to finish merges their partial softmax states in partition order. That needs
  * `workspace` of at least ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype) bytes
- * (256-byte aligned, zero-filled once by the owner: it starts with per-row arrival counters, which every
- * call leaves at zero; 0 bytes means none is needed). Calls sharing a workspace must be ordered (same
- * stream), which every caller in the decode loop is.
+ * (256-byte aligned, zero-filled once by the owner: it starts with the NS_WS_COUNTER_BYTES counter region,
+ * which every call leaves at zero; 0 bytes means none is needed). Calls of any shape may share one
+ * workspace if they are ordered (same stream), which every caller in the decode loop is. A row's
+ * partitions are fixed runs of pages (32 for the whole-row kernel, 16 / 8 for hd 64 / 128 otherwise), so
+ * the result depends on the row's context and pages only, not on the table width.
  */
 int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                          const void* k_pool, const void* v_pool,
@@ -91,8 +98,9 @@ size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_bl
  * Long contexts split a query tile's keys over several workgroups; in the same launch the last of them
  * merges the partial softmax states in order. That needs `workspace` of at least
  * ns_prefill_workspace_bytes(n_seqs, n_heads, head_dim, max_new, max_kv) bytes (256-byte aligned,
- * zero-filled once by the owner: it starts with arrival counters, which every call leaves at zero; 0 bytes
- * means none is needed). Calls sharing a workspace must be ordered (same stream).
+ * zero-filled once by the owner: it starts with the NS_WS_COUNTER_BYTES counter region, which every call
+ * leaves at zero; 0 bytes means none is needed). Calls of any shape may share one workspace if they are
+ * ordered (same stream).
  */
 int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh,
                           const void* k_pool, const void* v_pool,
@@ -224,8 +232,9 @@ int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void*
  * ld elements); NaN ranks above every number (torch.argmax semantics). int64 output.
  * Replaces logits.argmax(-1) of nanoserve/engine.py:239 / sampling.py:59-60.
  * workspace (optional, zero-initialised once by the caller, 256-byte aligned, at least
- * ns_argmax_workspace_bytes(rows, n) bytes): rows are split over several workgroups merged in the same
- * launch; every call leaves the workspace's counters at zero. NULL: one workgroup per row.
+ * ns_argmax_workspace_bytes(rows, n) bytes, which is 0 above 65,536 rows): rows are split over several
+ * workgroups merged in the same launch; every call leaves the counter region at zero, so calls with any row
+ * count may share one workspace. NULL: one workgroup per row.
  */
 size_t ns_argmax_workspace_bytes(int64_t rows, int n);
 int ns_argmax_rows(const void* x, int64_t ld, int64_t rows, int n, int dtype, int64_t* out, void* workspace,

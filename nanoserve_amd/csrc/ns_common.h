@@ -97,6 +97,13 @@ __device__ __forceinline__ void acquire_published() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Split-K workspaces (decode and prefill attention, argmax) start with a fixed region of arrival counters,
+// one 32-bit word per merged unit. Only the counter protocol (increment, reset by the last arriver) ever
+// touches it, so every call leaves it zero and calls of different shapes can share one buffer; the
+// partial results of any call start after it.
+constexpr size_t WS_COUNTER_BYTES = size_t(NS_WS_COUNTER_BYTES);
+constexpr int WS_MAX_COUNTERS = int(WS_COUNTER_BYTES / 4);
+
 // Host side: error slot and launch checking.
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);

@@ -344,8 +344,8 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
 //     of its own query's head.
 //   * a wave walks PPW pages with D pages of loads in flight (register slot i % D holds page i), so the
 //     softmax and MFMA work of early pages overlaps the stream of later ones.
-//   * partitions of at most PART = 32 pages, equal for the table width (pp pages each: the fewest such
-//     partitions that cover it); a row with several merges as the per-head kernel does: 16-byte
+//   * partitions of PART = 32 pages (the last one of a row shorter), so a row's split depends on its own
+//     context length only, never on the table width; a row with several merges as the per-head kernel does: 16-byte
 //     coherent (sc1) stores of (m, l, acc), a wait for them, the row's counter, and the last partition
 //     to arrive loads MB partitions per round trip and folds them in partition order.
 constexpr int ROWK_NW = 4, ROWK_PPW = 8, ROWK_D = 2, ROWK_PART = ROWK_NW * ROWK_PPW;
@@ -362,7 +362,8 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const bf16_t* __restrict__ vp, int64_t s_blk, const int32_t* __restrict__ bt, int64_t bt_sb,
     const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G, int nq,
     int max_blocks, int num_blocks, float scale_log2, unsigned* __restrict__ cnt, float* __restrict__ part_acc,
-    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h, int pp) {
+    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h) {
+  constexpr int pp = ROWK_PART;
   constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D;
   // A workgroup's token row: 128 elements (256 bytes) -- all KV heads of a token (nkv_grid == 1), or one
   // KV head of hd 128 when each KV head is a row of its own (nkv_grid == n_kv, token stride s_tok).
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   const int nq_w = nkv_grid > 1 ? G : nq;   // query heads of this workgroup: heads g G .. g G + nq_w - 1
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
-  const int p0 = part * pp;   // pp <= NW PPW pages per partition
+  const int p0 = part * pp;
 
   // ctx, this wave's block ids (lane i < PPW holds page i's) and Q go out together
   const int ctx = ctxl[b];
@@ -734,27 +735,19 @@ static inline size_t per_head_ws_bytes(int B, int n_kv_heads, int head_dim, int 
   const size_t parts = size_t(decode_parts(head_dim, max_blocks));
   if (parts <= 1) return 0;
   const size_t rows = size_t(B) * n_kv_heads, slots = rows * parts;
-  return align256(rows * sizeof(unsigned)) + align256(slots * 16 * 2 * sizeof(float)) +
-         align256(slots * 16 * size_t(head_dim) * sizeof(float));
+  return WS_COUNTER_BYTES + align256(slots * 16 * 2 * sizeof(float)) + align256(slots * 16 * size_t(head_dim) * sizeof(float));
 }
-// Pages per partition of the whole-row kernel: the fewest partitions of at most ROWK_PART pages that cover
-// the table width, made equal, so rows near the width end in partitions of one size (a 73-page table: 25,
-// 25, 23 instead of 32, 32, 9) and the longest partition, which sets the kernel's time, is as short as it
-// can be without adding partitions.
-static inline int rows_pages_per_part(int max_blocks) {
-  const int n = (max_blocks + ROWK_PART - 1) / ROWK_PART;
-  return n > 0 ? (max_blocks + n - 1) / n : ROWK_PART;
-}
+static inline int rows_parts(int max_blocks) { return (max_blocks + ROWK_PART - 1) / ROWK_PART; }
 static inline size_t rows_ws_bytes(int B, int head_dim, int max_blocks) {
-  const size_t parts = size_t((max_blocks + rows_pages_per_part(max_blocks) - 1) / rows_pages_per_part(max_blocks));
+  const size_t parts = size_t(rows_parts(max_blocks));
   if (parts <= 1) return 0;
-  return align256(size_t(B) * sizeof(unsigned)) + align256(size_t(B) * parts * 32 * sizeof(float)) +
+  return WS_COUNTER_BYTES + align256(size_t(B) * parts * 32 * sizeof(float)) +
          align256(size_t(B) * parts * 16 * size_t(head_dim) * sizeof(float));
 }
 
-// Workspace: arrival counters at offset 0 (zeroed once by the owner; every launch leaves them at zero),
-// then the partitions' (m, l) and accumulators. Sized for whichever kernel the shape takes; both follow
-// the same publish-then-count protocol, so one buffer may serve calls of either.
+// Workspace: WS_COUNTER_BYTES of per-row arrival counters at offset 0 (zeroed once by the owner; every
+// launch leaves them at zero, and no launch stores anything else there, so calls of any shape may share
+// one buffer), then the partitions' (m, l) and accumulators. Sized for whichever kernel the shape takes.
 extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype) {
   if (dtype != NS_DTYPE_BF16 || B <= 0 || n_kv_heads <= 0 || max_blocks <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
@@ -764,12 +757,12 @@ extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim,
   return a > r ? a : r;
 }
 
-extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,
-                                    const void* v_pool, int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
-                                    const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
-                                    void* out, int64_t o_sb, int64_t o_sh, int B, int n_heads, int n_kv_heads,
-                                    int head_dim, int block_size, int max_blocks, int num_blocks, float scale,
-                                    int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool, const void* v_pool,
+                               int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh, const int32_t* block_tables,
+                               int64_t bt_sb, const int32_t* context_lens, void* out, int64_t o_sb, int64_t o_sh, int B,
+                               int n_heads, int n_kv_heads, int head_dim, int block_size, int max_blocks,
+                               int num_blocks, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                               void* stream) {
   NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "paged_attention_decode: dtype %d not supported",
              dtype);
   NS_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention_decode: head_dim %d not in {64, 128}", head_dim);
@@ -808,9 +801,10 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
   const float sl2 = scale * LOG2E;
   const int rgh = rows_kernel_grid_heads(n_heads, n_kv_heads, head_dim, kv_spos, kv_sh, max_blocks);
   if (rgh > 0) {
-    const int rpp = rows_pages_per_part(max_blocks);
-    const int rparts = (max_blocks + rpp - 1) / rpp;
+    const int rparts = rows_parts(max_blocks);
     const int rrows = B * rgh;
+    NS_REQUIRE(rrows <= WS_MAX_COUNTERS, "paged_attention_decode: %d rows x KV heads exceed %d", rrows,
+               WS_MAX_COUNTERS);
     unsigned* rcnt = nullptr;
     float* rml = nullptr;
     float* racc = nullptr;
@@ -825,9 +819,8 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                  "paged_attention_decode: workspace not 256-byte aligned");
       char* w = static_cast<char*>(workspace);
       rcnt = reinterpret_cast<unsigned*>(w);
-      rml = reinterpret_cast<float*>(w + align256(size_t(rrows) * sizeof(unsigned)));
-      racc = reinterpret_cast<float*>(w + align256(size_t(rrows) * sizeof(unsigned)) +
-                                      align256(size_t(rrows) * rparts * 32 * sizeof(float)));
+      rml = reinterpret_cast<float*>(w + WS_COUNTER_BYTES);
+      racc = reinterpret_cast<float*>(w + WS_COUNTER_BYTES + align256(size_t(rrows) * rparts * 32 * sizeof(float)));
     }
     const dim3 rgrid(unsigned(rparts) * unsigned(rrows));
     if (rgh > 1)
@@ -835,19 +828,19 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, rgh, kv_spos, kv_sh, rpp);
+                         rml, B, rparts, rgh, kv_spos, kv_sh);
     else if (head_dim == 64)
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh, rpp);
+                         rml, B, rparts, 1, int64_t(128), kv_sh);
     else
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh, rpp);
+                         rml, B, rparts, 1, int64_t(128), kv_sh);
     return check_launch("paged_attention_decode(bf16 rows)");
   }
   const int parts = decode_parts(head_dim, max_blocks);
@@ -866,10 +859,12 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
     }
     NS_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "paged_attention_decode: workspace not 256-byte aligned");
     const size_t rows = size_t(B) * n_kv_heads, slots = rows * parts;
+    NS_REQUIRE(rows <= size_t(WS_MAX_COUNTERS), "paged_attention_decode: %zu rows x KV heads exceed %d", rows,
+               WS_MAX_COUNTERS);
     char* w = static_cast<char*>(workspace);
     ws_cnt = reinterpret_cast<unsigned*>(w);
-    ws_ml = reinterpret_cast<float*>(w + align256(rows * sizeof(unsigned)));
-    ws_acc = reinterpret_cast<float*>(w + align256(rows * sizeof(unsigned)) + align256(slots * 16 * 2 * sizeof(float)));
+    ws_ml = reinterpret_cast<float*>(w + WS_COUNTER_BYTES);
+    ws_acc = reinterpret_cast<float*>(w + WS_COUNTER_BYTES + align256(slots * 16 * 2 * sizeof(float)));
   }
   const dim3 grid(unsigned(parts) * unsigned(n_kv_heads) * unsigned(B));
   if (head_dim == 64)
@@ -885,4 +880,15 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
                        static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, ws_cnt, B,
                        n_kv_heads, parts);
   return check_launch("paged_attention_decode(bf16)");
+}
+
+extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,
+                                    const void* v_pool, int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                                    const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                                    void* out, int64_t o_sb, int64_t o_sh, int B, int n_heads, int n_kv_heads,
+                                    int head_dim, int block_size, int max_blocks, int num_blocks, float scale,
+                                    int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
+                             context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
+                             num_blocks, scale, dtype, workspace, workspace_bytes, stream);
 }

@@ -449,8 +449,9 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 using namespace ns;
 
-// Workspace: [n_seqs * n_heads * tiles] arrival counters, then per work unit the (m, l) and the
-// accumulators of a tile's partition. Zero bytes when no tile can span more than one partition.
+// Workspace: the fixed counter region (one arrival counter per tile of [n_seqs, n_heads, tiles]; shared
+// safely by calls of any shape), then per work unit the (m, l) and the accumulators of a tile's partition.
+// Zero bytes when no tile can span more than one partition.
 extern "C" size_t ns_prefill_workspace_bytes(int n_seqs, int n_heads, int head_dim, int max_new, int max_kv) {
   if (n_seqs <= 0 || n_heads <= 0 || max_new <= 0 || max_kv <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
@@ -458,7 +459,7 @@ extern "C" size_t ns_prefill_workspace_bytes(int n_seqs, int n_heads, int head_d
   if (parts <= 1) return 0;
   const size_t tiles = size_t((max_new + PF_QT - 1) / PF_QT) * n_seqs * n_heads;
   const size_t units = tiles * parts;
-  return align256(tiles * sizeof(unsigned)) + align256(units * PF_R * 2 * PF_THREADS * sizeof(float)) +
+  return WS_COUNTER_BYTES + align256(units * PF_R * 2 * PF_THREADS * sizeof(float)) +
          align256(units * PF_R * (head_dim / 16) * 4 * PF_THREADS * sizeof(float));
 }
 
@@ -503,11 +504,12 @@ extern "C" int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh, 
     }
     NS_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "paged_attention_prefill: workspace not 256-byte aligned");
     const size_t ntile = size_t(tiles) * n_seqs * n_heads, units = ntile * parts;
+    NS_REQUIRE(ntile <= size_t(WS_MAX_COUNTERS), "paged_attention_prefill: %zu query tiles x heads exceed %d",
+               ntile, WS_MAX_COUNTERS);
     char* wsb = static_cast<char*>(workspace);
     cnt = reinterpret_cast<unsigned*>(wsb);
-    ws_ml = reinterpret_cast<float*>(wsb + align256(ntile * sizeof(unsigned)));
-    ws_acc = reinterpret_cast<float*>(wsb + align256(ntile * sizeof(unsigned)) +
-                                      align256(units * PF_R * 2 * PF_THREADS * sizeof(float)));
+    ws_ml = reinterpret_cast<float*>(wsb + WS_COUNTER_BYTES);
+    ws_acc = reinterpret_cast<float*>(wsb + WS_COUNTER_BYTES + align256(units * PF_R * 2 * PF_THREADS * sizeof(float)));
   }
   PrefillArgs a{static_cast<const bf16_t*>(q), q_st, q_sh, static_cast<const bf16_t*>(k_pool),
                 static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, seq_info,

@@ -203,9 +203,11 @@ static int argmax_splits(int64_t rows, int n) {
 
 using namespace ns;
 
+// Workspace: the fixed counter region (one arrival counter per row; shared safely by calls with any row
+// count), then each row's per-split (value, index) partials.
 extern "C" size_t ns_argmax_workspace_bytes(int64_t rows, int n) {
-  if (rows <= 0 || n <= 0) return 0;
-  return ((size_t(rows) * sizeof(unsigned) + 255) & ~size_t(255)) + size_t(rows) * AM_MAX_SPLITS * 8;
+  if (rows <= 0 || n <= 0 || rows > WS_MAX_COUNTERS) return 0;
+  return WS_COUNTER_BYTES + size_t(rows) * AM_MAX_SPLITS * 8;
 }
 
 extern "C" int ns_argmax_rows(const void* x, int64_t ld, int64_t rows, int n, int dtype, int64_t* out, void* workspace,
@@ -218,13 +220,12 @@ extern "C" int ns_argmax_rows(const void* x, int64_t ld, int64_t rows, int n, in
   const int esz = dtype == NS_DTYPE_BF16 ? 2 : 4;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ld * esz) % 16 == 0;
   const int splits = argmax_splits(rows, n);
-  if (workspace != nullptr && aligned && splits > 1 && rows <= (int64_t(1) << 24)) {
+  if (workspace != nullptr && aligned && splits > 1 && rows <= WS_MAX_COUNTERS) {
     NS_REQUIRE(workspace_bytes >= ns_argmax_workspace_bytes(rows, n) && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
                "argmax_rows: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed, got %zu",
                ns_argmax_workspace_bytes(rows, n), workspace_bytes);
     unsigned* cnt = static_cast<unsigned*>(workspace);
-    uint32_t* part = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
-                                                 ((size_t(rows) * sizeof(unsigned) + 255) & ~size_t(255)));
+    uint32_t* part = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
     const dim3 grid(unsigned(rows * splits));
     if (dtype == NS_DTYPE_BF16)
       hipLaunchKernelGGL(argmax_split_kernel<bf16_t>, grid, dim3(AM_THREADS), 0, s, static_cast<const bf16_t*>(x), ld,

@@ -90,6 +90,7 @@ def prefill_seq_info(q_starts: list[int], n_new: list[int], ctx_lens: list[int],
 
 
 _PREFILL_WS: dict[int, torch.Tensor] = {}
+_PREFILL_WS_RETIRED: list[torch.Tensor] = []   # superseded buffers stay alive: captured graphs may point at them
 
 
 def prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
@@ -101,6 +102,8 @@ def prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     if ws is None or ws.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("paged_attention_prefill: workspace must be sized by an eager call before capture")
+        if ws is not None:
+            _PREFILL_WS_RETIRED.append(ws)
         # zero-filled: the kernel's arrival counters start at zero and every call leaves them there
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _PREFILL_WS[idx] = ws

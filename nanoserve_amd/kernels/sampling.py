@@ -8,6 +8,10 @@ from nanoserve_amd import _lib
 
 
 _WS: dict[int, torch.Tensor] = {}
+# Superseded workspaces stay alive: a captured graph keeps the address it was recorded with, and replays
+# must not write counters into memory the caching allocator has handed to someone else.
+_WS_RETIRED: list[torch.Tensor] = []
+_WS_MIN_ROWS = 256      # the first buffer already covers every decode-graph bucket (at most 128 rows)
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
@@ -19,7 +23,10 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     if ws is None or ws.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             return None
-        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        floor = _lib.lib().ns_argmax_workspace_bytes(_WS_MIN_ROWS, 1 << 20)
+        if ws is not None:
+            _WS_RETIRED.append(ws)
+        ws = torch.zeros(max(nbytes, floor, 1 << 16), dtype=torch.uint8, device=device)
         _WS[idx] = ws
     return ws
 

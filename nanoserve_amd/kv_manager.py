@@ -45,6 +45,13 @@ class PagedKVManager:
     def num_free_blocks(self) -> int:
         return self.alloc.num_free
 
+    def refcount(self, block: int) -> int:
+        """How many block tables hold `block` (1 for an allocated block without prefix caching)."""
+        ref = getattr(self.alloc, "ref", None)
+        if ref is not None:
+            return ref.get(block, 0)
+        return int(block in self.alloc._used)
+
     def _blocks_for(self, n_tokens: int) -> int:
         return math.ceil(n_tokens / self.block_size)
 

@@ -1,0 +1,289 @@
+"""Correctness at the BASELINE configurations' own shapes (the headline decode step included).
+
+Config 3 (1.5B shape, bf16, B=32, 1024-token prompts, bucket-32 graph): the graph step equals the eager
+forward bitwise (the reference's tests/test_cuda_graphs.py:58-64 gate at the exact bucket); 128 greedy steps
+give identical streams with the one-step-ahead launch on, off, and with graphs off; logits are finite. The
+same shape with fewer layers is checked against the fp32 CPU oracle on the same bf16 weights under the
+approved tie rule (tests/test_llm_engine.py:17,72-87).
+Config 4 (a 1536-token chunk on 512 cached tokens plus 16 decode rows, one 1552-row step): the chunked-
+prefill kernel path against the same step with every prefill token as a decode row, and both against the
+oracle, at reduced layers.
+Config 5 (3B shape, 1024-token shared prefix, 211-token suffixes, 32 requests): the shared blocks sit at the
+head of every table with refcount 32, and the streams with and without prefix caching follow the oracle
+under the tie rule, at reduced layers.
+"""
+import dataclasses
+import random
+
+import pytest
+import torch
+
+from nanoserve_amd.model import QWEN25_1_5B, QWEN25_3B, DecodeMeta, Qwen2Model, SeqInput, random_state_dict
+from oracle.model import OracleModel
+
+pytestmark = pytest.mark.gpu
+
+TIE_GAP_BF16 = 0.25
+
+
+def prompts(n, length, vocab, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randint(0, vocab, (length,), generator=g).tolist() for _ in range(n)]
+
+
+def first_divergence(a, b):
+    return next((k for k in range(min(len(a), len(b))) if a[k] != b[k]), None)
+
+
+def check_tie_rule(ours, ref, ref_logits, label):
+    same = 0
+    for i, (a, b) in enumerate(zip(ours, ref)):
+        j = first_divergence(a, b)
+        if j is None:
+            same += 1
+            continue
+        top2 = ref_logits[i][j].float().topk(2).values
+        gap = (top2[0] - top2[1]).item()
+        print(f"{label}: request {i} diverges at token {j}, oracle top-2 gap {gap:.3e}")
+        assert gap <= TIE_GAP_BF16, f"{label}: request {i} diverged at {j} with a top-2 gap of {gap}"
+    print(f"{label}: {same}/{len(ours)} streams identical to the fp32 oracle")
+
+
+def run_engine(eng, reqs, waves=None, on_step=None):
+    """Add requests (optionally in waves (step, count)) and step until done; tokens per request."""
+    outs, idx, steps = {}, {}, 0
+    pending = list(waves) if waves else [(0, len(reqs))]
+    while pending or eng.has_unfinished():
+        while pending and steps >= pending[0][0]:
+            _, end = pending.pop(0)
+            for i in range(len(idx), end):
+                p, n = reqs[i]
+                idx[eng.add_request(p, n, ignore_eos=True)] = i
+                outs[i] = []
+        for o in eng.step():
+            outs[idx[o.seq_id]].append(o.token)
+        if on_step is not None:
+            on_step(eng, steps)
+        steps += 1
+    return [outs[i] for i in range(len(reqs))]
+
+
+def engine(model, **kw):
+    from nanoserve_amd.engine import LLMEngine
+    args = dict(max_seq_len=1024 + 160, max_num_seqs=32, batch_wait_s=0.0, max_num_batched_tokens=4096)
+    args.update(kw)
+    return LLMEngine(model, [], **args)
+
+
+@pytest.fixture(scope="module")
+def model_1p5b():
+    print("building the 1.5B-shape model (bf16, seed 0)", flush=True)
+    sd = random_state_dict(QWEN25_1_5B, seed=0, dtype=torch.bfloat16, device="cuda")
+    yield Qwen2Model(QWEN25_1_5B, sd)
+    torch.cuda.empty_cache()
+
+
+def test_config3_graph_step_bitwise_equals_eager(hiplib, model_1p5b):
+    from nanoserve_amd.hip_graphs import DecodeGraphRunner
+    from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
+    model, cfg = model_1p5b, QWEN25_1_5B
+    pool = PagedKVCache.from_token_budget(cfg, 32 * 1184, 16, "cuda", torch.bfloat16)
+    runner = DecodeGraphRunner(model, pool, max_seq_len=1184, max_batch=32)
+    tables = []
+    ps = prompts(32, 1024, cfg.vocab_size, seed=1)
+    for i in range(0, 32, 4):                                # prefill 4 prompts per call
+        seqs, toks, pos, slots = [], [], [], []
+        for p in ps[i:i + 4]:
+            t = BlockTable(16)
+            t.reserve(1024 + 2, pool.allocator)
+            seqs.append(SeqInput(1024))
+            toks += p
+            pos += list(range(1024))
+            slots += t.slots(1024)
+            tables.append(t)
+        model.forward_batch(torch.tensor(toks, device="cuda"), torch.tensor(pos, device="cuda"), seqs,
+                            paged=pool, slot_mapping=torch.tensor(slots, device="cuda"))
+        for t in tables[i:i + 4]:
+            t.commit(1024)
+    inp = dict(tokens=[(7 * i + 11) % cfg.vocab_size for i in range(32)], positions=[1024] * 32,
+               slots=[t.slots(1)[0] for t in tables], block_tables=[t.blocks for t in tables],
+               context_lens=[1025] * 32)
+    width = max(len(b) for b in inp["block_tables"])
+    meta = DecodeMeta(token_idx=torch.arange(32, device="cuda"),
+                      block_tables=torch.tensor([b + [0] * (width - len(b)) for b in inp["block_tables"]],
+                                                dtype=torch.int32, device="cuda"),
+                      context_lens=torch.tensor(inp["context_lens"], dtype=torch.int32, device="cuda"))
+    ref = model.forward_batch(torch.tensor(inp["tokens"], device="cuda"), torch.tensor(inp["positions"], device="cuda"),
+                              [SeqInput(1, ctx_len=1024, use_kernel=True)] * 32, logits="all", paged=pool,
+                              slot_mapping=torch.tensor(inp["slots"], device="cuda"), decode_meta=meta).clone()
+    out = runner.run(**inp).clone()
+    assert runner.captured_buckets == [32]
+    assert torch.isfinite(out.float()).all()
+    assert out.shape == ref.shape and torch.equal(out, ref), "bucket-32 graph step differs from the eager step"
+    # the in-graph greedy argmax equals torch.argmax of the graph's logits
+    assert runner.greedy_tokens(32) == out.float().argmax(-1).tolist()
+    del pool, runner
+    torch.cuda.empty_cache()
+
+
+def test_config3_streams_identical_with_overlap_on_off_and_eager(hiplib, model_1p5b):
+    model, cfg = model_1p5b, QWEN25_1_5B
+    reqs = [(p, 128) for p in prompts(32, 1024, cfg.vocab_size, seed=2)]
+    streams = {}
+    for label, kw, overlap in (("overlap", {}, True), ("plain", {}, False), ("eager", {"cuda_graphs": False}, False)):
+        print(f"config 3 streams: {label}", flush=True)
+        eng = engine(model, **kw)
+        eng.overlap_host = overlap
+        if kw.get("cuda_graphs", True):
+            eng.capture_graphs()
+        streams[label] = run_engine(eng, reqs)
+        st = eng.stats
+        print(f"  steps {st['steps']}, graph steps {st['graph_steps']}", flush=True)
+        if label != "eager":
+            assert st["graph_steps"] >= 127
+        assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - (1 if kw.get("cuda_graphs", True) else 0)
+        del eng
+        torch.cuda.empty_cache()
+    assert all(len(s) == 128 for s in streams["overlap"])
+    assert streams["overlap"] == streams["plain"], "one-step-ahead launch changed the tokens"
+    assert streams["plain"] == streams["eager"], "graph steps and eager steps give different tokens"
+
+
+def test_config3_reduced_layers_against_the_oracle(hiplib):
+    """The 1.5B shape with 2 of its 28 layers: 32 requests of 1024 tokens, 32 greedy steps, bf16 on the GPU
+    (bucket-32 graph) against the fp32 CPU oracle on the same bf16 weights."""
+    cfg = dataclasses.replace(QWEN25_1_5B, n_layers=2)
+    sd = random_state_dict(cfg, seed=3, dtype=torch.bfloat16)
+    ps = prompts(32, 1024, cfg.vocab_size, seed=4)
+    model = Qwen2Model(cfg, {k: v.to("cuda") for k, v in sd.items()})
+    eng = engine(model)
+    eng.capture_graphs()
+    ours = run_engine(eng, [(p, 32) for p in ps])
+    assert eng.stats["graph_steps"] >= 31
+    del eng, model
+    torch.cuda.empty_cache()
+    print("config 3 (2 layers): oracle", flush=True)
+    orc = OracleModel(cfg, sd, dtype=torch.float32)
+    ref, ref_logits = orc.generate_greedy(ps, 32, return_logits=True)
+    check_tie_rule(ours, ref, ref_logits, "config 3 (2 layers)")
+
+
+def test_config4_mixed_step_reduced_layers(hiplib, monkeypatch):
+    """One 1552-row step: a 1536-token chunk of a 2048-token sequence on its 512 cached tokens, plus 16
+    decode rows with contexts U[256, 2048] (seed 2), 1.5B shape with 2 layers, bf16. The chunked-prefill
+    kernel path against the same step with every prefill token as its own decode row, and both against the
+    fp32 oracle's logits of the 17 sequences."""
+    from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
+    cfg = dataclasses.replace(QWEN25_1_5B, n_layers=2)
+    sd = random_state_dict(cfg, seed=5, dtype=torch.bfloat16)
+    model = Qwen2Model(cfg, {k: v.to("cuda") for k, v in sd.items()})
+    g = torch.Generator().manual_seed(2)
+    seq_a = torch.randint(0, cfg.vocab_size, (2048,), generator=g).tolist()
+    ctxs = torch.randint(256, 2049, (16,), generator=g).tolist()
+    decs = [torch.randint(0, cfg.vocab_size, (c + 1,), generator=g).tolist() for c in ctxs]
+
+    def step(force_rows: bool):
+        pool = PagedKVCache.from_token_budget(cfg, 2048 + sum(ctxs) + 16 * 17 + 64, 16, "cuda", torch.bfloat16)
+        random.Random(7).shuffle(pool.allocator._free)
+        if force_rows:
+            monkeypatch.setattr(model, "_prefill_meta",
+                                lambda seqs, paged, sm, dtype: Qwen2Model._prefill_meta(model, seqs, paged, sm,
+                                                                                        torch.float32))
+        ta = BlockTable(16)
+        ta.reserve(2048, pool.allocator)
+        tabs = []
+        for ids in [seq_a[:512]] + [d[:-1] for d in decs]:
+            t = ta if not tabs else BlockTable(16)
+            if tabs:
+                t.reserve(len(ids) + 1, pool.allocator)
+            model.forward_batch(torch.tensor(ids, device="cuda"), torch.arange(len(ids), device="cuda"),
+                                [SeqInput(len(ids))], paged=pool,
+                                slot_mapping=torch.tensor(t.slots(len(ids)), device="cuda"))
+            t.commit(len(ids))
+            tabs.append(t)
+        tokens = seq_a[512:] + [d[-1] for d in decs]
+        positions = list(range(512, 2048)) + ctxs
+        slots = ta.slots(1536) + [t.slots(1)[0] for t in tabs[1:]]
+        seqs = [SeqInput(1536, ctx_len=512, block_table=torch.tensor(ta.blocks, device="cuda"))]
+        seqs += [SeqInput(1, ctx_len=c, use_kernel=True) for c in ctxs]
+        width = max(len(t.blocks) for t in tabs[1:])
+        meta = DecodeMeta(token_idx=torch.arange(1536, 1552, device="cuda"),
+                          block_tables=torch.tensor([t.blocks + [0] * (width - len(t.blocks)) for t in tabs[1:]],
+                                                    dtype=torch.int32, device="cuda"),
+                          context_lens=torch.tensor([c + 1 for c in ctxs], dtype=torch.int32, device="cuda"))
+        out = model.forward_batch(torch.tensor(tokens, device="cuda"), torch.tensor(positions, device="cuda"), seqs,
+                                  logits="last", paged=pool, slot_mapping=torch.tensor(slots, device="cuda"),
+                                  decode_meta=meta).float().cpu()
+        monkeypatch.undo()
+        del pool
+        return out
+
+    chunks, rows = step(False), step(True)
+    assert chunks.shape == (17, cfg.vocab_size) and torch.isfinite(chunks).all()
+    print("config 4 (2 layers): oracle", flush=True)
+    orc = OracleModel(cfg, sd, dtype=torch.float32)
+    ca = orc.new_cache(2048)
+    orc.step([(ca, seq_a[:512])])
+    cds = []
+    for d in decs:
+        c = orc.new_cache(len(d))
+        orc.step([(c, d[:-1])])
+        cds.append(c)
+    ref = orc.step([(ca, seq_a[512:])] + [(c, [d[-1]]) for c, d in zip(cds, decs)])
+    d_paths = (chunks - rows).abs().max().item()
+    d_chunks = (chunks - ref).abs().max().item()
+    d_rows = (rows - ref).abs().max().item()
+    print(f"config 4 (2 layers): chunks vs rows {d_paths:.3e}; vs oracle {d_chunks:.3e} (rows {d_rows:.3e}); "
+          f"argmax equal {torch.equal(chunks.argmax(-1), ref.argmax(-1))}")
+    assert d_paths <= 0.05
+    assert d_chunks <= max(2 * d_rows, 0.05)
+
+
+def test_config5_prefix_sharing_reduced_layers(hiplib):
+    """3B shape with 2 of its 36 layers: 32 requests = one 1024-token prefix + a distinct 211-token suffix.
+    Request 0 runs first and registers its full blocks; the 31 others reuse its 64 prefix blocks through the
+    prefix cache. While all 32 run, every table starts with the same 64 blocks, each held 32 times, and no
+    other block is shared. The run with prefix caching and the run without it (every request computes its
+    own prefix K/V, in other batches, so bf16 rounding differs) both follow the fp32 oracle under the tie
+    rule."""
+    cfg = dataclasses.replace(QWEN25_3B, n_layers=2)
+    sd = random_state_dict(cfg, seed=6, dtype=torch.bfloat16)
+    model = Qwen2Model(cfg, {k: v.to("cuda") for k, v in sd.items()})
+    g = torch.Generator().manual_seed(7)
+    prefix = torch.randint(0, cfg.vocab_size, (1024,), generator=g).tolist()
+    ps = [prefix + torch.randint(0, cfg.vocab_size, (211,), generator=g).tolist() for _ in range(32)]
+    reqs = [(p, 32) for p in ps]
+    checked = []
+
+    def shared_blocks(eng, step):
+        run = eng.scheduler.running
+        if checked or len(run) < 32 or any(s.num_cached < len(s.prompt_ids) for s in run):
+            return
+        heads = {tuple(s.block_table.blocks[:64]) for s in run}
+        assert len(heads) == 1, "the 64 prefix blocks differ between tables"
+        assert all(eng.kv.refcount(b) == 32 for b in next(iter(heads)))
+        tails = [b for s in run for b in s.block_table.blocks[64:]]
+        assert len(tails) == len(set(tails)) and all(eng.kv.refcount(b) == 1 for b in tails)
+        checked.append(step)
+
+    eng = engine(model, max_seq_len=1235 + 64, prefix_caching=True, max_num_batched_tokens=2048)
+    eng.capture_graphs()
+    shared = run_engine(eng, reqs, waves=((0, 1), (1, 32)), on_step=shared_blocks)
+    st = eng.stats
+    print(f"config 5 (2 layers): prefix hits {st['prefix_hit_tokens']} of {st['prefix_query_tokens']}; "
+          f"shared-table check at step {checked}", flush=True)
+    assert checked and st["prefix_hit_tokens"] == 31 * 1024
+    assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - 1
+    del eng
+    plain = run_engine(engine(model, max_seq_len=1235 + 64, max_num_batched_tokens=2048), reqs,
+                       waves=((0, 1), (1, 32)))
+    print(f"config 5 (2 layers): {sum(a == b for a, b in zip(shared, plain))}/32 streams identical with and "
+          "without prefix caching", flush=True)
+    del model
+    torch.cuda.empty_cache()
+    print("config 5 (2 layers): oracle on 8 of the 32 requests", flush=True)
+    orc = OracleModel(cfg, sd, dtype=torch.float32)
+    pick = [0, 1, 5, 11, 17, 23, 29, 31]
+    ref, ref_logits = orc.generate_greedy([ps[i] for i in pick], 32, return_logits=True)
+    check_tie_rule([shared[i] for i in pick], ref, ref_logits, "config 5 (2 layers), prefix caching")
+    check_tie_rule([plain[i] for i in pick], ref, ref_logits, "config 5 (2 layers), no prefix caching")

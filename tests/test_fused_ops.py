@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 DT = [torch.float32, torch.bfloat16]
 
 
-def check(out, ref, dtype):
+def check(out, ref, dtype, ulps=1):
     out = out.cpu()
     assert out.shape == ref.shape and out.dtype == ref.dtype
     if dtype == torch.float32:
@@ -24,55 +24,64 @@ def check(out, ref, dtype):
         return
     same = (out == ref).float().mean().item()
     assert same >= 0.99, f"only {same:.4f} bitwise identical"
-    torch.testing.assert_close(out.float(), ref.float(), rtol=2 ** -7, atol=1e-6)   # <= 1 bf16 ulp
+    torch.testing.assert_close(out.float(), ref.float(), rtol=ulps * 2 ** -7, atol=1e-6)   # <= `ulps` bf16 ulps
+
+
+# RMSNorm rounds twice: y = round(x * inv), out = round(w * y). A different fp32 summation order can move inv
+# by an fp32 ulp and flip y by one bf16 ulp, which w (|w| ~ 1.3 at most here) carries into out: at most
+# 2^-7 |w y| before the final rounding, so 2 bf16 ulps of out. The reference's 1-ulp gate holds at its
+# 37-row shapes; at 1552 x 1536 rows a flip of y lands on a large |w| now and then.
+def norm_ulps(rows):
+    return 1 if rows <= 64 else 2
 
 
 @pytest.mark.parametrize("dtype", DT)
-@pytest.mark.parametrize("n", [896, 1536, 2048])
-def test_rms_norm(hiplib, dtype, n):
+@pytest.mark.parametrize("rows,n", [(37, 896), (37, 1536), (37, 2048), (1552, 1536)])
+def test_rms_norm(hiplib, dtype, rows, n):
     from nanoserve_amd.kernels.fused import rms_norm
     g = cpu_gen(0)
-    x = (torch.randn(37, n, generator=g) * 3).to(dtype)
+    x = (torch.randn(rows, n, generator=g) * 3).to(dtype)
     w = (1 + 0.1 * torch.randn(n, generator=g)).to(dtype)
-    check(rms_norm(x.cuda(), w.cuda(), 1e-6), ops.rms_norm(x, w, 1e-6), dtype)
+    check(rms_norm(x.cuda(), w.cuda(), 1e-6), ops.rms_norm(x, w, 1e-6), dtype, norm_ulps(rows))
 
 
 @pytest.mark.parametrize("dtype", DT)
-def test_rms_norm_with_residual_add(hiplib, dtype):
+@pytest.mark.parametrize("rows,n", [(37, 896), (1552, 1536)])
+def test_rms_norm_with_residual_add(hiplib, dtype, rows, n):
     from nanoserve_amd.kernels.fused import rms_norm
     g = cpu_gen(1)
-    x, a = (torch.randn(1, 37, 896, generator=g).to(dtype) for _ in range(2))
-    w = (1 + 0.1 * torch.randn(896, generator=g)).to(dtype)
+    x, a = (torch.randn(1, rows, n, generator=g).to(dtype) for _ in range(2))
+    w = (1 + 0.1 * torch.randn(n, generator=g)).to(dtype)
     out, res = rms_norm(a.cuda(), w.cuda(), 1e-6, residual=x.cuda())
     ref_out, ref_res = ops.rms_norm_residual(a, w, 1e-6, x)
     assert torch.equal(res.cpu(), ref_res)                     # the add is exact: same rounding as PyTorch
-    check(out, ref_out, dtype)
+    check(out, ref_out, dtype, norm_ulps(rows))
 
 
 @pytest.mark.parametrize("dtype", DT)
-@pytest.mark.parametrize("n", [4864, 8960, 11008, 100])
-def test_silu_mul(hiplib, dtype, n):
+@pytest.mark.parametrize("rows,n", [(37, 4864), (37, 8960), (37, 11008), (37, 100), (1552, 8960)])
+def test_silu_mul(hiplib, dtype, rows, n):
     from nanoserve_amd.kernels.fused import silu_mul
     g = cpu_gen(2)
-    x = (torch.randn(1, 37, 2 * n, generator=g) * 2).to(dtype)
+    x = (torch.randn(1, rows, 2 * n, generator=g) * 2).to(dtype)
     check(silu_mul(x.cuda()), ops.silu_mul(x), dtype)
 
 
 @pytest.mark.parametrize("dtype", DT)
-@pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (12, 2, 128), (16, 2, 128)])
-def test_rope_qkv_and_cache_write(hiplib, dtype, nh, nkv, hd):
+@pytest.mark.parametrize("N,nh,nkv,hd", [(37, 14, 2, 64), (37, 12, 2, 128), (37, 16, 2, 128), (1552, 12, 2, 128)])
+def test_rope_qkv_and_cache_write(hiplib, dtype, N, nh, nkv, hd):
     from nanoserve_amd.kernels.fused import rope_qkv
     g = cpu_gen(3)
-    N = 37
+    NB = max(8, -(-2 * N // 16))
     qkv = torch.randn(N, (nh + 2 * nkv) * hd, generator=g).to(dtype)
     positions = torch.randint(0, 2000, (N,), generator=g)
     cos, sin = ops.rope_tables(positions, hd, 1_000_000.0, dtype)
-    slots = torch.randperm(8 * 16, generator=g)[:N]
-    k_cache = torch.zeros(8, 16, nkv, hd, dtype=dtype, device="cuda")
+    slots = torch.randperm(NB * 16, generator=g)[:N]
+    k_cache = torch.zeros(NB, 16, nkv, hd, dtype=dtype, device="cuda")
     v_cache = torch.zeros_like(k_cache)
     q, k, v = rope_qkv(qkv.cuda(), cos.cuda(), sin.cuda(), nh, nkv, hd, k_cache, v_cache, slots.cuda())
 
-    rk, rv = torch.zeros(8, 16, nkv, hd, dtype=dtype), torch.zeros(8, 16, nkv, hd, dtype=dtype)
+    rk, rv = torch.zeros(NB, 16, nkv, hd, dtype=dtype), torch.zeros(NB, 16, nkv, hd, dtype=dtype)
     q0, k0, v0 = ops.rope_qkv(qkv, cos, sin, nh, nkv, hd, rk, rv, slots)
     check(q, q0, dtype)
     check(k, k0, dtype)
@@ -80,7 +89,7 @@ def test_rope_qkv_and_cache_write(hiplib, dtype, nh, nkv, hd):
     k, v = k.cpu(), v.cpu()
     flat_k, flat_v = k_cache.cpu().view(-1, nkv, hd), v_cache.cpu().view(-1, nkv, hd)
     assert torch.equal(flat_k[slots], k) and torch.equal(flat_v[slots], v)
-    untouched = torch.ones(8 * 16, dtype=torch.bool)
+    untouched = torch.ones(NB * 16, dtype=torch.bool)
     untouched[slots] = False
     assert not flat_k[untouched].any() and not flat_v[untouched].any()
 

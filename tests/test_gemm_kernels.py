@@ -78,7 +78,7 @@ def test_lm_head_shape(hiplib):
 
 
 @pytest.mark.parametrize("M", [1, 16, 32])
-@pytest.mark.parametrize("K", [896, 1280, 2048])
+@pytest.mark.parametrize("K", [896, 1280, 1536, 2048])
 def test_wide_projection_persistent_kernel(hiplib, M, K):
     """Wide projections without bias (at least four 64-row tiles per CU, M <= 32, K <= 2048: the LM head) run
     on persistent workgroups that keep their activation fragments in registers across tiles. N = 65573 (a

@@ -203,8 +203,13 @@ def test_config1_greedy_tokens_identical_to_oracle_fp32(hiplib):
     ours = run_all(eng, [(p, 32) for p in ps])
     same = sum(a == b for a, b in zip(ours, ref))
     print(f"config 1 fp32: {same}/4 token streams identical; graph steps {eng.stats['graph_steps']}")
+    for i, (a, b) in enumerate(zip(ours, ref)):
+        j = first_divergence(a, b)
+        if j is not None:
+            top2 = ref_logits[i][j].float().topk(2).values
+            print(f"config 1 fp32: request {i} diverges at token {j}, oracle top-2 gap {(top2[0] - top2[1]).item():.3e}")
     assert eng.stats["graph_steps"] > 0
-    check_tokens_with_tie_rule(ours, ref, ref_logits, TIE_GAP_FP32, "config1 fp32")
+    assert ours == ref, "config 1: fp32 greedy streams must be identical for all 32 steps"
     assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - 1     # only the garbage block is held
 
 
@@ -418,7 +423,7 @@ def test_overlapped_host_staging_matches_plain_steps(hiplib):
             log.append([(o.seq_id, o.token, o.finished) for o in eng.step()])
             prelaunched += eng._pre is not None
             steps += 1
-        assert eng.kv.num_free_blocks == eng.kv.alloc.num_free and not eng.sequences
+        assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - 1 and not eng.sequences
         return log, prelaunched
 
     plain, _ = drive(False, [])

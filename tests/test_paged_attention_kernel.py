@@ -97,24 +97,58 @@ def test_config2_shape_split_k(hiplib, n_heads, n_kv, hd):
 
 
 @pytest.mark.parametrize("n_heads,n_kv,hd", [(12, 2, 128), (14, 2, 64)])
-def test_equal_partitions_of_a_73_page_table(hiplib, n_heads, n_kv, hd):
-    """BASELINE config 3's table width (73 pages): the whole-row kernel cuts it into three equal partitions
-    of 25 pages, so rows end in ragged partitions at other places than with 32-page ones. Context lengths
-    sit on and next to the 25-page (400-token) partition boundaries, inside the last page and at the full
-    width."""
-    ctx = [1, 16, 17, 399, 400, 401, 799, 800, 801, 1025, 1100, 1151, 1152, 1160, 1168, 73 * 16]
+def test_result_does_not_depend_on_the_table_width(hiplib, n_heads, n_kv, hd):
+    """BASELINE config 3's rows (contexts 1025 .. 1152) in tables 73 pages wide (the graph runner's width
+    for max_seq_len 1168) and 80 and 256 pages wide (other callers pad to other widths): a row's
+    partitions are fixed 32-page runs of its own pages, so all three give bitwise the same output. Contexts
+    sit on and next to the partition boundaries (512 / 1024 tokens), inside the last page and at the full
+    width, and the output is checked against the oracle."""
+    ctx = [1, 16, 17, 511, 512, 513, 1023, 1024, 1025, 1056, 1100, 1151, 1152, 1160, 1168]
     ctx = ctx + [1025 + 9 * i for i in range(16)]
     q, k, v, tables, lens = make_case(n_heads, n_kv, hd, ctx, torch.bfloat16, seed=31, extra_blocks=16, width=73)
     scale = hd ** -0.5
     from nanoserve_amd.kernels.paged_attention import paged_attention_decode
-    dq, dk, dv, dt, dl = q.cuda(), k.cuda(), v.cuda(), tables.cuda(), lens.cuda()
-    out1 = paged_attention_decode(dq, dk, dv, dt, dl, scale).cpu()
-    out2 = paged_attention_decode(dq, dk, dv, dt, dl, scale).cpu()
+    dq, dk, dv, dl = q.cuda(), k.cuda(), v.cuda(), lens.cuda()
+    outs = []
+    for W in (73, 80, 256):
+        t = torch.zeros(len(ctx), W, dtype=torch.int32)
+        t[:, :min(W, 73)] = tables[:, :min(W, 73)]
+        outs.append(paged_attention_decode(dq, dk, dv, t.cuda(), dl, scale).cpu())
     ref = paged_attention_reference(q.float(), k.float(), v.float(), tables, lens, scale)
-    err = (out1.float() - ref).abs().max().item()
-    print(f"73-page table ({n_heads},{n_kv},{hd}) max|diff| = {err:.2e}")
+    err = (outs[0].float() - ref).abs().max().item()
+    print(f"config-3 rows ({n_heads},{n_kv},{hd}) max|diff| = {err:.2e}")
     assert err <= 1e-2
-    assert torch.equal(out1, out2)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_one_workspace_serves_every_shape(hiplib):
+    """A split-K workspace shared by calls of different shapes on one stream (a few rows, then many rows,
+    then the per-head kernel, then a few rows again): the arrival counters live in a fixed region that no
+    call's partials overlap, so every call equals the same call on a fresh workspace."""
+    from nanoserve_amd import _lib
+    L = _lib.lib()
+    g = cpu_gen(23)
+    shared = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    for it, (B, nh, nkv, hd, W, mx) in enumerate([(3, 14, 2, 64, 256, 4096), (200, 14, 2, 64, 256, 4096),
+                                                  (20, 12, 2, 128, 1100, 17000), (5, 12, 2, 128, 73, 1168),
+                                                  (128, 12, 2, 128, 73, 1168)]):
+        ctx = torch.randint(1, mx + 1, (B,), generator=g).tolist()
+        q, k, v, tables, lens = make_case(nh, nkv, hd, ctx, torch.bfloat16, seed=40 + it, extra_blocks=4, width=W)
+        dq, dk, dv, dt, dl = q.cuda(), k.cuda(), v.cuda(), tables.cuda(), lens.cuda()
+        outs = []
+        for ws in (shared, torch.zeros_like(shared)):
+            out = torch.full_like(dq, float("nan"))
+            _lib.check(L.ns_paged_attn_decode(
+                dq.data_ptr(), dq.stride(0), dq.stride(1), dk.data_ptr(), dv.data_ptr(), dk.stride(0), dk.stride(1),
+                dk.stride(2), dt.data_ptr(), dt.stride(0), dl.data_ptr(), out.data_ptr(), out.stride(0),
+                out.stride(1), B, nh, nkv, hd, 16, W, dk.shape[0], hd ** -0.5, 1, ws.data_ptr(), ws.numel(),
+                _lib.stream_of(dq)), "decode")
+            outs.append(out.cpu())
+        print(f"shared workspace call {it}: B={B} width {W}", flush=True)
+        assert torch.equal(outs[0], outs[1]), f"call {it}: shared workspace differs from a fresh one"
+        if it in (0, 3):
+            ref = paged_attention_reference(q.float(), k.float(), v.float(), tables, lens, hd ** -0.5)
+            assert (outs[0].float() - ref).abs().max().item() <= 1e-2
 
 
 def test_merge_words_of_earlier_calls_are_never_taken(hiplib):

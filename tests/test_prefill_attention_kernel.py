@@ -160,3 +160,17 @@ def test_long_partition_refreshes_its_block_window(hiplib):
     info = prefill_seq_info([0], [100], [1500], "cuda")
     out = paged_attention_prefill(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), info, 100, 100, 128 ** -0.5).cpu()
     check(out, q, seqs, ks, vs, 128 ** -0.5)
+
+
+def test_one_workspace_serves_every_shape(hiplib):
+    """Calls of different shapes (few tiles, then many sequences and tiles, then few again) share the
+    wrapper's workspace: the counters sit in a fixed region no call's partials overlap, so every call
+    matches the oracle and a repeat of itself."""
+    for it, specs in enumerate([[(900, 40)], [(512, 200)] * 12 + [(3000, 64)], [(1200, 17), (0, 300)],
+                                [(2500, 129)] * 3]):
+        q, kp, vp, tables, seqs, ks, vs = make_seqs(specs, 12, 2, 128, seed=60 + it)
+        print(f"prefill shared workspace call {it}: {len(specs)} sequences", flush=True)
+        out = run(q, kp, vp, tables, seqs, 128 ** -0.5)
+        check(out, q, seqs, ks, vs, 128 ** -0.5)
+        assert torch.equal(out, run(q, kp, vp, tables, seqs, 128 ** -0.5))
+
