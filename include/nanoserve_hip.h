@@ -77,6 +77,27 @@ int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
 size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype);
 
 /*
+ * ns_paged_attn_decode without the workspace argument, for callers that cannot allocate device memory
+ * (code under hipGraph capture that must not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation). No counterpart in the reference: nanoserve's Triton kernel needs no workspace.
+ * The split-K workspace is a fixed array of NS_DECODE_SCRATCH_BYTES in the library's device memory, one
+ * per GPU, held until the process ends; its address is looked up on the first call with that GPU current
+ * (which also clears it with a kernel on `stream`). This call allocates nothing: a shape whose
+ * ns_decode_workspace_bytes exceeds NS_DECODE_SCRATCH_BYTES is rejected with NS_E_INVALID.
+ * Every call on one GPU shares that GPU's array: calls that may overlap in time on one GPU (different
+ * streams, different threads without ordering) race and give wrong results; calls on one stream are safe.
+ * Results are bitwise those of ns_paged_attn_decode with a caller workspace.
+ */
+#define NS_DECODE_SCRATCH_BYTES (16u << 20)
+int ns_paged_attn_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                                 const void* k_pool, const void* v_pool,
+                                 int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                                 const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                                 void* out, int64_t o_sb, int64_t o_sh,
+                                 int B, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                                 int max_blocks, int num_blocks, float scale, int dtype, void* stream);
+
+/*
  * Paged chunked-prefill attention: several sequences' new tokens attend to their cached context plus
  * themselves, causally. seq_info (device, int32 [n_seqs, 4]) holds per sequence s:
  *   q_start (first row of s in q / out), n_new (T, its new tokens), ctx_len (tokens cached before this

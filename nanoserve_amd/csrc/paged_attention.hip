@@ -30,6 +30,7 @@
 // it serves the fp32 correctness paths.
 #include "ns_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace ns {
@@ -891,4 +892,74 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
   return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
                              context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
                              num_blocks, scale, dtype, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Allocation-free variant: the split-K workspace is a file-scope device array instead of a caller buffer.
+// In host code `scratch` names a host-side stand-in, not device memory: its device address is looked up
+// once per device with hipGetSymbolAddress and only that address is passed to kernels.
+// ---------------------------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[NS_DECODE_SCRATCH_BYTES];
+
+namespace ns {
+
+__global__ void zero_words_kernel(uint32_t* p, size_t n_words) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n_words; i += size_t(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Device address of this device's `scratch`, looked up (and cleared, by a fill kernel on `s`, ordered
+// before the caller's launch) the first time a call runs with the device current.
+static int scratch_for_current_device(hipStream_t s, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("paged_attention_decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return NS_E_HIP_BASE + int(e);
+  }
+  NS_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "paged_attention_decode_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("paged_attention_decode_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return NS_E_HIP_BASE + int(e == hipSuccess ? hipErrorInvalidSymbol : e);
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p),
+                       size_t(NS_DECODE_SCRATCH_BYTES) / 4);
+    const int st = check_launch("paged_attention_decode_noalloc(scratch clear)");
+    if (st != NS_OK) return st;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NS_OK;
+}
+
+}  // namespace ns
+
+extern "C" int ns_paged_attn_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,
+                                            const void* v_pool, int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                                            const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                                            void* out, int64_t o_sb, int64_t o_sh, int B, int n_heads,
+                                            int n_kv_heads, int head_dim, int block_size, int max_blocks,
+                                            int num_blocks, float scale, int dtype, void* stream) {
+  const size_t need = ns_decode_workspace_bytes(B, n_kv_heads, head_dim, max_blocks, dtype);
+  NS_REQUIRE(need <= size_t(NS_DECODE_SCRATCH_BYTES),
+             "paged_attention_decode_noalloc: this shape (B=%d, n_kv=%d, head_dim=%d, table width %d) needs %zu "
+             "bytes of split-K scratch, more than the library's fixed %zu",
+             B, n_kv_heads, head_dim, max_blocks, need, size_t(NS_DECODE_SCRATCH_BYTES));
+  void* ws = nullptr;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (need > 0) {
+    const int st = scratch_for_current_device(s, &ws);
+    if (st != NS_OK) return st;
+  }
+  return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
+                             context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
+                             num_blocks, scale, dtype, ws, need > 0 ? size_t(NS_DECODE_SCRATCH_BYTES) : 0, stream);
 }
