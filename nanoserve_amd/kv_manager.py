@@ -1,101 +1,114 @@
-"""Paged KV manager: the scheduler's and engine's interface to the block pool (host-side integers).
+"""Paged KV manager: how the scheduler and the engine get KV blocks for requests (host-side integers).
 
-Semantics follow nanoserve/kv_manager.py:70-202 (PagedKVManager):
-  * admission by an explicit token budget, keeping a 1% watermark of blocks free (:116-121);
-  * with prefix caching, admission starts from the longest cached prefix, leaving at least one token to
+Decisions follow nanoserve/kv_manager.py:70-202 (PagedKVManager), pinned step by step by
+tests/golden/host_traces.json:
+  * admission needs the request's uncached tokens in whole blocks, less cached prefix hits, plus the hits
+    that must be taken back from the parked (cached, unheld) set, within the free blocks minus a 1%
+    watermark (:116-121);
+  * with prefix caching a request starts from the longest cached prefix, leaving at least one token to
     compute, i.e. at most (len - 1) // block_size hit blocks (:101-107, :123-138);
-  * per step: slot mapping of every scheduled token, DecodeMeta for one-token decodes on a context
-    (ctx + 1 including the new token, tables as int32 padded with 0 to the step's widest), graph inputs,
-    and registration of newly full blocks at commit (:153-196).
-The contiguous manager of the reference (M1/M2 A/B comparisons) is not part of the decode loop.
+  * per step: the slot of every scheduled token, the decode rows (one new token on a stored context,
+    context length ctx + 1 including it), and at commit the registration of newly full blocks (:153-196).
+
+Design (this build's own): one call, batch(plan), turns a StepPlan into a StepBatch -- the flattened token
+ids, positions and slots, one SeqInput per sequence, and the decode rows' indices, tables and context
+lengths as plain lists -- which the executor stages straight into its pinned buffers (graph steps) or
+turns into tensors (eager steps). Every prefill sequence carries its block table, a fresh one included:
+the HIP prefill attention reads its pages in place (the reference's SDPA path needs none for ctx = 0).
 """
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass, field
 
 import torch
 
-from nanoserve_amd.kv_cache import BlockTable, PagedKVCache, PrefixCachingAllocator
+from nanoserve_amd.kv_cache import BlockTable, PagedKVCache
 from nanoserve_amd.model import DecodeMeta, ModelConfig, SeqInput
+
+
+@dataclass
+class StepBatch:
+    """Everything the model needs for one step, host side."""
+    token_ids: list[int] = field(default_factory=list)
+    positions: list[int] = field(default_factory=list)
+    slots: list[int] = field(default_factory=list)
+    seqs: list[SeqInput] = field(default_factory=list)
+    tables: list[list[int]] = field(default_factory=list)   # per sequence: its block list (the live list)
+    dec_idx: list[int] = field(default_factory=list)        # decode rows: index in the flattened step
+    dec_tables: list[list[int]] = field(default_factory=list)
+    dec_lens: list[int] = field(default_factory=list)       # context incl. this step's token
+    n_prefill: int = 0                                      # sequences that are prefilling
+
+    @property
+    def n_tokens(self) -> int:
+        return len(self.token_ids)
+
+    @property
+    def pure_decode(self) -> bool:
+        return len(self.dec_idx) == len(self.seqs)
 
 
 class PagedKVManager:
     kind = "paged"
 
     def __init__(self, cfg: ModelConfig, budget_tokens: int, block_size: int = 16, device="cuda",
-                 dtype=torch.bfloat16, watermark: float = 0.01, attn_backend: str = "hip",
-                 prefix_caching: bool = False):
-        self.pool = PagedKVCache.from_token_budget(cfg, budget_tokens, block_size, device, dtype)
+                 dtype=torch.bfloat16, watermark: float = 0.01, prefix_caching: bool = False):
+        self.pool = PagedKVCache.from_token_budget(cfg, budget_tokens, block_size, device, dtype, prefix_caching)
+        self.alloc = self.pool.allocator
         self.block_size = block_size
         self.device = device
-        self.attn_backend = attn_backend
         self.prefix_caching = prefix_caching
-        self.alloc = (PrefixCachingAllocator(self.pool.allocator, block_size) if prefix_caching
-                      else self.pool.allocator)
         self.prefix_query_tokens = 0     # prompt tokens looked up at admission
         self.prefix_hit_tokens = 0       # ... of which were found cached (prefill skipped)
         self.watermark_blocks = math.floor(watermark * self.pool.num_blocks)
-        self._slots: list[int] = []
-        self._offset = 0
-        self._dec_idx: list[int] = []
-        self._dec_tables: list[list[int]] = []
-        self._dec_lens: list[int] = []
 
     @property
     def num_free_blocks(self) -> int:
         return self.alloc.num_free
 
     def refcount(self, block: int) -> int:
-        """How many block tables hold `block` (1 for an allocated block without prefix caching)."""
-        ref = getattr(self.alloc, "ref", None)
-        if ref is not None:
-            return ref.get(block, 0)
-        return int(block in self.alloc._used)
-
-    def _blocks_for(self, n_tokens: int) -> int:
-        return math.ceil(n_tokens / self.block_size)
-
-    def _hits(self, seq) -> list[int]:
-        """Cached blocks of the longest known prefix, leaving >= 1 token to compute (its logits are needed)."""
-        if not self.prefix_caching:
-            return []
-        toks = seq.prompt_ids + seq.output_ids
-        return self.alloc.lookup(toks, max_blocks=(len(toks) - 1) // self.block_size)
+        return self.alloc.refcount(block)
 
     def reset_stats(self) -> None:
         self.prefix_query_tokens = self.prefix_hit_tokens = 0
 
-    # --- scheduler interface
+    def _prefix_hits(self, seq) -> list[int]:
+        if not self.prefix_caching:
+            return []
+        return self.alloc.lookup(seq.tokens, max_blocks=(seq.num_tokens - 1) // self.block_size)
+
+    # ------------------------------------------------------------------------- scheduler interface
     def can_ever_fit(self, n_tokens: int) -> bool:
-        return self._blocks_for(n_tokens) <= self.pool.num_blocks
+        return -(-n_tokens // self.block_size) <= self.pool.num_blocks
 
     def can_admit(self, seq) -> bool:
-        hits = self._hits(seq)
-        parked = sum(1 for b in hits if self.alloc.ref.get(b, 0) == 0)   # pinning them uses free capacity
-        need = self._blocks_for(seq.step_cost) - len(hits) + parked
-        return need <= self.num_free_blocks - self.watermark_blocks
+        hits = self._prefix_hits(seq)
+        parked = sum(1 for b in hits if self.alloc.refcount(b) == 0)   # taking them back uses free capacity
+        need = -(-seq.step_cost // self.block_size) - len(hits) + parked
+        return need <= self.alloc.num_free - self.watermark_blocks
 
     def admit(self, seq) -> None:
         table = BlockTable(self.block_size)
         if self.prefix_caching:
-            hits = self._hits(seq)
             self.prefix_query_tokens += seq.num_tokens
+            hits = self._prefix_hits(seq)
             if hits:
                 self.alloc.pin(hits)
                 table.blocks = list(hits)
                 table.num_hashed = len(hits)
-                table.num_tokens = len(hits) * self.block_size
-                table.prefix_node = self.alloc.node_of[hits[-1]]
-                seq.num_cached = table.num_tokens
+                table.num_tokens = seq.num_cached = len(hits) * self.block_size
+                table.prefix_node = self.alloc.node_of(hits[-1])
                 self.prefix_hit_tokens += table.num_tokens
         seq.block_table = table
         table.reserve(seq.step_cost, self.alloc)
 
     def try_append(self, seq) -> bool:
-        """Room for one more token (a decode step); False if the pool is out of blocks."""
-        if seq.block_table.blocks_needed(1) > self.num_free_blocks:
+        """Room for one more token; False if the pool cannot provide the block it needs."""
+        t = seq.block_table
+        if t.blocks_needed(1) > self.alloc.num_free:
             return False
-        seq.block_table.reserve(1, self.alloc)
+        t.reserve(1, self.alloc)
         return True
 
     def free(self, seq) -> None:
@@ -103,57 +116,52 @@ class PagedKVManager:
             seq.block_table.release(self.alloc)
             seq.block_table = None
 
-    # --- engine interface
-    def begin_step(self) -> None:
-        self._slots = []
-        self._offset = 0
-        self._dec_idx, self._dec_tables, self._dec_lens = [], [], []
+    # ---------------------------------------------------------------------------- engine interface
+    def batch(self, plan) -> StepBatch:
+        """The step's model inputs, in plan order."""
+        sb = StepBatch()
+        for seq, n in zip(plan.scheduled, plan.chunks):
+            t = seq.block_table
+            ctx = t.num_tokens
+            toks, pos = seq.step_tokens(n)
+            row = len(sb.token_ids)
+            sb.token_ids += toks
+            sb.positions += pos
+            sb.slots += t.slots(n)
+            sb.tables.append(t.blocks)
+            if n == 1 and ctx > 0:
+                sb.dec_idx.append(row)
+                sb.dec_tables.append(t.blocks)
+                sb.dec_lens.append(ctx + 1)
+                sb.seqs.append(SeqInput(1, ctx_len=ctx, use_kernel=True))
+            else:
+                sb.seqs.append(SeqInput(n, block_table=t.blocks, ctx_len=ctx))
+            sb.n_prefill += seq.is_prefill
+        return sb
 
-    def seq_input(self, seq, n_tokens: int) -> SeqInput:
-        table = seq.block_table
-        self._slots += table.slots(n_tokens)
-        ctx = table.num_tokens
-        use_kernel = n_tokens == 1 and ctx > 0
-        if use_kernel:
-            self._dec_idx.append(self._offset)
-            self._dec_tables.append(table.blocks)
-            self._dec_lens.append(ctx + 1)
-        self._offset += n_tokens
-        # the HIP attention reads every prefill token's pages in place: give it the table (also ctx == 0)
-        bt = None if use_kernel else torch.tensor(table.blocks, dtype=torch.int32, device=self.device)
-        return SeqInput(n_tokens, block_table=bt, ctx_len=ctx, use_kernel=use_kernel)
-
-    def decode_meta(self) -> DecodeMeta | None:
-        """Kernel inputs of this step's one-token decodes (None if there are none)."""
-        if not self._dec_idx:
+    def decode_meta(self, sb: StepBatch, width: int | None = None) -> DecodeMeta | None:
+        """Device tensors of the decode rows (tables padded with 0 to `width`, default the widest row)."""
+        if not sb.dec_idx:
             return None
-        width = max(len(t) for t in self._dec_tables)
-        tables = [t + [0] * (width - len(t)) for t in self._dec_tables]
-        all_rows = self._dec_idx == list(range(self._offset))
-        return DecodeMeta(token_idx=torch.tensor(self._dec_idx, device=self.device),
-                          block_tables=torch.tensor(tables, dtype=torch.int32, device=self.device),
-                          context_lens=torch.tensor(self._dec_lens, dtype=torch.int32, device=self.device),
-                          all_rows=all_rows)
-
-    def forward_kwargs(self) -> dict:
-        kw = {"paged": self.pool, "slot_mapping": torch.tensor(self._slots, device=self.device)}
-        meta = self.decode_meta()
-        if meta is not None:
-            kw["decode_meta"] = meta
-        return kw
-
-    def graph_inputs(self) -> tuple[list[int], list[list[int]], list[int]]:
-        """(slots, block tables, context lens) of this step's decodes, for the graph path."""
-        return self._slots, self._dec_tables, self._dec_lens
+        w = width or max(len(t) for t in sb.dec_tables)
+        rows = [t + [0] * (w - len(t)) for t in sb.dec_tables]
+        dev = self.device
+        return DecodeMeta(token_idx=torch.tensor(sb.dec_idx, device=dev),
+                          block_tables=torch.tensor(rows, dtype=torch.int32, device=dev),
+                          context_lens=torch.tensor(sb.dec_lens, dtype=torch.int32, device=dev),
+                          all_rows=sb.pure_decode)
 
     def commit(self, seq, n_tokens: int) -> None:
-        table = seq.block_table
-        table.commit(n_tokens)
-        if self.prefix_caching and table.num_tokens // self.block_size > table.num_hashed:
-            self.alloc.register(table, seq.prompt_ids + seq.output_ids)
+        t = seq.block_table
+        t.commit(n_tokens)
+        if self.prefix_caching and t.num_tokens // self.block_size > t.num_hashed:
+            self.alloc.register(t, seq.tokens)      # newly full blocks become reusable
 
     def usage(self, running) -> tuple[int, int]:
         """(tokens actually stored, tokens reserved = blocks held x block_size)."""
-        used = sum(s.block_table.num_tokens for s in running if s.block_table)
-        held = sum(len(s.block_table.blocks) for s in running if s.block_table)
+        used = held = 0
+        for s in running:
+            if s.block_table is not None:
+                used += s.block_table.num_tokens
+                held += len(s.block_table.blocks)
         return used, held * self.block_size

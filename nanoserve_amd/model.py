@@ -134,8 +134,8 @@ class LayerWeights:
 @dataclass
 class SeqInput:
     """One sequence's slice of a batched step (nanoserve/model.py:117-129). Paged only: `block_table` =
-    this request's block ids (int tensor on the device; may be None for a fresh prefill, whose pages are
-    then read off the slot mapping), `ctx_len` = tokens already stored before this step."""
+    this request's block ids (a list, or an int tensor on the device; may be None for a fresh prefill, whose
+    pages are then read off the slot mapping), `ctx_len` = tokens already stored before this step."""
     n_tokens: int
     cache: object | None = None
     block_table: torch.Tensor | None = None
@@ -325,7 +325,9 @@ class Qwen2Model:
             T = s.n_tokens
             if not s.use_kernel and T > 0:
                 n_pages = -(-(s.ctx_len + T) // bs)
-                if s.block_table is not None:
+                if isinstance(s.block_table, list):
+                    bt = torch.tensor(s.block_table[:n_pages], dtype=torch.int32, device=dev)
+                elif s.block_table is not None:
                     bt = s.block_table.to(device=dev, dtype=torch.int32)[:n_pages]
                     if bt.shape[0] < n_pages:
                         raise ValueError(f"block_table holds {bt.shape[0]} blocks, {n_pages} needed")

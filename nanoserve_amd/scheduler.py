@@ -1,14 +1,22 @@
-"""Continuous / static batching: which requests run in each engine step (host-side integer logic).
+"""Which requests run in each engine step (host-side integer logic).
 
-Semantics follow nanoserve/scheduler.py:25-200, so a step sees exactly the batch the reference would
-build:
+The decisions are nanoserve/scheduler.py:25-200's, so every step schedules the batch the reference would
+(pinned step by step by tests/golden/host_traces.json):
 
-  * budget order per step: (1) every running decode, 1 token each; (2) running requests part-way through
-    a chunked prefill, min(remaining, budget) tokens; (3) first-come-first-served admissions, which never
-    skip the head of the queue;
-  * before that, every running request reserves KV room for this step's token; if the pool is out of
-    blocks, the most recently admitted request is preempted (LIFO) and recomputes prompt + outputs later;
+  * budget order: every running decode (1 token each), then running requests part-way through a chunked
+    prefill (min(remaining, budget) tokens), then admissions first come first served -- the head of the
+    queue is never skipped (scheduler.py:161-200);
+  * before that, every running request reserves KV room for this step's token; when the pool runs dry the
+    most recently admitted running request is preempted (LIFO) and later recomputes prompt + outputs
+    (scheduler.py:128-146);
   * policy "static" admits only between batches, once the batch is full or has waited batch_wait_s.
+
+Design (this build's own): a Sequence keeps one list of all its known token ids (prompt, then outputs),
+so step inputs and prefix-cache keys slice it instead of concatenating prompt and outputs every step; a
+step's plan is a StepPlan of parallel lists whose decode rows always come first, which the engine's
+mixed-step graph relies on (decode rows are rows 0 .. n_decode-1 of the flattened step). With the
+engine's one-step-ahead launch (LLMEngine.overlap_host), a request added between step() calls is planned
+one step later than the reference would; with it off the plans are identical.
 """
 from __future__ import annotations
 
@@ -23,56 +31,70 @@ class SeqStatus(Enum):
     FINISHED = "finished"
 
 
-@dataclass(eq=False)
 class Sequence:
-    """One request inside the engine."""
-    seq_id: int
-    prompt_ids: list[int]
-    max_new_tokens: int
-    ignore_eos: bool = False
-    arrival_time: float = 0.0
-    output_ids: list[int] = field(default_factory=list)
-    status: SeqStatus = SeqStatus.WAITING
-    cache: object | None = None        # unused by the paged path (kept for interface parity)
-    block_table: object | None = None  # paged KV, set on admission
-    num_cached: int = 0                # tokens whose K/V are stored; 0 => must (re)prefill
-    sampling: object | None = None     # SamplingParams (None = greedy)
-    seed: int = 0                      # this request's random stream
+    """One request inside the engine: its token ids, its KV (block table) and how much of it is stored."""
+
+    __slots__ = ("seq_id", "tokens", "n_prompt", "max_new_tokens", "ignore_eos", "arrival_time", "status",
+                 "block_table", "num_cached")
+
+    def __init__(self, seq_id: int, prompt_ids: list[int], max_new_tokens: int, ignore_eos: bool = False,
+                 arrival_time: float = 0.0):
+        self.seq_id = seq_id
+        self.tokens: list[int] = list(prompt_ids)     # prompt, then every generated token
+        self.n_prompt = len(self.tokens)
+        self.max_new_tokens = max_new_tokens
+        self.ignore_eos = ignore_eos
+        self.arrival_time = arrival_time
+        self.status = SeqStatus.WAITING
+        self.block_table = None                       # set on admission (paged KV)
+        self.num_cached = 0                           # tokens whose K/V are stored; 0 -> (re)prefill
+
+    @property
+    def prompt_ids(self) -> list[int]:
+        return self.tokens[:self.n_prompt]
+
+    @property
+    def output_ids(self) -> list[int]:
+        return self.tokens[self.n_prompt:]
+
+    @property
+    def num_outputs(self) -> int:
+        return len(self.tokens) - self.n_prompt
 
     @property
     def num_tokens(self) -> int:
-        return len(self.prompt_ids) + len(self.output_ids)
+        return len(self.tokens)
 
     @property
     def remaining(self) -> int:
         """Known tokens whose K/V is not stored yet."""
-        return self.num_tokens - self.num_cached
+        return len(self.tokens) - self.num_cached
 
     @property
     def is_prefill(self) -> bool:
-        """Prefilling = new, preempted (recomputing), or part-way through a chunked prefill. Decoding =
-        exactly one uncached token (the newest output)."""
-        return self.num_cached == 0 or self.remaining > 1
-
-    def step_tokens(self, n: int | None = None) -> tuple[list[int], list[int]]:
-        """(token ids, positions) of the next n uncached tokens (default: all of them)."""
-        n = self.remaining if n is None else n
-        if n == 1 and self.remaining == 1 and self.output_ids:
-            return [self.output_ids[-1]], [self.num_tokens - 1]
-        start = self.num_cached
-        known = self.prompt_ids + self.output_ids
-        return known[start:start + n], list(range(start, start + n))
+        """New, preempted (recomputing) or part-way through a chunked prefill; decoding means exactly one
+        uncached token, the newest output."""
+        return self.num_cached == 0 or len(self.tokens) - self.num_cached > 1
 
     @property
     def step_cost(self) -> int:
-        return self.remaining
+        return len(self.tokens) - self.num_cached
+
+    def step_tokens(self, n: int | None = None) -> tuple[list[int], range]:
+        """(token ids, positions) of the next n uncached tokens (default: all of them)."""
+        a = self.num_cached
+        b = len(self.tokens) if n is None else a + n
+        return self.tokens[a:b], range(a, b)
 
 
 @dataclass
-class SchedulerOutput:
-    scheduled: list[Sequence]   # everyone running this step, in batch order
-    admitted: list[Sequence]    # the subset newly admitted this step
-    chunks: list[int] = field(default_factory=list)   # tokens each scheduled sequence processes
+class StepPlan:
+    """One step: the sequences that run, in batch order (decode rows first), and how many tokens each
+    feeds; `admitted` is the subset admitted this step."""
+    scheduled: list[Sequence] = field(default_factory=list)
+    chunks: list[int] = field(default_factory=list)
+    admitted: list[Sequence] = field(default_factory=list)
+    n_decode: int = 0
 
 
 class Scheduler:
@@ -84,20 +106,21 @@ class Scheduler:
         self.max_num_seqs = max_num_seqs
         self.max_num_batched_tokens = max_num_batched_tokens
         self.batch_wait_s = batch_wait_s
-        self.kv = kv
+        self.kv = kv                  # KV manager, or None for unlimited KV (host-logic tests)
         self.chunked_prefill = chunked_prefill
         self.waiting: deque[Sequence] = deque()
         self.running: list[Sequence] = []
         self.num_preemptions = 0
 
+    # ---------------------------------------------------------------------------- request lifetime
     def add(self, seq: Sequence) -> None:
-        n_prompt = len(seq.prompt_ids)
-        if not self.chunked_prefill and n_prompt > self.max_num_batched_tokens:
-            raise ValueError(f"prompt of {n_prompt} tokens exceeds the per-step token budget "
+        if not self.chunked_prefill and seq.n_prompt > self.max_num_batched_tokens:
+            raise ValueError(f"prompt of {seq.n_prompt} tokens exceeds the per-step token budget "
                              f"({self.max_num_batched_tokens}) and chunked prefill is off")
-        if self.kv is not None and not self.kv.can_ever_fit(n_prompt + seq.max_new_tokens):
-            raise ValueError(f"request needs up to {n_prompt + seq.max_new_tokens} tokens of KV, more than the "
-                             f"whole KV budget: it could never finish")
+        worst = seq.n_prompt + seq.max_new_tokens
+        if self.kv is not None and not self.kv.can_ever_fit(worst):
+            raise ValueError(f"request needs up to {worst} tokens of KV, more than the whole KV budget: "
+                             "it could never finish")
         seq.status = SeqStatus.WAITING
         self.waiting.append(seq)
 
@@ -108,76 +131,81 @@ class Scheduler:
             self.kv.free(seq)
 
     def abort(self, seq: Sequence) -> None:
-        """Drop a request wherever it is."""
-        if seq in self.running:
+        """Drop a request wherever it is (client went away)."""
+        if seq.status is SeqStatus.RUNNING and seq in self.running:
             self.finish(seq)
         elif seq in self.waiting:
             self.waiting.remove(seq)
             seq.status = SeqStatus.FINISHED
 
-    def _preempt(self, seq: Sequence) -> None:
-        """Free a running request's KV, keep its outputs, put it back at the front of the queue."""
-        self.running.remove(seq)
-        self.kv.free(seq)
-        seq.num_cached = 0
-        seq.status = SeqStatus.WAITING
-        self.waiting.appendleft(seq)
+    def has_unfinished(self) -> bool:
+        return bool(self.waiting) or bool(self.running)
+
+    # ------------------------------------------------------------------------------------ planning
+    def _evict_newest(self) -> None:
+        """Recompute-preemption of the most recently admitted running request: its KV is freed, its outputs
+        kept, and it waits at the head of the queue."""
+        victim = self.running.pop()
+        self.kv.free(victim)
+        victim.num_cached = 0
+        victim.status = SeqStatus.WAITING
+        self.waiting.appendleft(victim)
         self.num_preemptions += 1
 
-    def _reserve_decode_slots(self) -> None:
-        """Room for this step's token for every running request; preempt the newest while blocks run out."""
+    def _grow_running(self) -> None:
+        """Room for this step's token for every running request, evicting from the back as needed."""
         i = 0
         while i < len(self.running):
             if self.kv.try_append(self.running[i]):
                 i += 1
             else:
-                self._preempt(self.running[-1])   # may be running[i] itself: the loop then moves on
+                self._evict_newest()   # possibly running[i] itself: then i == len(running) and the loop ends
 
-    def has_unfinished(self) -> bool:
-        return bool(self.waiting or self.running)
-
-    def _may_admit(self, now: float) -> bool:
+    def _admission_open(self, now: float) -> bool:
         if self.policy == "continuous":
             return True
         if self.running or not self.waiting:
             return False
         return len(self.waiting) >= self.max_num_seqs or now - self.waiting[0].arrival_time >= self.batch_wait_s
 
-    def schedule(self, now: float) -> SchedulerOutput:
+    def _head_fits(self, budget: int, n_admitted: int) -> bool:
+        if not self.waiting or len(self.running) + n_admitted >= self.max_num_seqs:
+            return False
+        head = self.waiting[0]
+        if not (budget > 0 if self.chunked_prefill else head.step_cost <= budget):
+            return False
+        return self.kv is None or self.kv.can_admit(head)
+
+    def schedule(self, now: float) -> StepPlan:
         if self.kv is not None:
-            self._reserve_decode_slots()
+            self._grow_running()
+        plan = StepPlan()
         budget = self.max_num_batched_tokens
-        scheduled: list[Sequence] = []
-        chunks: list[int] = []
-        partial: list[Sequence] = []
-        for seq in self.running:
+        partial = []
+        for seq in self.running:                       # (1) decodes, one token each, always
             if seq.is_prefill:
                 partial.append(seq)
             else:
-                scheduled.append(seq)
-                chunks.append(1)
+                plan.scheduled.append(seq)
+                plan.chunks.append(1)
                 budget -= 1
-        for seq in partial:
+        plan.n_decode = len(plan.scheduled)
+        for seq in partial:                            # (2) chunked prefills already under way
             n = min(seq.remaining, budget) if self.chunked_prefill else seq.remaining
             if n > 0:
-                scheduled.append(seq)
-                chunks.append(n)
+                plan.scheduled.append(seq)
+                plan.chunks.append(n)
                 budget -= n
-        admitted: list[Sequence] = []
-        if self._may_admit(now):
-            while self.waiting and len(self.running) + len(admitted) < self.max_num_seqs:
-                head = self.waiting[0]
-                fits = budget > 0 if self.chunked_prefill else head.step_cost <= budget
-                if not fits or (self.kv is not None and not self.kv.can_admit(head)):
-                    break
+        if self._admission_open(now):                  # (3) admissions, first come first served
+            while self._head_fits(budget, len(plan.admitted)):
                 seq = self.waiting.popleft()
                 if self.kv is not None:
-                    self.kv.admit(seq)   # may start from cached prefix blocks: admit before sizing the chunk
+                    self.kv.admit(seq)                 # may start from cached prefix blocks
                 n = min(seq.step_cost, budget) if self.chunked_prefill else seq.step_cost
                 budget -= n
                 seq.status = SeqStatus.RUNNING
-                admitted.append(seq)
-                scheduled.append(seq)
-                chunks.append(n)
-            self.running.extend(admitted)
-        return SchedulerOutput(scheduled=scheduled, admitted=admitted, chunks=chunks)
+                plan.admitted.append(seq)
+                plan.scheduled.append(seq)
+                plan.chunks.append(n)
+            self.running.extend(plan.admitted)
+        return plan

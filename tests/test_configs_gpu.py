@@ -13,7 +13,6 @@ head of every table with refcount 32, and the streams with and without prefix ca
 under the tie rule, at reduced layers.
 """
 import dataclasses
-import random
 
 import pytest
 import torch
@@ -184,7 +183,7 @@ def test_config4_mixed_step_reduced_layers(hiplib, monkeypatch):
 
     def step(force_rows: bool):
         pool = PagedKVCache.from_token_budget(cfg, 2048 + sum(ctxs) + 16 * 17 + 64, 16, "cuda", torch.bfloat16)
-        random.Random(7).shuffle(pool.allocator._free)
+        pool.allocator.shuffle_free(7)
         if force_rows:
             monkeypatch.setattr(model, "_prefill_meta",
                                 lambda seqs, paged, sm, dtype: Qwen2Model._prefill_meta(model, seqs, paged, sm,
