@@ -30,13 +30,16 @@ prefix_sharing: BASELINE config 5 (3B shape, a 1024-token prefix shared by 32 re
 cache, 211-token suffixes): decode tokens/s and the step's HBM roofline, logical (a shared block counted
 once per row that reads it) and unique bytes.
 
-cpu_baseline: the CPU oracle (oracle/model.py, the reference algorithm restated in PyTorch) on this
-host's cores: one fp32 decode step of the same 1.5B shape at batch 32 with 1024-token contexts
-(random-valued caches), median of 3 timed steps after 1 warm-up.
+cpu_baseline: the CPU oracle (oracle/, the reference algorithm restated in PyTorch) on this process's
+physical cores (torch threads set to that count; the count, the logical CPUs and the CPU model are recorded):
+value = one fp32 decode step of the same 1.5B shape at batch 32 with 1024-token contexts (random-valued
+caches), median of 3 timed steps after 1 warm-up; `configs` holds bounded samples of configs 1, 2 (gather +
+SDPA per call, fp32 and bf16, also copied beside the roofline), 4 and 5.
 """
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -434,30 +437,186 @@ def pmc_traffic() -> int | None:
     return None
 
 
-def cpu_baseline(sd_cpu: dict, cfg, B: int, ctx: int) -> dict:
-    """The CPU oracle's decode step at the benchmark shape (fp32), bounded sample."""
-    from oracle.model import OracleModel
-    threads = torch.get_num_threads()
-    orc = OracleModel(cfg, sd_cpu, dtype=torch.float32)
-    g = torch.Generator().manual_seed(11)
-    caches = []
-    for _ in range(B):
-        c = orc.new_cache(ctx + 8)
-        c.k[:, :, :ctx].normal_(generator=g)
-        c.v[:, :, :ctx].normal_(generator=g)
-        c.length = ctx
-        caches.append(c)
-    toks = torch.randint(0, cfg.vocab_size, (B,), generator=g).tolist()
-    times = []
-    for r in range(4):
+def host_cpu() -> dict:
+    """This process's CPU share: physical cores (distinct package/core pairs among the CPUs it may run on),
+    capped by a cgroup CPU quota and by OMP_NUM_THREADS when those are set; the logical CPU count; the model
+    name from /proc/cpuinfo."""
+    aff = set(os.sched_getaffinity(0))
+    phys, model = set(), None
+    try:
+        for blk in open("/proc/cpuinfo").read().split("\n\n"):
+            d = dict((k.strip(), v.strip()) for k, v in (ln.split(":", 1) for ln in blk.splitlines() if ":" in ln))
+            if "processor" not in d:
+                continue
+            model = model or d.get("model name")
+            if int(d["processor"]) in aff:
+                phys.add((d.get("physical id", "0"), d.get("core id", d["processor"])))
+    except OSError:
+        pass
+    cores = len(phys) or len(aff)
+    caps = {}
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            caps["cgroup_quota_cpus"] = math.ceil(int(quota) / int(period))
+    except (OSError, ValueError):
+        pass
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        caps["OMP_NUM_THREADS"] = int(os.environ["OMP_NUM_THREADS"])
+    threads = min([cores] + [v for v in caps.values() if v > 0])
+    return {"threads": threads, "physical_cores": cores, "logical_cpus": os.cpu_count(), "affinity_cpus": len(aff),
+            "caps": caps, "model": model}
+
+
+def _timed(fn, reps: int = 3) -> float:
+    """Median seconds of `reps` calls after one warm-up call."""
+    fn()
+    ts = []
+    for _ in range(reps):
         t0 = time.perf_counter()
-        lg = orc.step([(c, [t]) for c, t in zip(caches, toks)])
-        toks = lg.argmax(-1).tolist()
-        times.append(time.perf_counter() - t0)
-    step_s = statistics.median(times[1:])
-    return {"value": round(B / step_s, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"CPU oracle fp32 decode step, 1.5B shape, batch {B}, {ctx}-token contexts "
-                      f"(random-valued caches), median of 3 steps after 1 warm-up: {step_s * 1e3:.0f} ms/step"}
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _filled_cache(orc, ctx: int, room: int, g) -> "object":
+    c = orc.new_cache(ctx + room)
+    c.k[:, :, :ctx].normal_(generator=g)
+    c.v[:, :, :ctx].normal_(generator=g)
+    c.length = ctx
+    return c
+
+
+def cpu_baseline(sd_cpu: dict, cfg, B: int, ctx: int) -> dict:
+    """The CPU oracle (oracle/, the reference's algorithm restated in PyTorch) on this host's physical cores,
+    for every BASELINE config, each a bounded sample timed with perf_counter (one warm-up, median of 3):
+      config 1: 0.5B shape fp32, batch 4, 128-token prompts: batched prefill time and decode tok/s over the
+                31 batched greedy steps that follow it;
+      config 2: gather + SDPA per call (oracle/ops.py paged_attention_reference), fp32 and bf16, on the
+                roofline's seeded draws (B 32, 14/2 heads, hd 64, contexts U[512, 4096]);
+      config 3: one fp32 decode step of the 1.5B shape, batch B, ctx-token contexts (random-valued caches);
+      config 4: one fp32 mixed step of the 1.5B shape (a 1536-token chunk on 512 cached tokens + 16 decode
+                rows, contexts U[256, 2048]);
+      config 5: fp32 decode step of the 3B shape at batch 32 with 1235-token contexts, from 2- and 4-layer
+                slices (time = a + b * layers, extrapolated to 36 layers); the oracle keeps one cache per
+                sequence, so prefix sharing changes nothing it computes.
+    The headline value is config 3's tokens/s (the bench's own workload)."""
+    from nanoserve_amd.model import QWEN25_0_5B, QWEN25_3B, random_state_dict
+    from oracle.model import OracleModel
+    from oracle.ops import paged_attention_reference
+    host = host_cpu()
+    torch.set_num_threads(host["threads"])
+    g = torch.Generator().manual_seed(11)
+    out = {"host": host}
+
+    # config 3 (headline): the bench's decode step
+    orc = OracleModel(cfg, sd_cpu, dtype=torch.float32)
+    caches = [_filled_cache(orc, ctx, 8, g) for _ in range(B)]
+    toks = torch.randint(0, cfg.vocab_size, (B,), generator=g).tolist()
+
+    def step3():
+        for c in caches:
+            c.length = ctx
+        orc.step([(c, [t]) for c, t in zip(caches, toks)])
+    s3 = _timed(step3)
+    out["config3"] = {"ms_per_step": round(s3 * 1e3, 1), "tok_s": round(B / s3, 2)}
+    log(f"cpu config 3: {s3 * 1e3:.0f} ms/step")
+
+    # config 4: one mixed step on the same weights
+    g4 = torch.Generator().manual_seed(2)
+    ctxs = torch.randint(256, 2049, (16,), generator=g4).tolist()
+    ca = _filled_cache(orc, 512, 1536, g)
+    dec = [_filled_cache(orc, c, 1, g) for c in ctxs]
+    chunk = torch.randint(0, cfg.vocab_size, (1536,), generator=g4).tolist()
+    last = torch.randint(0, cfg.vocab_size, (16,), generator=g4).tolist()
+
+    def step4():
+        ca.length = 512
+        for c, n in zip(dec, ctxs):
+            c.length = n
+        orc.step([(ca, chunk)] + [(c, [t]) for c, t in zip(dec, last)])
+    s4 = _timed(step4)
+    out["config4"] = {"ms_per_mixed_step": round(s4 * 1e3, 1), "rows": 1552}
+    log(f"cpu config 4: {s4 * 1e3:.0f} ms/mixed step")
+    del orc, caches, ca, dec
+
+    # config 2: gather + SDPA per call
+    NB, NKV, HD, NH = 65536, 2, 64, 14
+    g2 = torch.Generator().manual_seed(2)
+    kf = torch.randn(NB, 16, NKV, HD, generator=g2)
+    vf = torch.randn(NB, 16, NKV, HD, generator=g2)
+    perm = torch.randperm(NB, generator=g2)
+    cl = torch.randint(512, 4097, (32,), generator=g2)
+    tab = torch.zeros(32, 256, dtype=torch.int32)
+    used = 0
+    for i, c in enumerate(cl.tolist()):
+        n = -(-c // 16)
+        tab[i, :n] = perm[used:used + n].int()
+        used += n
+    qf = torch.randn(32, NH, HD, generator=g2)
+    c2 = {}
+    for name, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        kk, vv, qq = kf.to(dt), vf.to(dt), qf.to(dt)
+        t2 = _timed(lambda: paged_attention_reference(qq, kk, vv, tab, cl, HD ** -0.5))
+        nbytes = int(cl.sum()) * NKV * HD * 2 * kk.element_size() + 2 * 32 * NH * HD * kk.element_size()
+        c2[name] = {"ms_per_call": round(t2 * 1e3, 2), "effective_GBs": round(nbytes / t2 / 1e9, 2)}
+        del kk, vv, qq
+    out["config2"] = c2
+    log(f"cpu config 2: gather+SDPA {c2['fp32']['ms_per_call']} ms (fp32), {c2['bf16']['ms_per_call']} ms (bf16)")
+    del kf, vf
+
+    # config 1: 0.5B fp32, batch 4, 128-token prompts, prefill + 31 decode steps
+    orc1 = OracleModel(QWEN25_0_5B, random_state_dict(QWEN25_0_5B, seed=0, dtype=torch.float32))
+    g1 = torch.Generator().manual_seed(1)
+    prompts = [torch.randint(0, QWEN25_0_5B.vocab_size, (128,), generator=g1).tolist() for _ in range(4)]
+    cs1 = [orc1.new_cache(160) for _ in prompts]
+    res = {}
+
+    def run1():
+        for c in cs1:
+            c.length = 0
+            c.tokens = []
+        t0 = time.perf_counter()
+        lg = orc1.step([(c, p) for c, p in zip(cs1, prompts)])
+        t1 = time.perf_counter()
+        nxt = lg.argmax(-1).tolist()
+        for _ in range(31):
+            nxt = orc1.step([(c, [t]) for c, t in zip(cs1, nxt)]).argmax(-1).tolist()
+        res.setdefault("prefill", []).append(t1 - t0)
+        res.setdefault("decode", []).append(time.perf_counter() - t1)
+    for _ in range(4):
+        run1()
+    pre, decs = statistics.median(res["prefill"][1:]), statistics.median(res["decode"][1:])
+    out["config1"] = {"prefill_ms": round(pre * 1e3, 1), "decode_tok_s": round(4 * 31 / decs, 2)}
+    log(f"cpu config 1: prefill {pre * 1e3:.0f} ms, decode {4 * 31 / decs:.1f} tok/s")
+    del orc1, cs1
+
+    # config 5: 3B shape from 2- and 4-layer slices
+    t5 = {}
+    for L in (2, 4):
+        c5 = dataclasses.replace(QWEN25_3B, n_layers=L)
+        o5 = OracleModel(c5, random_state_dict(c5, seed=5, dtype=torch.float32))
+        cc = [_filled_cache(o5, 1235, 2, g) for _ in range(32)]
+        tk = torch.randint(0, c5.vocab_size, (32,), generator=g).tolist()
+
+        def step5():
+            for c in cc:
+                c.length = 1235
+            o5.step([(c, [t]) for c, t in zip(cc, tk)])
+        t5[L] = _timed(step5)
+        del o5, cc
+    per_layer = (t5[4] - t5[2]) / 2
+    s5 = t5[2] + per_layer * (QWEN25_3B.n_layers - 2)
+    out["config5"] = {"ms_per_step": round(s5 * 1e3, 1), "tok_s": round(32 / s5, 2),
+                      "sliced_ms": {str(k): round(v * 1e3, 1) for k, v in t5.items()}}
+    log(f"cpu config 5: {s5 * 1e3:.0f} ms/step (extrapolated)")
+
+    return {"value": round(B / s3, 2), "unit": "tokens/s", "cores": host["threads"], "kind": "port",
+            "sample": f"CPU oracle (fp32 PyTorch restatement of the reference) on {host['threads']} threads = "
+                      f"physical cores of this process's CPU share ({host['model']}): config-3 decode step, 1.5B "
+                      f"shape, batch {B}, {ctx}-token random-valued contexts, median of 3 steps after 1 "
+                      f"warm-up: {s3 * 1e3:.0f} ms/step; per-config samples under 'configs'",
+            "configs": out}
 
 
 def main() -> int:
@@ -541,6 +700,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         cpu = cpu_baseline(sd_cpu, cfg, B, P)
         log(f"cpu: {cpu['value']} tok/s on {cpu['cores']} threads")
+        roof["cpu_gather_sdpa"] = cpu["configs"]["config2"]
 
     out = {
         "metric": "decode tok/s, Qwen2.5-1.5B-shape b=32; paged-attn HBM GB/s as % of peak",
