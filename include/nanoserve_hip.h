@@ -179,7 +179,8 @@ int ns_embed_rope(const int64_t* token_ids, const int64_t* positions, int64_t n_
                   void* sin_out, float* row_sumsq, int dtype, void* stream);
 
 /*
- * Skinny GEMMs of the decode step (bf16, 1 <= M <= 64, K a multiple of 32; W row-major [N, K], x [M, K],
+ * GEMMs of the decode loop (bf16, K a multiple of 32; skinny kernels for 1 <= M <= 64, and for ns_gemm and
+ * ns_gemm_silu_mul a tiled kernel above that; W row-major [N, K], x [M, K],
  * outputs row-major, every pointer 16-byte aligned). They replace the F.linear calls of
  * nanoserve/model.py:231,256-257,362 for decode-sized batches: y = x W^T (+ bias) with fp32 accumulation
  * and one rounding to bf16, like F.linear; each fused variant rounds where the unfused ops it replaces
@@ -202,7 +203,14 @@ size_t ns_gemm_workspace_bytes(int M, int N, int K);
  * x_sumsq == NULL: x is used as is (x_norm_w, x_eps ignored).
  */
 
-/* y = round(x W^T + bias); bias may be NULL. */
+/*
+ * y = round(x W^T + bias); bias may be NULL.
+ * Any M >= 1: above 64 rows (prefill chunks, mixed steps, speculative verify batches; nanoserve/model.py:231,
+ * 256-257 on the large-token path) a tiled MFMA kernel computes the product (128 x 128 or 256 x 256 output
+ * tiles, K sliced and the slices summed in a fixed order when there are few tiles); x_sumsq must then be NULL
+ * (materialise a normalised input with ns_rms_norm_apply first), and the workspace is sized by
+ * ns_gemm_workspace_bytes(M, N, K) as for the skinny kernels.
+ */
 int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, int dtype,
             const float* x_sumsq, const void* x_norm_w, float x_eps,
             void* workspace, size_t workspace_bytes, void* stream);
@@ -211,7 +219,7 @@ int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int 
  * Merged gate/up projection + SwiGLU: w_gate_up = [gate; up] ([N2, K], N2 = 2 * intermediate);
  * out[M, N2/2] = round(round(silu(round(x Wg^T))) * round(x Wu^T)).
  * Replaces silu_mul(F.linear(h, gate_up_w)) (nanoserve/model.py:257, fused.py:75).
- * Workspace: ns_gemm_workspace_bytes(M, N2, K).
+ * Workspace: ns_gemm_workspace_bytes(M, N2, K). Any M >= 1 (above 64 rows: the tiled kernel, as ns_gemm).
  */
 int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int N2, int K, int dtype,
                      const float* x_sumsq, const void* x_norm_w, float x_eps,

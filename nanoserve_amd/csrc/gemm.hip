@@ -38,6 +38,7 @@
 //            qkv = round(acc + bias), then out_lo = r(r(xl cl) - r(xh sl)), out_hi = r(r(xh ch) + r(xl sh))
 //            for q and k heads, v copied; k and v also stored at the token's cache slot
 // Cross-workgroup data moves through agent-scope atomic stores/loads (ns_common.h: publish_*).
+#include <climits>
 #include <cstdlib>
 #include <type_traits>
 
@@ -1002,6 +1003,288 @@ __global__ __launch_bounds__(64) void rms_norm_apply_kernel(const bf16_t* __rest
   }
 }
 
+// ------------------------------------------------------------------------------------- tiled GEMM (M > 64)
+// Prefill chunks, mixed steps and speculative verify batches: Y[M, N] = X[M, K] . W[N, K]^T for any M, bf16
+// in, fp32 accumulate, with the STORE (+ bias) and SILU epilogues of the skinny kernels (same rounding).
+//   * BM x BN output tiles (SILU: BN/2 gate rows + the matching BN/2 up rows of W -> BN/2 output columns),
+//     2 x WN waves, each BM/2 x 64 (WM x 4 mfma_f32_16x16x32_bf16 tiles). Two shapes: 256 x 256 (8 waves,
+//     one workgroup per CU) and 128 x 128 (4 waves, three per CU); the larger tile moves half the L2 -> LDS
+//     bytes per flop, so the plan takes it whenever it alone fills the GPU.
+//   * K in 32-wide steps through a ring of S LDS stages (BM x 64 bytes of X rows + BN x 64 bytes of W rows
+//     each; four stages at one workgroup per CU, three at three), filled by buffer DMA (16 bytes per lane, each instruction 16 rows x 64 bytes; rows past M
+//     or N and empty trailing stages read zeros through the buffer bounds, with no memory access). Each
+//     64-byte row keeps its four 16-byte chunks XOR-swizzled by (row / 2) & 3, so the 16-lane fragment reads
+//     are free of bank conflicts. One barrier per step: a wave waits for its own DMA of the step (vmcnt), the
+//     barrier makes every wave's part visible and retires the stage read one step earlier, which is
+//     refilled next. Fragment reads are inline asm, so the compiler does not drain the DMA ring before them.
+//   * Few tiles, or long K with fewer tiles than CUs: K is cut into `splits` slices; each publishes its fp32
+//     tile to the workspace (agent-scope stores, a per-tile arrival counter in the fixed counter region) and
+//     the last to arrive sums the slices in slice order -- deterministic -- and runs the epilogue.
+//   * Epilogue: the tile goes through LDS as fp32 in passes of [64][132] and 256 threads finish it in
+//     row-contiguous 16-byte pieces.
+constexpr int TG_BK = 32;
+constexpr int TG_CROWS = 64;                  // output rows per epilogue pass
+constexpr int TG_MAX_SPLITS = 16;
+constexpr int TG_RSRC3 = 0x00020000;          // buffer resource word 3: raw (untyped) 32-bit accesses
+
+template <int WN, int WM>
+struct TgShape {
+  static constexpr int NW = 2 * WN;                         // waves
+  static constexpr int NT = 64 * NW;                        // threads
+  static constexpr int BM = 32 * WM;                        // X rows of a tile
+  static constexpr int BN = 64 * WN;                        // W rows of a tile
+  static constexpr int S = NW == 8 ? 4 : 3;                 // ring stages (one workgroup per CU: four)
+  static constexpr int AROWS = BM * TG_BK * 2;              // bytes of the X rows of a stage
+  static constexpr int STAGE = AROWS + BN * TG_BK * 2;
+  static constexpr int CP = BN + 4;                         // floats per row of the staged output tile
+  static constexpr int LDS = S * STAGE > TG_CROWS * CP * 4 ? S * STAGE : TG_CROWS * CP * 4;
+  static constexpr int WG_PER_CU = NW == 8 ? 1 : 3;
+  static constexpr int PART = BM * BN;                      // floats of one published slice of a tile
+  static constexpr int AJ = BM / (16 * NW), BJ = BN / (16 * NW);   // DMA instructions per wave per stage
+  static constexpr int DMA = AJ + BJ;
+};
+
+struct TgArgs {
+  const bf16_t* x;
+  const bf16_t* w;
+  const bf16_t* bias;
+  bf16_t* y;
+  int M, N, K;         // N: rows of w (SILU: gate rows then up rows)
+  int tiles_m, tiles_n, splits, kps;   // kps: 32-wide k-steps per slice
+  unsigned* cnt;
+  float* part;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tg_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, int(bytes), TG_RSRC3);
+}
+__device__ __forceinline__ uint32_t tg_lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+// four 16-byte fragment reads, one wait (early-clobber: a read's data may land before a later read issues)
+__device__ __forceinline__ void tg_read4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, g_u32x4_t& v0,
+                                         g_u32x4_t& v1, g_u32x4_t& v2, g_u32x4_t& v3) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+}
+// Workgroup barrier for LDS data (no wait for the wave's outstanding DMA, unlike __syncthreads)
+__device__ __forceinline__ void tg_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// waitcnt immediate: at most n vector memory operations of this wave still outstanding
+constexpr int tg_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+
+template <int EPI, int WN, int WM>
+__global__ __launch_bounds__((TgShape<WN, WM>::NT), (TgShape<WN, WM>::WG_PER_CU)) void tiled_gemm_kernel(TgArgs a) {
+  using SH = TgShape<WN, WM>;
+  constexpr int BM = SH::BM, BN = SH::BN, NT = SH::NT, CP = SH::CP;
+  __shared__ __align__(16) unsigned char lds[SH::LDS];
+  __shared__ unsigned s_last;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int tiles = a.tiles_m * a.tiles_n, grid = tiles * a.splits;
+  // XCD-aware order: workgroup i runs on XCD i % 8, so consecutive tiles (same W rows, successive X rows)
+  // go to one XCD and share its L2
+  int bid = blockIdx.x;
+  if (grid % 8 == 0) bid = (bid & 7) * (grid >> 3) + (bid >> 3);
+  const int split = bid / tiles, t = bid - split * tiles;
+  const int tm = t % a.tiles_m, tn = t / a.tiles_m;
+  const int m0 = tm * BM;
+  const int K = a.K, M = a.M, N = a.N, half = N >> 1;
+  const int kb = split * a.kps, nk = min(a.kps, K / TG_BK - kb);
+
+  // DMA lanes: X instruction j of wave w stages rows 16 (AJ w + j) + l / 4, W instruction j rows
+  // 16 (BJ w + j) + l / 4; slot l % 4 of a row holds chunk (l % 4) ^ ((row / 2) & 3). Row offsets go in the
+  // per-lane offset, so rows past M / N fail the bounds.
+  constexpr int AJ = SH::AJ, BJ = SH::BJ;
+  uint32_t voa[AJ], vob[BJ];
+#pragma unroll
+  for (int j = 0; j < AJ; ++j) {
+    const int r = 16 * (AJ * w + j) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
+    voa[j] = (uint32_t(m0 + r) * uint32_t(K) + uint32_t(8 * c)) * 2u;
+  }
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    const int r = 16 * (BJ * w + j) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
+    const int wrow = EPI == EPI_SILU ? (r < BN / 2 ? (BN / 2) * tn + r : half + (BN / 2) * tn + r - BN / 2) : BN * tn + r;
+    vob[j] = (uint32_t(wrow) * uint32_t(K) + uint32_t(8 * c)) * 2u;
+  }
+  const __amdgpu_buffer_rsrc_t xr = tg_rsrc(a.x, uint32_t(M) * uint32_t(K) * 2u), xnone = tg_rsrc(a.x, 0u);
+  const __amdgpu_buffer_rsrc_t wr = tg_rsrc(a.w, uint32_t(N) * uint32_t(K) * 2u), wnone = tg_rsrc(a.w, 0u);
+  auto issue = [&](int q) __attribute__((always_inline)) {   // stage q of the slice (past nk: zeros, no traffic)
+    const bool live = q < nk;
+    const __amdgpu_buffer_rsrc_t xs = live ? xr : xnone, wsr = live ? wr : wnone;
+    const int soff = live ? (kb + q) * TG_BK * 2 : 0;
+    unsigned char* st = lds + (q % SH::S) * SH::STAGE;
+#pragma unroll
+    for (int j = 0; j < AJ; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (__attribute__((address_space(3))) void*)(st + 16 * (AJ * w + j) * 64),
+                                               16, int(voa[j]), soff, 0, 0);
+#pragma unroll
+    for (int j = 0; j < BJ; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (__attribute__((address_space(3))) void*)(st + SH::AROWS + 16 * (BJ * w + j) * 64),
+                                               16, int(vob[j]), soff, 0, 0);
+  };
+#pragma unroll
+  for (int q = 0; q < SH::S - 1; ++q) issue(q);
+
+  // fragment offsets within a stage: lane -> row l % 16 of the 16-row tile, 16-byte chunk l / 16
+  const int wm = w & 1, wn = w >> 1;
+  uint32_t fa[WM], fb[4];
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int ra = (BM / 2) * wm + 16 * i + (l & 15);
+    fa[i] = uint32_t(ra * 64 + 16 * ((l >> 4) ^ ((ra >> 1) & 3)));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rb = 64 * wn + 16 * i + (l & 15);
+    fb[i] = uint32_t(SH::AROWS + rb * 64 + 16 * ((l >> 4) ^ ((rb >> 1) & 3)));
+  }
+  g_float4_t acc[WM][4];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
+  const uint32_t lds0 = tg_lds_addr(lds);
+  for (int q = 0; q < nk; ++q) {
+    __builtin_amdgcn_s_waitcnt(tg_vmcnt(SH::DMA * (SH::S - 2)));   // this wave's loads of stage q are done
+    tg_barrier();                                                 // ... and every wave's; stage q - 1 is free
+    issue(q + SH::S - 1);
+    const uint32_t sb = lds0 + uint32_t((q % SH::S) * SH::STAGE);
+    g_u32x4_t bf[4];
+    tg_read4(sb + fb[0], sb + fb[1], sb + fb[2], sb + fb[3], bf[0], bf[1], bf[2], bf[3]);
+#pragma unroll
+    for (int i0 = 0; i0 < WM; i0 += 4) {
+      g_u32x4_t af[4];
+      tg_read4(sb + fa[i0], sb + fa[i0 + 1], sb + fa[i0 + 2], sb + fa[i0 + 3], af[0], af[1], af[2], af[3]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i0 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, af[i]),
+                                                                   __builtin_bit_cast(g_bf16x8_t, bf[j]),
+                                                                   acc[i0 + i][j], 0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(tg_vmcnt(0));
+  tg_barrier();
+
+  // ---- K slices: publish, count, and the last slice sums them in slice order
+  if (a.splits > 1) {
+    float* mine = a.part + (int64_t(t) * a.splits + split) * SH::PART;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const g_float4_t v = acc[i][j];
+        publish_store16(mine + (int64_t(i * 4 + j) * NT + tid) * 4,
+                        pub_u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                    __float_as_uint(v[3])});
+      }
+    publish_complete();
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = publish_count(a.cnt + t);
+      const bool last = prev == unsigned(a.splits - 1);
+      if (last) publish_reset(a.cnt + t);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last == 0u) return;
+    acquire_published();
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
+    const float* base = a.part + int64_t(t) * a.splits * SH::PART;
+    for (int s = 0; s < a.splits; ++s) {
+#pragma unroll
+      for (int i0 = 0; i0 < WM; i0 += 4) {
+        pub_u32x4_t v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          v[e] = publish_load16(base + int64_t(s) * SH::PART + (int64_t(i0 * 4 + e) * NT + tid) * 4);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i0 + (e >> 2)][e & 3][r] += __uint_as_float(v[e][r]);
+      }
+    }
+  }
+
+  // ---- the tile through LDS in passes of 64 rows (pass p: the waves with wm == p / (WM / 4), their m-tiles
+  // 4 (p % (WM / 4)) .. + 3): C[m][n] (lane: column l % 16, rows 4 (l / 16) + r of each 16 x 16 tile)
+  float* C = reinterpret_cast<float*>(lds);
+  constexpr int PASSES = BM / TG_CROWS, PW = WM / 4;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    if (wm == p / PW) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            C[(16 * i + 4 * (l >> 4) + r) * CP + 64 * wn + 16 * j + (l & 15)] = acc[4 * (p % PW) + i][j][r];
+    }
+    __syncthreads();
+    const int mb = m0 + TG_CROWS * p;
+    if constexpr (EPI == EPI_STORE) {
+      // items (row m, 8 columns): 64 x BN / 8
+      constexpr int IPR = BN / 8;
+#pragma unroll 2
+      for (int it = tid; it < TG_CROWS * IPR; it += NT) {
+        const int m = it / IPR, c8 = it % IPR, gm = mb + m, gn = BN * tn + 8 * c8;
+        if (gm >= M || gn >= N) continue;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = C[m * CP + 8 * c8 + e];
+        if (a.bias != nullptr) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] += gn + e < N ? bf16_to_f32(a.bias[gn + e]) : 0.f;
+        }
+        bf16_t* dst = a.y + int64_t(gm) * N + gn;
+        if ((N & 7) == 0) {
+          store_bf16x8(dst, v);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gn + e < N) dst[e] = f32_to_bf16(v[e]);
+        }
+      }
+    } else {   // EPI_SILU: columns [0, BN/2) gate, [BN/2, BN) up; items (row m, 8 output columns): 64 x BN / 16
+      constexpr int IPR = BN / 16;
+#pragma unroll 2
+      for (int it = tid; it < TG_CROWS * IPR; it += NT) {
+        const int m = it / IPR, c8 = it % IPR, gm = mb + m, gn = (BN / 2) * tn + 8 * c8;
+        if (gm >= M || gn >= half) continue;
+        float out[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float gb = round_bf16(C[m * CP + 8 * c8 + e]), ub = round_bf16(C[m * CP + BN / 2 + 8 * c8 + e]);
+          out[e] = round_bf16(gb / (1.0f + expf(-gb))) * ub;
+        }
+        bf16_t* dst = a.y + int64_t(gm) * half + gn;
+        if ((half & 7) == 0) {
+          store_bf16x8(dst, out);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gn + e < half) dst[e] = f32_to_bf16(out[e]);
+        }
+      }
+    }
+    if (p + 1 < PASSES) __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------------------------------------- host side
 // Workgroups that stream at once: one per CU (NS_GEMM_WGS overrides, for experiments).
 static int target_workgroups() {
@@ -1049,9 +1332,10 @@ static Plan make_plan(int tiles, int K) {
   return p;
 }
 
-static int check_common(const void* x, const void* w, int M, int N, int K, int dtype) {
+// max_m: G_MAX_M for the entry points that only have skinny kernels, INT_MAX where M > 64 goes tiled
+static int check_common(const void* x, const void* w, int M, int N, int K, int dtype, int max_m = G_MAX_M) {
   NS_REQUIRE(dtype == NS_DTYPE_BF16, "skinny gemm: bf16 only (dtype %d)", dtype);
-  NS_REQUIRE(M >= 1 && M <= G_MAX_M, "skinny gemm: M=%d outside [1, %d]", M, G_MAX_M);
+  NS_REQUIRE(M >= 1 && M <= max_m, "skinny gemm: M=%d outside [1, %d]", M, max_m);
   NS_REQUIRE(N >= 1 && K >= 32 && K % 32 == 0, "skinny gemm: N=%d K=%d (K must be a positive multiple of 32)", N, K);
   NS_REQUIRE(x != nullptr && w != nullptr, "skinny gemm: null operand");
   NS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
@@ -1189,6 +1473,80 @@ static int bind_xnorm(GemmArgs& a, const float* x_sumsq, const void* x_norm_w, f
   return NS_OK;
 }
 
+// ---- tiled GEMM plan and launch (M > 64)
+struct TgPlan {
+  int wn, wm;   // tile 32 wm x 64 wn: (4, 8) 256 x 256, (2, 4) 128 x 128
+  int tiles_m, tiles_n, splits, kps;
+  size_t bytes;   // workspace (0: no K slices)
+};
+static void tg_tiles(TgPlan& p, int M, int N, bool silu) {
+  const int bm = 32 * p.wm, bn = 64 * p.wn;
+  p.tiles_m = (M + bm - 1) / bm;
+  p.tiles_n = silu ? (N / 2 + bn / 2 - 1) / (bn / 2) : (N + bn - 1) / bn;
+}
+// 256 x 256 tiles when there is one for every CU; otherwise 128 x 128 tiles, and K is sliced when there are
+// fewer tiles than half the CU count, or fewer than the CU count with long K (at least 128 steps): enough
+// slices to reach the CU count, each at least eight 32-wide steps, at most TG_MAX_SPLITS.
+static TgPlan tg_plan(int M, int N, int K, bool silu) {
+  TgPlan p;
+  const int T = target_workgroups(), steps = K / TG_BK;
+  p.wn = 4;
+  p.wm = 8;
+  tg_tiles(p, M, N, silu);
+  if (int64_t(p.tiles_m) * p.tiles_n < T) {
+    p.wn = 2;
+    p.wm = 4;
+    tg_tiles(p, M, N, silu);
+  }
+  const int tiles = p.tiles_m * p.tiles_n;
+  int splits = 1;
+  if (tiles < T / 2 || (tiles < T && steps >= 128)) {
+    splits = (T + tiles - 1) / tiles;
+    if (splits > TG_MAX_SPLITS) splits = TG_MAX_SPLITS;
+    if (splits > steps / 8) splits = steps / 8 > 1 ? steps / 8 : 1;
+  }
+  p.kps = (steps + splits - 1) / splits;
+  p.splits = (steps + p.kps - 1) / p.kps;   // every slice non-empty
+  p.bytes = p.splits > 1 ? G_CNT_BYTES + align256(sizeof(float) * size_t(tiles) * p.splits * 32 * p.wm * 64 * p.wn) : 0;
+  return p;
+}
+template <int EPI>
+static int launch_tiled(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, void* ws,
+                        size_t ws_bytes, hipStream_t st) {
+  // 32-bit buffer offsets: every row offset of X and W (plus a tile's overhang) must fit
+  NS_REQUIRE((int64_t(M) + 256) * K * 2 < (int64_t(1) << 31) && (int64_t(N) + 256) * K * 2 < (int64_t(1) << 31),
+             "gemm: X [%d, %d] or W [%d, %d] too large for 32-bit buffer offsets", M, K, N, K);
+  const TgPlan p = tg_plan(M, N, K, EPI == EPI_SILU);
+  TgArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.w = static_cast<const bf16_t*>(w);
+  a.bias = static_cast<const bf16_t*>(bias);
+  a.y = static_cast<bf16_t*>(y);
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.tiles_m = p.tiles_m;
+  a.tiles_n = p.tiles_n;
+  a.splits = p.splits;
+  a.kps = p.kps;
+  if (p.splits > 1) {
+    NS_REQUIRE(p.tiles_m * p.tiles_n <= G_MAX_TILES, "gemm: %d tiles exceed the counter region", p.tiles_m * p.tiles_n);
+    if (ws == nullptr || ws_bytes < p.bytes || reinterpret_cast<uintptr_t>(ws) % 256 != 0) {
+      set_error("gemm: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed, got %zu", p.bytes,
+                ws == nullptr ? size_t(0) : ws_bytes);
+      return NS_E_WORKSPACE;
+    }
+    a.cnt = static_cast<unsigned*>(ws);
+    a.part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + G_CNT_BYTES);
+  }
+  const dim3 grid(unsigned(p.tiles_m * p.tiles_n * p.splits));
+  if (p.wn == 4)
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 4, 8>), grid, dim3(TgShape<4, 8>::NT), 0, st, a);
+  else
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 2, 4>), grid, dim3(TgShape<2, 4>::NT), 0, st, a);
+  return check_launch("gemm(tiled)");
+}
+
 static GemmArgs base_args(const void* x, const void* w, int M, int N, int K) {
   GemmArgs a{};
   a.x = static_cast<const bf16_t*>(x);
@@ -1208,15 +1566,23 @@ using namespace ns;
 // Largest workspace any entry point needs for this shape (the SILU plan has at most as many tiles).
 extern "C" size_t ns_gemm_workspace_bytes(int M, int N, int K) {
   if (M < 1 || N < 1 || K < 32) return 0;
+  if (M > G_MAX_M) {
+    const size_t a = tg_plan(M, N, K, false).bytes, b = tg_plan(M, N, K, true).bytes;
+    return a > b ? a : b;
+  }
   return make_plan((N + 63) / 64, K).bytes;
 }
 
 extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, int dtype,
                        const float* x_sumsq, const void* x_norm_w, float x_eps, void* ws, size_t ws_bytes,
                        void* stream) {
-  int st = check_common(x, w, M, N, K, dtype);
+  int st = check_common(x, w, M, N, K, dtype, INT_MAX);
   if (st != NS_OK) return st;
   NS_REQUIRE(y != nullptr && aligned16(y), "gemm: output must be 16-byte aligned");
+  if (M > G_MAX_M) {
+    NS_REQUIRE(x_sumsq == nullptr, "gemm: a normalised input (x_sumsq) needs M <= %d", G_MAX_M);
+    return launch_tiled<EPI_STORE>(x, w, bias, y, M, N, K, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+  }
   GemmArgs a = base_args(x, w, M, N, K);
   a.bias = static_cast<const bf16_t*>(bias);
   a.y = static_cast<bf16_t*>(y);
@@ -1230,10 +1596,15 @@ extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, 
 extern "C" int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int N2, int K, int dtype,
                                 const float* x_sumsq, const void* x_norm_w, float x_eps, void* ws, size_t ws_bytes,
                                 void* stream) {
-  int st = check_common(x, w_gate_up, M, N2, K, dtype);
+  int st = check_common(x, w_gate_up, M, N2, K, dtype, INT_MAX);
   if (st != NS_OK) return st;
   NS_REQUIRE(N2 % 2 == 0, "gemm_silu_mul: merged gate/up rows %d must be even", N2);
   NS_REQUIRE(out != nullptr && aligned16(out), "gemm_silu_mul: output must be 16-byte aligned");
+  if (M > G_MAX_M) {
+    NS_REQUIRE(x_sumsq == nullptr, "gemm_silu_mul: a normalised input (x_sumsq) needs M <= %d", G_MAX_M);
+    return launch_tiled<EPI_SILU>(x, w_gate_up, nullptr, out, M, N2, K, ws, ws_bytes,
+                                  reinterpret_cast<hipStream_t>(stream));
+  }
   GemmArgs a = base_args(x, w_gate_up, M, N2, K);
   a.y = static_cast<bf16_t*>(out);
   if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;

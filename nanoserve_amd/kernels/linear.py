@@ -1,11 +1,12 @@
 """Projection GEMMs of the decode loop: y = x @ W^T (+ b), x [M, K], W [N, K] row-major.
 
 The one indirection point for every projection of the model (QKV, O, gate/up, down, LM head;
-nanoserve/model.py:231,256-257,362). Decode-sized bf16 products (M <= 64) run the skinny HIP GEMMs
-(csrc/gemm.hip), which stream each weight once and fold the neighbouring token-wise ops into their
-epilogues; larger products (prefill chunks) and fp32 go to the vendor GEMM through torch (hipBLASLt on
-ROCm) followed by the standalone HIP token-wise kernels. Both routes round where the unfused PyTorch ops
-round, so they differ only in the fp32 summation order of the products.
+nanoserve/model.py:231,256-257,362). Every bf16 product runs a HIP GEMM of csrc/gemm.hip: decode-sized ones
+(M <= 64) the skinny kernels, which stream each weight once and fold the neighbouring token-wise ops into
+their epilogues; larger ones (prefill chunks, mixed steps, speculative verify batches) the tiled MFMA
+kernel, with the SiLU epilogue fused and the residual/RMSNorm and RoPE steps in the standalone HIP
+token-wise kernels. fp32 (the correctness paths) goes through torch. Every route rounds where the unfused
+PyTorch ops round, so they differ only in the fp32 summation order of the products.
 
 RMSNorm between projections is not a pass of its own on the skinny route: the projection that produces
 the residual stream also writes per-16-column row sums of its square, and the projection that consumes
@@ -95,12 +96,26 @@ def _dense(x) -> torch.Tensor:
     return x.tensor() if isinstance(x, NormedRows) else x
 
 
-def skinny_ok(x, w: torch.Tensor) -> bool:
+def hip_ok(x, w: torch.Tensor) -> bool:
+    """A product the HIP GEMMs take: bf16 on the GPU, K a multiple of 32, contiguous 16-byte aligned operands."""
     t = x.r if isinstance(x, NormedRows) else x
     M, K = t.shape
-    return (t.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and t.device.type == "cuda" and 1 <= M <= SKINNY_MAX_M
+    return (t.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and t.device.type == "cuda" and M >= 1
             and K % 32 == 0 and t.is_contiguous() and w.is_contiguous() and t.data_ptr() % 16 == 0
             and w.data_ptr() % 16 == 0)
+
+
+def skinny_ok(x, w: torch.Tensor) -> bool:
+    """A decode-sized product (M <= 64): the skinny kernels, with norm on load and the fused epilogues."""
+    return hip_ok(x, w) and x.shape[0] <= SKINNY_MAX_M
+
+
+def _tiled_input(x) -> torch.Tensor:
+    """The tiled kernel reads a plain tensor: a NormedRows input is materialised first."""
+    x = _dense(x)
+    if not (x.is_contiguous() and x.data_ptr() % 16 == 0):
+        x = x.contiguous()
+    return x
 
 
 def _x_args(x):
@@ -117,8 +132,10 @@ def _ws_args(x, N: int):
 
 
 def linear(x, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
-    if not skinny_ok(x, w):
+    if not hip_ok(x, w):
         return F.linear(_dense(x), w, b)
+    if not skinny_ok(x, w):
+        x = _tiled_input(x)
     M, K = x.shape
     N = w.shape[0]
     y = torch.empty(M, N, device=x.device, dtype=x.dtype)
@@ -130,8 +147,10 @@ def linear(x, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
 
 
 def linear_silu_mul(x, w_gate_up: torch.Tensor) -> torch.Tensor:
-    if not skinny_ok(x, w_gate_up):
+    if not hip_ok(x, w_gate_up):
         return silu_mul(F.linear(_dense(x), w_gate_up))
+    if not skinny_ok(x, w_gate_up):
+        x = _tiled_input(x)
     M, K = x.shape
     N2 = w_gate_up.shape[0]
     out = torch.empty(M, N2 // 2, device=x.device, dtype=x.dtype)
@@ -147,7 +166,7 @@ def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.T
     """(rms_norm(residual + x W^T), residual + x W^T) with the sum rounded to the dtype; norm_w None -> (None, sum).
     x [M, K], residual [M, N]. On the skinny route the first element is a NormedRows."""
     if not skinny_ok(x, w) or not residual.is_contiguous() or w.shape[0] % 8 != 0:
-        y = F.linear(x, w)
+        y = linear(x, w)
         if norm_w is None:
             return None, residual + y
         return rms_norm(y, norm_w, eps, residual=residual)
@@ -167,7 +186,7 @@ def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.T
 def linear_rope_qkv(x, w: torch.Tensor, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
                     n_heads: int, n_kv_heads: int, head_dim: int, k_cache=None, v_cache=None, slots=None):
     if not skinny_ok(x, w) or not (cos.is_contiguous() and sin.is_contiguous()) or head_dim not in (64, 128):
-        return rope_qkv(F.linear(_dense(x), w, b), cos, sin, n_heads, n_kv_heads, head_dim, k_cache, v_cache, slots)
+        return rope_qkv(linear(x, w, b), cos, sin, n_heads, n_kv_heads, head_dim, k_cache, v_cache, slots)
     M, K = x.shape
     N = w.shape[0]
     assert N == (n_heads + 2 * n_kv_heads) * head_dim and cos.shape == (M, head_dim) and sin.shape == (M, head_dim)
