@@ -1,4 +1,4 @@
-"""hipGraph capture of the decode step (torch.cuda.CUDAGraph records hipGraphs on ROCm).
+"""hipGraph capture of the decode step and of mixed steps (torch.cuda.CUDAGraph records hipGraphs on ROCm).
 
 Contract of nanoserve/cuda_graphs.py:42-126 (DecodeGraphRunner):
   * batch buckets 1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128; a batch of n replays the smallest bucket >= n;
@@ -16,9 +16,24 @@ is staged incrementally: block lists only grow between steps (truncation and rel
 row staged from the same list needs only its new tail. The next step can be staged while the current one
 runs (prestage / launch_prestaged), which the engine uses for steady greedy decode. Captures share one
 side stream; a runner's graphs share one memory pool.
+
+Mixed steps (prefill chunks + decode rows; the role of nanoserve/cuda_graphs.py:151-259, PiecewiseGraphRunner,
+in this build's own design): the whole step is one graph, attention included -- the chunked-prefill kernel
+reads the pages in place, so nothing has to run eagerly between pieces. A MixedStepGraph is keyed by a row
+bucket N (a multiple of 128, the tiled GEMM's row tile) and by the prefill-sequence capacity S (1, 2, 4, 8);
+it holds N + 1 rows, the last always padding. Its packed static inputs: token ids, positions and slots of
+every row; the prefill kernel's seq_info [S, 4] and tables [S, W]; the decode rows' indices, tables and
+context lengths [D] (D = the runner's decode capacity); and the rows whose logits are wanted (each
+sequence's last token). Unused prefill entries have no new tokens (their workgroups exit at once), unused
+decode entries attend over the garbage block from the padding row, and padding rows write their K/V into
+the garbage block. The greedy tokens go into pinned host memory inside the graph, as in the decode graph.
+A runner made with capture=False stages the same padded rows and runs the same forward without recording
+it, so an engine without graphs computes its mixed steps exactly as one with them (the kernels' tilings and
+K slices depend on the row count, so an unpadded step may round differently).
 """
 from __future__ import annotations
 
+import gc
 import math
 
 import torch
@@ -44,16 +59,25 @@ def capture(fn, pool):
     """Warm fn up twice on the side stream, then record it into a graph drawing on memory pool `pool`;
     returns (graph, fn's output). Capture always begins outside inference mode (fn may enter it): the
     graph-safe RNG state torch registers at the first capture is then an ordinary tensor, which later
-    captures and replays may update whether or not they run under inference mode."""
+    captures and replays may update whether or not they run under inference mode. Python's cyclic garbage
+    collector is run first and held off while recording: graphs are captured mid-run, and a collection
+    inside the capture would free earlier graphs' pinned buffers, which a stream capture does not allow."""
     side = _side_stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         fn()
         fn()
     torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.inference_mode(False), torch.cuda.graph(graph, pool=pool):
-        out = fn()
+    gc.collect()
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.inference_mode(False), torch.cuda.graph(graph, pool=pool):
+            out = fn()
+    finally:
+        if was_enabled:
+            gc.enable()
     return graph, out
 
 
@@ -216,5 +240,157 @@ class DecodeGraphRunner:
     def greedy_tokens(self, n: int) -> list[int]:
         """Argmax of the first n rows of the last replay (written into pinned memory inside the graph):
         waits for the replay, then reads the host buffer."""
+        torch.cuda.current_stream().synchronize()
+        return self.last.greedy[:n].tolist()
+
+
+MIXED_ROW_STEP = 128
+MIXED_SEQ_BUCKETS = (1, 2, 4, 8)
+
+
+class MixedStepGraph:
+    """One mixed-step bucket: N + 1 rows, S prefill entries, D decode entries (see the module docstring)."""
+
+    def __init__(self, runner: "MixedGraphRunner", N: int, S: int):
+        from nanoserve_amd.kernels.sampling import argmax_rows
+        self.N, self.S, self.D, self.W = N, S, runner.max_decode, runner.max_blocks
+        R, D, W = N + 1, self.D, self.W
+        self.garbage_block = runner.garbage_block
+        self.garbage_slot = runner.garbage_block * runner.block_size
+        # int64 section: tokens, positions, slots [R]; decode row index [D]; logit rows [S + D]
+        # int32 section: seq_info [S, 4]; decode context lengths [D]; prefill tables [S, W]; decode tables [D, W]
+        n64 = 3 * R + D + (S + D)
+        n32 = 4 * S + D + S * W + D * W
+        self.nbytes = 8 * n64 + 4 * n32
+        dev = runner.model.device
+        self.dev_buf = torch.zeros(self.nbytes, dtype=torch.uint8, device=dev)
+        self.twins = [torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        self.np = [self._views(t, numpy=True) for t in self.twins]
+        self.greedy = torch.empty(S + D, dtype=torch.int64, pin_memory=True)
+        self.par = 1
+        for v in self.np:
+            self._pad_all(v)
+        self.dev_buf.copy_(self.twins[0])
+        tok, pos, slots, dec_idx, rows, info, dec_lens, pf_tab, dec_tab = self._views(self.dev_buf)
+        meta = DecodeMeta(dec_idx, dec_tab, dec_lens)
+        # a sequence's new tokens fit both the rows and its table
+        prefill = ("chunks", pf_tab, info, min(N, W * runner.block_size), W * runner.block_size)
+        seqs = [SeqInput(R)]
+
+        def forward():
+            logits = runner.model.forward_batch(tok, pos, seqs, logits=rows, paged=runner.pool, slot_mapping=slots,
+                                                decode_meta=meta, prefill_meta=prefill)
+            argmax_rows(logits, self.greedy)
+            return logits
+
+        self.forward = forward
+        self.graph, self.logits = None, None
+        if runner.capture:
+            # warm-up and capture run on padding only: no new prefill tokens, decode entries on the garbage block
+            self.graph, self.logits = capture(forward, runner.mempool)
+
+    def _views(self, buf: torch.Tensor, numpy: bool = False):
+        R, S, D, W = self.N + 1, self.S, self.D, self.W
+        o, out = 0, []
+        for n in (R, R, R, D, S + D):
+            out.append(buf[o:o + 8 * n].view(torch.int64))
+            o += 8 * n
+        for shape in ((S, 4), (D,), (S, W), (D, W)):
+            n = 1
+            for d in shape:
+                n *= d
+            out.append(buf[o:o + 4 * n].view(torch.int32).view(*shape))
+            o += 4 * n
+        return tuple(x.numpy() for x in out) if numpy else tuple(out)
+
+    def _pad_all(self, v) -> None:
+        tok, pos, slots, dec_idx, rows, info, dec_lens, pf_tab, dec_tab = v
+        tok[:] = 0
+        pos[:] = 0
+        slots[:] = self.garbage_slot
+        dec_idx[:] = self.N
+        rows[:] = self.N
+        info[:] = 0
+        dec_lens[:] = 1
+        pf_tab[:] = 0
+        dec_tab[:] = 0
+        dec_tab[:, 0] = self.garbage_block
+
+    def stage(self, par: int, sb) -> None:
+        """Write StepBatch sb into pinned twin `par` (everything past its rows and entries is padding)."""
+        v = self.np[par]
+        self._pad_all(v)
+        tok, pos, slots, dec_idx, rows, info, dec_lens, pf_tab, dec_tab = v
+        n = len(sb.token_ids)
+        tok[:n] = sb.token_ids
+        pos[:n] = sb.positions
+        slots[:n] = sb.slots
+        start, j = 0, 0
+        for i, s in enumerate(sb.seqs):
+            T = s.n_tokens
+            rows[i] = start + T - 1
+            if not s.use_kernel:
+                t = sb.tables[i]
+                info[j] = (start, T, s.ctx_len, 0)
+                pf_tab[j, :len(t)] = t
+                j += 1
+            start += T
+        nd = len(sb.dec_idx)
+        dec_idx[:nd] = sb.dec_idx
+        dec_lens[:nd] = sb.dec_lens
+        for i, t in enumerate(sb.dec_tables):
+            dec_tab[i] = 0
+            dec_tab[i, :len(t)] = t
+
+    def launch(self, par: int) -> None:
+        self.par = par
+        self.dev_buf.copy_(self.twins[par], non_blocking=True)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.logits = self.forward()
+
+
+class MixedGraphRunner:
+    """Mixed-step graphs of one model and pool, captured on first use per (row bucket, prefill capacity);
+    with capture=False the same staged steps run without being recorded."""
+
+    def __init__(self, model: Qwen2Model, pool: PagedKVCache, max_seq_len: int, max_decode: int,
+                 max_rows: int, garbage_block: int, capture: bool = True):
+        self.model, self.pool = model, pool
+        self.capture = capture
+        self.block_size = pool.block_size
+        self.max_blocks = math.ceil(max_seq_len / pool.block_size)
+        self.max_decode = max_decode
+        self.max_rows = max_rows
+        self.garbage_block = garbage_block
+        self.graphs: dict[tuple[int, int], MixedStepGraph] = {}
+        self.mempool = torch.cuda.graph_pool_handle()
+        self.last: MixedStepGraph | None = None
+
+    @staticmethod
+    def bucket(n_rows: int) -> int:
+        return max(MIXED_ROW_STEP, -(-n_rows // MIXED_ROW_STEP) * MIXED_ROW_STEP)
+
+    def fits(self, sb) -> bool:
+        n_pf = len(sb.seqs) - len(sb.dec_idx)
+        return (self.model.dtype == torch.bfloat16 and 0 < n_pf <= MIXED_SEQ_BUCKETS[-1]
+                and len(sb.token_ids) <= self.max_rows and len(sb.dec_idx) <= self.max_decode
+                and all(len(t) <= self.max_blocks for t in sb.tables))
+
+    def run(self, sb) -> torch.Tensor:
+        n_pf = len(sb.seqs) - len(sb.dec_idx)
+        key = (self.bucket(len(sb.token_ids)), next(s for s in MIXED_SEQ_BUCKETS if s >= n_pf))
+        g = self.graphs.get(key)
+        if g is None:
+            g = self.graphs[key] = MixedStepGraph(self, *key)
+        par = g.par ^ 1
+        torch.cuda.current_stream().synchronize()   # the twin about to be rewritten may still be copying
+        g.stage(par, sb)
+        g.launch(par)
+        self.last = g
+        return g.logits[:len(sb.seqs)]
+
+    def greedy_tokens(self, n: int) -> list[int]:
         torch.cuda.current_stream().synchronize()
         return self.last.greedy[:n].tolist()

@@ -362,16 +362,18 @@ class Qwen2Model:
     @torch.inference_mode()
     def forward_batch(self, token_ids: torch.Tensor, positions: torch.Tensor, seqs: list[SeqInput],
                       logits="last", paged=None, slot_mapping: torch.Tensor | None = None,
-                      decode_meta: DecodeMeta | None = None) -> torch.Tensor:
+                      decode_meta: DecodeMeta | None = None, prefill_meta: tuple | None = None) -> torch.Tensor:
         """One forward pass over several sequences (prefilling, continuing a chunked prefill on a cached
         context, or decoding one token). token_ids/positions: [N] in `seqs` order. Returns logits
         [len(seqs), vocab] for each sequence's last token ("last"), [N, vocab] ("all"), or the rows of an
-        index tensor."""
+        index tensor. prefill_meta: the chunked-prefill kernel's inputs already on the device, ("chunks",
+        tables int32 [S, W], seq_info int32 [S, 4], max_new, max_kv) -- the non-decode rows are then described
+        by them alone (a captured mixed step), and `seqs` only has to cover the rows."""
         self._require_gpu()
         if paged is None:
             raise ValueError("the HIP path needs the paged KV cache (`paged` + `slot_mapping`)")
         assert sum(s.n_tokens for s in seqs) == token_ids.shape[0], "seqs must cover token_ids exactly"
-        self._rows_cache = None
+        self._rows_cache = None if prefill_meta is None else (seqs, slot_mapping, prefill_meta)
         from nanoserve_amd.kernels.fused import embed_rope, rms_norm
         from nanoserve_amd.kernels.linear import SKINNY_MAX_M, NormedRows
         L, eps = self.cfg.n_layers, self.cfg.rms_norm_eps

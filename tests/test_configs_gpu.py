@@ -140,7 +140,7 @@ def test_config3_streams_identical_with_overlap_on_off_and_eager(hiplib, model_1
         print(f"  steps {st['steps']}, graph steps {st['graph_steps']}", flush=True)
         if label != "eager":
             assert st["graph_steps"] >= 127
-        assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - (1 if kw.get("cuda_graphs", True) else 0)
+        assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - eng.executor.reserved_blocks
         del eng
         torch.cuda.empty_cache()
     assert all(len(s) == 128 for s in streams["overlap"])
