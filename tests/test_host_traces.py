@@ -151,3 +151,43 @@ def test_traces_cover_the_behaviours_they_pin():
     assert any(r["evictable"] for r in by["prefix_eviction"]["records"])
     eos = [o for r in by["eos_and_abort"]["records"] for o in r["out"] if o[2] and o[1] == STUB_EOS]
     assert eos
+
+
+def _fails(scenarios) -> list[str]:
+    bad = []
+    for scn in scenarios:
+        try:
+            test_engine_host_state_matches_the_reference_trace(scn)
+        except (AssertionError, IndexError, ValueError):   # a diverging run may also break an invariant
+            bad.append(scn["name"])
+    return bad
+
+
+def test_planted_host_mistakes_fail_the_traces(monkeypatch):
+    """Plausible slips in the host integer logic break at least one reference trace: freeing a request's
+    blocks head first with prefix caching (the LRU order of cached blocks), and preempting the oldest running
+    request instead of the newest. (The prefix-hit cap of (len - 1) // 16 blocks matters only for a fully
+    cached prompt of whole blocks, which no trace holds; tests/test_host_logic.py pins it by known answer.)"""
+    from nanoserve_amd import kv_cache, scheduler
+    assert _fails(TRACES["scenarios"]) == []
+
+    orig_free = kv_cache.BlockPool.free
+
+    def free_head_first(self, blocks):
+        pc, self.prefix_caching = self.prefix_caching, False
+        try:
+            orig_free(self, blocks)
+        finally:
+            self.prefix_caching = pc
+
+    orig_evict = scheduler.Scheduler._evict_newest
+
+    def evict_oldest(self):
+        self.running.append(self.running.pop(0))
+        return orig_evict(self)
+
+    for name, (owner, attr, fn) in {"free order": (kv_cache.BlockPool, "free", free_head_first),
+                                    "preemption order": (scheduler.Scheduler, "_evict_newest", evict_oldest)}.items():
+        with monkeypatch.context() as m:
+            m.setattr(owner, attr, fn)
+            assert _fails(TRACES["scenarios"]), f"planted mistake '{name}' passes every trace"
