@@ -349,7 +349,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
 //     context length only, never on the table width; a row with several merges as the per-head kernel does: 16-byte
 //     coherent (sc1) stores of (m, l, acc), a wait for them, the row's counter, and the last partition
 //     to arrive loads MB partitions per round trip and folds them in partition order.
-constexpr int ROWK_NW = 4, ROWK_PPW = 8, ROWK_D = 2, ROWK_PART = ROWK_NW * ROWK_PPW;
+constexpr int ROWK_NW = 8, ROWK_PPW = 4, ROWK_D = 2, ROWK_PART = ROWK_NW * ROWK_PPW;
 constexpr int ROWK_MB = 8;
 constexpr int ROWK_MAX_PARTS = 32;
 typedef __attribute__((ext_vector_type(4))) unsigned int rk_u32x4_t;
@@ -515,15 +515,29 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   };
   using Z0 = std::integral_constant<int, 0>;
   using Z1 = std::integral_constant<int, 1>;
-  static_assert(D == 2 && PPW % 2 == 0, "the page loop is unrolled for two slots");
-  issue(0, Z0{});
-  issue(1, Z1{});
+  using Z2 = std::integral_constant<int, 2>;
+  using Z3 = std::integral_constant<int, 3>;
+  if constexpr (D == 4) {   // every page of the wave in flight at once
+    static_assert(PPW == 4, "four slots hold the wave's four pages");
+    issue(0, Z0{});
+    issue(1, Z1{});
+    issue(2, Z2{});
+    issue(3, Z3{});
+    if (0 < n_live) page(0, Z0{});   // wave-uniform
+    if (1 < n_live) page(1, Z1{});
+    if (2 < n_live) page(2, Z2{});
+    if (3 < n_live) page(3, Z3{});
+  } else {
+    static_assert(D == 2 && PPW % 2 == 0, "the page loop is unrolled for two slots");
+    issue(0, Z0{});
+    issue(1, Z1{});
 #pragma unroll
-  for (int i0 = 0; i0 < PPW; i0 += 2) {
-    if (i0 < n_live) page(i0, Z0{});       // wave-uniform
-    if (i0 + 2 < PPW) issue(i0 + 2, Z0{});
-    if (i0 + 1 < n_live) page(i0 + 1, Z1{});
-    if (i0 + 3 < PPW) issue(i0 + 3, Z1{});
+    for (int i0 = 0; i0 < PPW; i0 += 2) {
+      if (i0 < n_live) page(i0, Z0{});       // wave-uniform
+      if (i0 + 2 < PPW) issue(i0 + 2, Z0{});
+      if (i0 + 1 < n_live) page(i0 + 1, Z1{});
+      if (i0 + 3 < PPW) issue(i0 + 3, Z1{});
+    }
   }
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
