@@ -656,6 +656,8 @@ def main() -> int:
     ap.add_argument("--no-prefix-sharing", action="store_true", help="skip the config-5 prefix-sharing decode run")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the paged-attention roofline and the copy calibration (for rocprofv3 --pmc passes)")
+    ap.add_argument("--mixed-only", action="store_true",
+                    help="only the config-4 mixed step, graphed and eager (for rocprofv3 kernel traces)")
     ap.add_argument("--ops-only", action="store_true",
                     help="only the fused token-wise ops, the chunked-prefill kernel alone and the copy calibration "
                          "(for rocprofv3 --pmc passes)")
@@ -685,6 +687,11 @@ def main() -> int:
     log("generating random-init 1.5B weights (CPU, fp32, seeded)")
     sd_cpu = random_state_dict(cfg, seed=0, dtype=torch.float32)
     model = Qwen2Model(cfg, {n: t.to("cuda", torch.bfloat16) for n, t in sd_cpu.items()})
+    if args.mixed_only:
+        mixed = mixed_step_bench(model, cfg)
+        log(f"mixed step: {mixed['ms_per_step']} ms graphed, {mixed['eager_ms_per_step']} ms eager")
+        print(json.dumps({"mixed_step": mixed}), flush=True)
+        return 0
     g = torch.Generator().manual_seed(1)
     prompts = [torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist() for _ in range(B)]
     run = decode_run(model, prompts, K, W)
