@@ -1005,43 +1005,61 @@ __global__ __launch_bounds__(64) void rms_norm_apply_kernel(const bf16_t* __rest
 
 // ------------------------------------------------------------------------------------- tiled GEMM (M > 64)
 // Prefill chunks, mixed steps and speculative verify batches: Y[M, N] = X[M, K] . W[N, K]^T for any M, bf16
-// in, fp32 accumulate, with the STORE (+ bias) and SILU epilogues of the skinny kernels (same rounding).
-//   * BM x BN output tiles (SILU: BN/2 gate rows + the matching BN/2 up rows of W -> BN/2 output columns),
-//     2 x WN waves, each BM/2 x 64 (WM x 4 mfma_f32_16x16x32_bf16 tiles). Two shapes: 256 x 256 (8 waves,
-//     one workgroup per CU) and 128 x 128 (4 waves, three per CU); the larger tile moves half the L2 -> LDS
-//     bytes per flop, so the plan takes it whenever it alone fills the GPU.
+// in, fp32 accumulate, with the STORE (+ bias) and SILU epilogues of the skinny kernels.
+//   * BM x BN output tiles, NW waves in a 2 x (NW / 2) grid, each a (16 FM) x (16 FN) block of
+//     mfma_f32_16x16x32_bf16 tiles. Shapes: 256 x 256 (8 waves of 128 x 64, one workgroup per CU) and
+//     128 x 128 (4 waves of 64 x 64, two per CU). A CU's vector memory path moves about 64 bytes per clock
+//     (L2-resident loads into LDS or VGPRs alike); a 256 x 256 tile asks 7.8 bytes per kFLOP of it, half of
+//     what the MFMA rate allows, a 128 x 128 tile 15.6 -- all of it -- so the plan takes the larger tile
+//     whenever it alone fills the GPU.
+//   * SILU: each wave's FN W-row tiles are FN / 2 gate tiles and the FN / 2 matching up tiles, so a lane
+//     holds gate and up of the same outputs and finishes them in registers.
 //   * K in 32-wide steps through a ring of S LDS stages (BM x 64 bytes of X rows + BN x 64 bytes of W rows
-//     each; four stages at one workgroup per CU, three at three), filled by buffer DMA (16 bytes per lane, each instruction 16 rows x 64 bytes; rows past M
-//     or N and empty trailing stages read zeros through the buffer bounds, with no memory access). Each
+//     each), filled by buffer DMA (16 bytes per lane, each instruction 16 rows x 64 bytes; rows past M or N
+//     and the empty stages past the slice read zeros through the buffer bounds, with no memory access). Each
 //     64-byte row keeps its four 16-byte chunks XOR-swizzled by (row / 2) & 3, so the 16-lane fragment reads
-//     are free of bank conflicts. One barrier per step: a wave waits for its own DMA of the step (vmcnt), the
-//     barrier makes every wave's part visible and retires the stage read one step earlier, which is
-//     refilled next. Fragment reads are inline asm, so the compiler does not drain the DMA ring before them.
+//     are free of bank conflicts.
+//   * Software pipeline, one barrier per step: step q waits for the wave's own DMA of stage q + 1 (vmcnt)
+//     and meets the other waves at the barrier (which also retires the fragment reads of step q, freeing
+//     stage q's slot), then issues the MFMAs of step q row by row with, between them, the DMA of stage
+//     q + S into the freed slot and the fragment reads of step q + 1: A fragment i right after row i is
+//     issued (an MFMA reads its sources at issue), the W fragments into the second of two sets. Fragment
+//     reads are inline asm, so the compiler does not drain the DMA ring before them; the barrier's
+//     lgkmcnt(0) is their wait.
+//   * Workgroups map XCD-contiguously: XCD x runs a contiguous run of tiles (same W rows, successive X
+//     rows), which share its L2.
 //   * Few tiles, or long K with fewer tiles than CUs: K is cut into `splits` slices; each publishes its fp32
 //     tile to the workspace (agent-scope stores, a per-tile arrival counter in the fixed counter region) and
 //     the last to arrive sums the slices in slice order -- deterministic -- and runs the epilogue.
-//   * Epilogue: the tile goes through LDS as fp32 in passes of [64][132] and 256 threads finish it in
-//     row-contiguous 16-byte pieces.
+//   * Epilogues: STORE passes the fp32 tile through LDS in 64-row passes; SILU stages only the bf16 outputs
+//     (one pass). All threads then write row-contiguous 16-byte pieces. Roundings to bf16 use the hardware
+//     conversion (round to nearest even); the SiLU is g * rcp(1 + exp2(-g log2 e)) on the transcendental
+//     unit (within 2 ulp of fp32 division before the bf16 rounding).
 constexpr int TG_BK = 32;
-constexpr int TG_CROWS = 64;                  // output rows per epilogue pass
-constexpr int TG_MAX_SPLITS = 16;
+constexpr int TG_CROWS = 64;                  // output rows per STORE epilogue pass
+constexpr int TG_MAX_SPLITS = 16;            // K slices at most (forced plans included)
+constexpr int TG_PLAN_SPLITS = 6;             // K slices the plan chooses at most
 constexpr int TG_RSRC3 = 0x00020000;          // buffer resource word 3: raw (untyped) 32-bit accesses
 
-template <int WN, int WM>
+template <int FM, int FN, int NW_>
 struct TgShape {
-  static constexpr int NW = 2 * WN;                         // waves
-  static constexpr int NT = 64 * NW;                        // threads
-  static constexpr int BM = 32 * WM;                        // X rows of a tile
-  static constexpr int BN = 64 * WN;                        // W rows of a tile
-  static constexpr int S = NW == 8 ? 4 : 3;                 // ring stages (one workgroup per CU: four)
-  static constexpr int AROWS = BM * TG_BK * 2;              // bytes of the X rows of a stage
+  static constexpr int NW = NW_, NT = 64 * NW, WNW = NW / 2;   // waves, threads, waves along N
+  static constexpr int BM = 32 * FM, BN = 16 * FN * WNW;      // X rows, W rows of a tile
+  static constexpr int WG_PER_CU = NW == 8 ? 1 : 2;
+  static constexpr int S = 4;                                 // ring stages
+  static constexpr int AROWS = BM * TG_BK * 2;                // bytes of the X rows of a stage
   static constexpr int STAGE = AROWS + BN * TG_BK * 2;
-  static constexpr int CP = BN + 4;                         // floats per row of the staged output tile
-  static constexpr int LDS = S * STAGE > TG_CROWS * CP * 4 ? S * STAGE : TG_CROWS * CP * 4;
-  static constexpr int WG_PER_CU = NW == 8 ? 1 : 3;
-  static constexpr int PART = BM * BN;                      // floats of one published slice of a tile
+  static constexpr int CP = BN + 4;                           // floats per row of the staged STORE tile
+  static constexpr int OCP = BN / 2 + 8;                      // bf16 per row of the staged SILU tile
+  static constexpr int CBYTES = TG_CROWS * CP * 4 > BM * OCP * 2 ? TG_CROWS * CP * 4 : BM * OCP * 2;
+  static constexpr int LDS = S * STAGE > CBYTES ? S * STAGE : CBYTES;
+  static constexpr int PART = BM * BN;                        // floats of one published slice of a tile
   static constexpr int AJ = BM / (16 * NW), BJ = BN / (16 * NW);   // DMA instructions per wave per stage
   static constexpr int DMA = AJ + BJ;
+  static constexpr int MF = FM * FN;                          // MFMAs per wave per step
+  static_assert(FM % 4 == 0 && FN % 4 == 0 && AJ >= 1 && BJ >= 1 && DMA <= MF && MF % 16 == 0 &&
+                    WG_PER_CU * LDS <= 160 * 1024,
+                "tile shape");
 };
 
 struct TgArgs {
@@ -1061,15 +1079,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tg_rsrc(const void* p, uint32_
 __device__ __forceinline__ uint32_t tg_lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
-// four 16-byte fragment reads, one wait (early-clobber: a read's data may land before a later read issues)
-__device__ __forceinline__ void tg_read4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, g_u32x4_t& v0,
-                                         g_u32x4_t& v1, g_u32x4_t& v2, g_u32x4_t& v3) {
-  asm volatile(
-      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
-      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
-      : "memory");
+// One 16-byte fragment read, no wait: the data is used only after the next barrier, whose lgkmcnt(0)
+// covers it.
+__device__ __forceinline__ void tg_read(uint32_t addr, g_u32x4_t& v) {
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
 }
 // Workgroup barrier for LDS data (no wait for the wave's outstanding DMA, unlike __syncthreads)
 __device__ __forceinline__ void tg_barrier() {
@@ -1080,19 +1093,36 @@ __device__ __forceinline__ void tg_barrier() {
 }
 // waitcnt immediate: at most n vector memory operations of this wave still outstanding
 constexpr int tg_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+// Workgroup i of a grid of n -> position in the XCD-contiguous order (a bijection on [0, n)): XCD i % 8
+// takes runs of n / 8 positions, the first n % 8 XCDs one more.
+__host__ __device__ __forceinline__ int tg_xcd_order(int i, int n) {
+  const int x = i & 7, j = i >> 3, q = n >> 3, r = n & 7;
+  return x * q + (x < r ? x : r) + j;
+}
+// fp32 rounded to bf16 (nearest even, hardware conversion), kept in fp32
+__device__ __forceinline__ float tg_round(float f) { return __uint_as_float(pack_bf16x2(f, 0.f) << 16); }
+// W row staged at row r of a tile's W rows. STORE: BN tn + r. SILU: tile tn covers output columns
+// (BN / 2) tn + [0, BN / 2); wave block c = r / (16 FN) stages its FN / 2 gate tiles, then the matching up tiles.
+template <int EPI, int FN, int BN>
+__device__ __forceinline__ int tg_wrow(int r, int tn, int half) {
+  if constexpr (EPI == EPI_SILU) {
+    const int c = r / (16 * FN), jj = (r / 16) % FN, rr = r % 16;
+    const int oc = (BN / 2) * tn + 8 * FN * c + 16 * (jj % (FN / 2)) + rr;
+    return jj < FN / 2 ? oc : half + oc;
+  } else {
+    return BN * tn + r;
+  }
+}
 
-template <int EPI, int WN, int WM>
-__global__ __launch_bounds__((TgShape<WN, WM>::NT), (TgShape<WN, WM>::WG_PER_CU)) void tiled_gemm_kernel(TgArgs a) {
-  using SH = TgShape<WN, WM>;
-  constexpr int BM = SH::BM, BN = SH::BN, NT = SH::NT, CP = SH::CP;
+template <int EPI, int FM, int FN, int NW>
+__global__ __launch_bounds__((TgShape<FM, FN, NW>::NT), (TgShape<FM, FN, NW>::WG_PER_CU)) void tiled_gemm_kernel(TgArgs a) {
+  using SH = TgShape<FM, FN, NW>;
+  constexpr int BM = SH::BM, BN = SH::BN, NT = SH::NT, S = SH::S;
   __shared__ __align__(16) unsigned char lds[SH::LDS];
   __shared__ unsigned s_last;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int tiles = a.tiles_m * a.tiles_n, grid = tiles * a.splits;
-  // XCD-aware order: workgroup i runs on XCD i % 8, so consecutive tiles (same W rows, successive X rows)
-  // go to one XCD and share its L2
-  int bid = blockIdx.x;
-  if (grid % 8 == 0) bid = (bid & 7) * (grid >> 3) + (bid >> 3);
+  const int bid = tg_xcd_order(int(blockIdx.x), grid);
   const int split = bid / tiles, t = bid - split * tiles;
   const int tm = t % a.tiles_m, tn = t / a.tiles_m;
   const int m0 = tm * BM;
@@ -1112,66 +1142,74 @@ __global__ __launch_bounds__((TgShape<WN, WM>::NT), (TgShape<WN, WM>::WG_PER_CU)
 #pragma unroll
   for (int j = 0; j < BJ; ++j) {
     const int r = 16 * (BJ * w + j) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
-    const int wrow = EPI == EPI_SILU ? (r < BN / 2 ? (BN / 2) * tn + r : half + (BN / 2) * tn + r - BN / 2) : BN * tn + r;
-    vob[j] = (uint32_t(wrow) * uint32_t(K) + uint32_t(8 * c)) * 2u;
+    vob[j] = (uint32_t(tg_wrow<EPI, FN, BN>(r, tn, half)) * uint32_t(K) + uint32_t(8 * c)) * 2u;
   }
   const __amdgpu_buffer_rsrc_t xr = tg_rsrc(a.x, uint32_t(M) * uint32_t(K) * 2u), xnone = tg_rsrc(a.x, 0u);
   const __amdgpu_buffer_rsrc_t wr = tg_rsrc(a.w, uint32_t(N) * uint32_t(K) * 2u), wnone = tg_rsrc(a.w, 0u);
-  auto issue = [&](int q) __attribute__((always_inline)) {   // stage q of the slice (past nk: zeros, no traffic)
+  // DMA instruction d (X rows for d < AJ, then W rows) of stage q of the slice (past nk: zeros, no traffic)
+  auto dma = [&](int q, int d) __attribute__((always_inline)) {
     const bool live = q < nk;
-    const __amdgpu_buffer_rsrc_t xs = live ? xr : xnone, wsr = live ? wr : wnone;
-    const int soff = live ? (kb + q) * TG_BK * 2 : 0;
-    unsigned char* st = lds + (q % SH::S) * SH::STAGE;
-#pragma unroll
-    for (int j = 0; j < AJ; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (__attribute__((address_space(3))) void*)(st + 16 * (AJ * w + j) * 64),
-                                               16, int(voa[j]), soff, 0, 0);
-#pragma unroll
-    for (int j = 0; j < BJ; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (__attribute__((address_space(3))) void*)(st + SH::AROWS + 16 * (BJ * w + j) * 64),
-                                               16, int(vob[j]), soff, 0, 0);
+    const int soff = __builtin_amdgcn_readfirstlane(live ? (kb + q) * TG_BK * 2 : 0);   // uniform: an SGPR
+    unsigned char* st = lds + (q % S) * SH::STAGE;
+    if (d < AJ)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? xr : xnone,
+                                               (__attribute__((address_space(3))) void*)(st + 16 * (AJ * w + d) * 64),
+                                               16, int(voa[d]), soff, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          live ? wr : wnone, (__attribute__((address_space(3))) void*)(st + SH::AROWS + 16 * (BJ * w + d - AJ) * 64), 16,
+          int(vob[d - AJ]), soff, 0, 0);
   };
-#pragma unroll
-  for (int q = 0; q < SH::S - 1; ++q) issue(q);
 
-  // fragment offsets within a stage: lane -> row l % 16 of the 16-row tile, 16-byte chunk l / 16
+  // fragment offsets within a stage: lane -> row l % 16 of the 16-row tile, 16-byte chunk l / 16; the swizzle
+  // of rows 16 i + l % 16 does not depend on i, so fragment i sits 1024 i bytes further
   const int wm = w & 1, wn = w >> 1;
-  uint32_t fa[WM], fb[4];
+  const int ra = 16 * FM * wm + (l & 15), rb = 16 * FN * wn + (l & 15);
+  const uint32_t foa = uint32_t(ra * 64 + 16 * ((l >> 4) ^ ((ra >> 1) & 3)));
+  const uint32_t fob = uint32_t(SH::AROWS + rb * 64 + 16 * ((l >> 4) ^ ((rb >> 1) & 3)));
+  g_float4_t acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < WM; ++i) {
-    const int ra = (BM / 2) * wm + 16 * i + (l & 15);
-    fa[i] = uint32_t(ra * 64 + 16 * ((l >> 4) ^ ((ra >> 1) & 3)));
-  }
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int rb = 64 * wn + 16 * i + (l & 15);
-    fb[i] = uint32_t(SH::AROWS + rb * 64 + 16 * ((l >> 4) ^ ((rb >> 1) & 3)));
-  }
-  g_float4_t acc[WM][4];
-#pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
   const uint32_t lds0 = tg_lds_addr(lds);
-  for (int q = 0; q < nk; ++q) {
-    __builtin_amdgcn_s_waitcnt(tg_vmcnt(SH::DMA * (SH::S - 2)));   // this wave's loads of stage q are done
-    tg_barrier();                                                 // ... and every wave's; stage q - 1 is free
-    issue(q + SH::S - 1);
-    const uint32_t sb = lds0 + uint32_t((q % SH::S) * SH::STAGE);
-    g_u32x4_t bf[4];
-    tg_read4(sb + fb[0], sb + fb[1], sb + fb[2], sb + fb[3], bf[0], bf[1], bf[2], bf[3]);
+
+  // Step q: the MFMAs of step q, row by row, from A and Bc; between them the DMA of stage q + S, and the
+  // reads of step q + 1: A[i] as soon as row i is issued, Bn spread over the step.
+  g_u32x4_t A[FM], B0[FN], B1[FN];
+  auto step = [&](int q, g_u32x4_t (&Bc)[FN], g_u32x4_t (&Bn)[FN]) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(tg_vmcnt(SH::DMA * (S - 2)));   // this wave's loads of stage q + 1 are done
+    tg_barrier();   // ... and every wave's; every read of step q has landed, so stage q's slot is free
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t sn = lds0 + uint32_t(((q + 1) % S) * SH::STAGE);
+    constexpr int EVERY = SH::MF / FN;
 #pragma unroll
-    for (int i0 = 0; i0 < WM; i0 += 4) {
-      g_u32x4_t af[4];
-      tg_read4(sb + fa[i0], sb + fa[i0 + 1], sb + fa[i0 + 2], sb + fa[i0 + 3], af[0], af[1], af[2], af[3]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i0 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, af[i]),
-                                                                   __builtin_bit_cast(g_bf16x8_t, bf[j]),
-                                                                   acc[i0 + i][j], 0, 0, 0);
+    for (int u = 0; u < SH::MF; ++u) {
+      const int i = u / FN, j = u % FN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, A[i]),
+                                                         __builtin_bit_cast(g_bf16x8_t, Bc[j]), acc[i][j], 0, 0, 0);
+      if (u < SH::DMA) dma(q + S, u);
+      if (j == FN - 1) tg_read(sn + foa + 1024u * i, A[i]);
+      if (u % EVERY == EVERY / 2) tg_read(sn + fob + 1024u * (u / EVERY), Bn[u / EVERY]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+
+#pragma unroll
+  for (int q = 0; q < S; ++q)
+#pragma unroll
+    for (int d = 0; d < SH::DMA; ++d) dma(q, d);
+  __builtin_amdgcn_s_waitcnt(tg_vmcnt(SH::DMA * (S - 1)));   // stage 0
+  tg_barrier();
+#pragma unroll
+  for (int i = 0; i < FM; ++i) tg_read(lds0 + foa + 1024u * i, A[i]);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) tg_read(lds0 + fob + 1024u * j, B0[j]);
+  for (int q = 0;; q += 2) {
+    step(q, B0, B1);
+    if (q + 1 >= nk) break;
+    step(q + 1, B1, B0);
+    if (q + 2 >= nk) break;
   }
   __builtin_amdgcn_s_waitcnt(tg_vmcnt(0));
   tg_barrier();
@@ -1180,11 +1218,11 @@ __global__ __launch_bounds__((TgShape<WN, WM>::NT), (TgShape<WN, WM>::WG_PER_CU)
   if (a.splits > 1) {
     float* mine = a.part + (int64_t(t) * a.splits + split) * SH::PART;
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < FN; ++j) {
         const g_float4_t v = acc[i][j];
-        publish_store16(mine + (int64_t(i * 4 + j) * NT + tid) * 4,
+        publish_store16(mine + (int64_t(i * FN + j) * NT + tid) * 4,
                         pub_u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
                                     __float_as_uint(v[3])});
       }
@@ -1200,45 +1238,44 @@ __global__ __launch_bounds__((TgShape<WN, WM>::NT), (TgShape<WN, WM>::WG_PER_CU)
     if (s_last == 0u) return;
     acquire_published();
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < FN; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
     const float* base = a.part + int64_t(t) * a.splits * SH::PART;
     for (int s = 0; s < a.splits; ++s) {
 #pragma unroll
-      for (int i0 = 0; i0 < WM; i0 += 4) {
+      for (int f0 = 0; f0 < SH::MF; f0 += 16) {
         pub_u32x4_t v[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          v[e] = publish_load16(base + int64_t(s) * SH::PART + (int64_t(i0 * 4 + e) * NT + tid) * 4);
+          v[e] = publish_load16(base + int64_t(s) * SH::PART + (int64_t(f0 + e) * NT + tid) * 4);
 #pragma unroll
         for (int e = 0; e < 16; ++e)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i0 + (e >> 2)][e & 3][r] += __uint_as_float(v[e][r]);
+          for (int r = 0; r < 4; ++r) acc[(f0 + e) / FN][(f0 + e) % FN][r] += __uint_as_float(v[e][r]);
       }
     }
   }
 
-  // ---- the tile through LDS in passes of 64 rows (pass p: the waves with wm == p / (WM / 4), their m-tiles
-  // 4 (p % (WM / 4)) .. + 3): C[m][n] (lane: column l % 16, rows 4 (l / 16) + r of each 16 x 16 tile)
-  float* C = reinterpret_cast<float*>(lds);
-  constexpr int PASSES = BM / TG_CROWS, PW = WM / 4;
+  // Lane layout of acc[i][j]: column 16 FN wn + 16 j + l % 16 of the tile, rows 16 FM wm + 16 i + 4 (l / 16) + r.
+  if constexpr (EPI == EPI_STORE) {
+    // the fp32 tile through LDS in passes of 64 rows (pass p: the waves with wm == p / (FM / 4), their
+    // m-tiles 4 (p % (FM / 4)) .. + 3), then items (row m, 8 columns) of 16 bytes
+    float* C = reinterpret_cast<float*>(lds);
+    constexpr int CP = SH::CP, PASSES = BM / TG_CROWS, PW = FM / 4, IPR = BN / 8;
 #pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    if (wm == p / PW) {
+    for (int p = 0; p < PASSES; ++p) {
+      if (wm == p / PW) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            C[(16 * i + 4 * (l >> 4) + r) * CP + 64 * wn + 16 * j + (l & 15)] = acc[4 * (p % PW) + i][j][r];
-    }
-    __syncthreads();
-    const int mb = m0 + TG_CROWS * p;
-    if constexpr (EPI == EPI_STORE) {
-      // items (row m, 8 columns): 64 x BN / 8
-      constexpr int IPR = BN / 8;
+            for (int r = 0; r < 4; ++r)
+              C[(16 * i + 4 * (l >> 4) + r) * CP + 16 * FN * wn + 16 * j + (l & 15)] = acc[4 * (p % PW) + i][j][r];
+      }
+      tg_barrier();   // LDS only: the global stores of the previous pass need not land first
+      const int mb = m0 + TG_CROWS * p;
 #pragma unroll 2
       for (int it = tid; it < TG_CROWS * IPR; it += NT) {
         const int m = it / IPR, c8 = it % IPR, gm = mb + m, gn = BN * tn + 8 * c8;
@@ -1247,8 +1284,15 @@ __global__ __launch_bounds__((TgShape<WN, WM>::NT), (TgShape<WN, WM>::WG_PER_CU)
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = C[m * CP + 8 * c8 + e];
         if (a.bias != nullptr) {
+          if ((N & 7) == 0) {
+            float b[8];
+            load_bf16x8(a.bias + gn, b);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] += gn + e < N ? bf16_to_f32(a.bias[gn + e]) : 0.f;
+            for (int e = 0; e < 8; ++e) v[e] += b[e];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] += gn + e < N ? bf16_to_f32(a.bias[gn + e]) : 0.f;
+          }
         }
         bf16_t* dst = a.y + int64_t(gm) * N + gn;
         if ((N & 7) == 0) {
@@ -1259,29 +1303,39 @@ __global__ __launch_bounds__((TgShape<WN, WM>::NT), (TgShape<WN, WM>::WG_PER_CU)
             if (gn + e < N) dst[e] = f32_to_bf16(v[e]);
         }
       }
-    } else {   // EPI_SILU: columns [0, BN/2) gate, [BN/2, BN) up; items (row m, 8 output columns): 64 x BN / 16
-      constexpr int IPR = BN / 16;
+      if (p + 1 < PASSES) tg_barrier();
+    }
+  } else {
+    // SILU: gate acc[i][j], up acc[i][j + FN / 2] -> output column 8 FN wn + 16 j + l % 16 of the tile's
+    // BN / 2; the bf16 outputs go through LDS ([BM][OCP]) in one pass, then items (row m, 8 columns)
+    bf16_t* O = reinterpret_cast<bf16_t*>(lds);
+    constexpr int OCP = SH::OCP, IPR = BN / 16;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN / 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gb = tg_round(acc[i][j][r]), ub = tg_round(acc[i][j + FN / 2][r]);
+          const float sg = gb * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb * -1.44269504088896341f));
+          O[(16 * FM * wm + 16 * i + 4 * (l >> 4) + r) * OCP + 8 * FN * wn + 16 * j + (l & 15)] =
+              bf16_t(pack_bf16x2(tg_round(sg) * ub, 0.f));
+        }
+    tg_barrier();
 #pragma unroll 2
-      for (int it = tid; it < TG_CROWS * IPR; it += NT) {
-        const int m = it / IPR, c8 = it % IPR, gm = mb + m, gn = (BN / 2) * tn + 8 * c8;
-        if (gm >= M || gn >= half) continue;
-        float out[8];
+    for (int it = tid; it < BM * IPR; it += NT) {
+      const int m = it / IPR, c8 = it % IPR, gm = m0 + m, gn = (BN / 2) * tn + 8 * c8;
+      if (gm >= M || gn >= half) continue;
+      const g_u32x4_t v = *reinterpret_cast<const g_u32x4_t*>(O + m * OCP + 8 * c8);
+      bf16_t* dst = a.y + int64_t(gm) * half + gn;
+      if ((half & 7) == 0) {
+        *reinterpret_cast<g_u32x4_t*>(dst) = v;
+      } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float gb = round_bf16(C[m * CP + 8 * c8 + e]), ub = round_bf16(C[m * CP + BN / 2 + 8 * c8 + e]);
-          out[e] = round_bf16(gb / (1.0f + expf(-gb))) * ub;
-        }
-        bf16_t* dst = a.y + int64_t(gm) * half + gn;
-        if ((half & 7) == 0) {
-          store_bf16x8(dst, out);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (gn + e < half) dst[e] = f32_to_bf16(out[e]);
-        }
+        for (int e = 0; e < 8; ++e)
+          if (gn + e < half) dst[e] = bf16_t(v[e >> 1] >> (16 * (e & 1)));
       }
     }
-    if (p + 1 < PASSES) __syncthreads();
   }
 }
 
@@ -1475,39 +1529,61 @@ static int bind_xnorm(GemmArgs& a, const float* x_sumsq, const void* x_norm_w, f
 
 // ---- tiled GEMM plan and launch (M > 64)
 struct TgPlan {
-  int wn, wm;   // tile 32 wm x 64 wn: (4, 8) 256 x 256, (2, 4) 128 x 128
+  int big;   // 256 x 256 tiles (8 waves), else 128 x 128 (4 waves)
   int tiles_m, tiles_n, splits, kps;
   size_t bytes;   // workspace (0: no K slices)
 };
+using TgBig = TgShape<8, 4, 8>;
+using TgSmall = TgShape<4, 4, 4>;
 static void tg_tiles(TgPlan& p, int M, int N, bool silu) {
-  const int bm = 32 * p.wm, bn = 64 * p.wn;
+  const int bm = p.big ? TgBig::BM : TgSmall::BM, bn = p.big ? TgBig::BN : TgSmall::BN;
   p.tiles_m = (M + bm - 1) / bm;
   p.tiles_n = silu ? (N / 2 + bn / 2 - 1) / (bn / 2) : (N + bn - 1) / bn;
 }
-// 256 x 256 tiles when there is one for every CU; otherwise 128 x 128 tiles, and K is sliced when there are
-// fewer tiles than half the CU count, or fewer than the CU count with long K (at least 128 steps): enough
-// slices to reach the CU count, each at least eight 32-wide steps, at most TG_MAX_SPLITS.
+// NS_TG_PLAN="big,splits" fixes the plan (big 1: 256 x 256 tiles, 0: 128 x 128; splits 0: the rule
+// below), for experiments
+static const int* tg_forced() {
+  static int v[2] = {-1, 0};
+  static const bool once = [] {
+    const char* e = getenv("NS_TG_PLAN");
+    if (e == nullptr || sscanf(e, "%d,%d", &v[0], &v[1]) != 2) v[0] = -1;
+    return true;
+  }();
+  (void)once;
+  return v[0] >= 0 ? v : nullptr;
+}
+// 256 x 256 tiles (one workgroup per CU) when there is one for every CU; otherwise 128 x 128 tiles (two per
+// CU). K is sliced only when it is long (at least 128 steps) and the tiles leave workgroup slots free: as many
+// slices as keep every workgroup resident in one round, at most TG_PLAN_SPLITS (the last slice's merge reads
+// every partial tile, and more slices cost more there than they win), each at least eight 32-wide steps.
+// Measured (1552 x 1536 x 8960: 3 slices 70.7 us, 2: 88.4, 4: 98.7; 96 x 1536 x 8960: 6 slices 29.6 us,
+// 8: 30.9, 3: 35.3; K = 1536 shapes were never faster sliced).
 static TgPlan tg_plan(int M, int N, int K, bool silu) {
   TgPlan p;
   const int T = target_workgroups(), steps = K / TG_BK;
-  p.wn = 4;
-  p.wm = 8;
+  const int* forced = tg_forced();
+  p.big = 1;
   tg_tiles(p, M, N, silu);
-  if (int64_t(p.tiles_m) * p.tiles_n < T) {
-    p.wn = 2;
-    p.wm = 4;
+  if (forced != nullptr ? forced[0] == 0 : int64_t(p.tiles_m) * p.tiles_n < T) {
+    p.big = 0;
     tg_tiles(p, M, N, silu);
   }
-  const int tiles = p.tiles_m * p.tiles_n;
+  const int tiles = p.tiles_m * p.tiles_n, slots = p.big ? T : 2 * T;
   int splits = 1;
-  if (tiles < T / 2 || (tiles < T && steps >= 128)) {
-    splits = (T + tiles - 1) / tiles;
-    if (splits > TG_MAX_SPLITS) splits = TG_MAX_SPLITS;
-    if (splits > steps / 8) splits = steps / 8 > 1 ? steps / 8 : 1;
+  if (forced != nullptr && forced[1] > 0) {
+    splits = forced[1];
+  } else if (steps >= 128 && tiles < slots) {
+    splits = slots / tiles;
+    if (splits > TG_PLAN_SPLITS) splits = TG_PLAN_SPLITS;
+    if (splits > steps / 8) splits = steps / 8;
   }
+  if (splits > TG_MAX_SPLITS) splits = TG_MAX_SPLITS;
+  if (splits > steps) splits = steps;
+  if (splits < 1) splits = 1;
   p.kps = (steps + splits - 1) / splits;
   p.splits = (steps + p.kps - 1) / p.kps;   // every slice non-empty
-  p.bytes = p.splits > 1 ? G_CNT_BYTES + align256(sizeof(float) * size_t(tiles) * p.splits * 32 * p.wm * 64 * p.wn) : 0;
+  const int part = p.big ? TgBig::PART : TgSmall::PART;
+  p.bytes = p.splits > 1 ? G_CNT_BYTES + align256(sizeof(float) * size_t(tiles) * p.splits * part) : 0;
   return p;
 }
 template <int EPI>
@@ -1540,10 +1616,10 @@ static int launch_tiled(const void* x, const void* w, const void* bias, void* y,
     a.part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + G_CNT_BYTES);
   }
   const dim3 grid(unsigned(p.tiles_m * p.tiles_n * p.splits));
-  if (p.wn == 4)
-    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 4, 8>), grid, dim3(TgShape<4, 8>::NT), 0, st, a);
+  if (p.big)
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 8, 4, 8>), grid, dim3(TgBig::NT), 0, st, a);
   else
-    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 2, 4>), grid, dim3(TgShape<2, 4>::NT), 0, st, a);
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 4, 4, 4>), grid, dim3(TgSmall::NT), 0, st, a);
   return check_launch("gemm(tiled)");
 }
 

@@ -3,9 +3,9 @@ CPU oracle, with the gate of the skinny-kernel tests: >= 99% bitwise identical t
 once-rounded product and every element within 1 bf16 ulp plus Higham's deterministic bound gamma_K * sum|x||w|
 (for both sides), propagated through the SiLU epilogue. The product replaces F.linear at
 nanoserve/model.py:231,256-257 on the large-token path. At 1552 rows the check covers every 128-row tile
-(its first, middle and last rows and the partial last tile) and every column; 1552 x 17920 runs the 256-row
-tiles, the rest the 128-row ones, K-sliced where there are few tiles.
-Also: K-sliced tiles (few tiles, small M) are deterministic and share the skinny kernels' workspace."""
+(its first, middle and last rows and the partial last tile) and every column; 1552 x 17920 runs the 256 x 256
+tiles, the rest the 128 x 128 ones, K-sliced where K is long (8960) and the tiles are few.
+Also: K-sliced tiles are deterministic and share the skinny kernels' workspace."""
 import pytest
 import torch
 
@@ -54,10 +54,10 @@ def test_tiled_linear_silu_mul(hiplib, M, I, K):
 
 
 def test_tiled_split_k_is_deterministic_and_shares_the_workspace(hiplib):
-    """M = 96 on a 1536 x 1536 projection: 12 tiles, so K is sliced; two calls agree bitwise, also with skinny
-    calls (which use the same workspace counters) in between."""
+    """M = 96 on the 1536 x 8960 down projection: 12 tiles and 280 k-steps, so K is sliced; two calls agree
+    bitwise, also with skinny calls (which use the same workspace counters) in between."""
     from nanoserve_amd.kernels.linear import linear
-    x, w = operands(96, 1536, 1536, seed=9)
+    x, w = operands(96, 1536, 8960, seed=9)
     xd, wd = x.cuda(), w.cuda()
     a = linear(xd, wd)
     linear(xd[:32].contiguous(), wd)
@@ -65,7 +65,7 @@ def test_tiled_split_k_is_deterministic_and_shares_the_workspace(hiplib):
     linear(xd[:7].contiguous(), wd)
     c = linear(xd, wd)
     assert torch.equal(a, b) and torch.equal(a, c)
-    bf16_check(a.cpu(), ref_linear(x, w), "split-K tiled 96x1536x1536", dot_bound(x, w))
+    bf16_check(a.cpu(), ref_linear(x, w), "split-K tiled 96x1536x8960", dot_bound(x, w))
 
 
 def test_tiled_rejects_normalised_input_through_the_c_abi(hiplib):
