@@ -216,6 +216,22 @@ int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int 
             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * LM head of a decode step with the greedy choice fused: y = round(x W^T) exactly as ns_gemm (no bias), and
+ * tokens[m] = ns_argmax_rows' result on row m of the stored y (first maximal index, NaN above every
+ * number), in one launch. Replaces F.linear(x, self.lm_head) (nanoserve/model.py:362) followed by
+ * logits.argmax(-1) (nanoserve/engine.py:239). Applies where ns_gemm_argmax_fused(M, N, K) returns 1 (at most
+ * 32 rows, K <= 2048, at least four 64-row weight tiles per CU: the persistent LM-head kernel); elsewhere
+ * call ns_gemm and ns_argmax_rows. argmax_workspace: the ns_argmax_rows workspace (zero-filled once,
+ * 256-byte aligned, at least NS_WS_COUNTER_BYTES bytes); the last 1 KB of its counter region holds this
+ * launch's arrival counter and per-row keys, which every launch leaves at zero. tokens may be pinned host
+ * memory.
+ */
+int ns_gemm_argmax_fused(int M, int N, int K);
+int ns_gemm_argmax(const void* x, const void* w, void* y, int M, int N, int K, int dtype,
+                   const float* x_sumsq, const void* x_norm_w, float x_eps, int64_t* tokens,
+                   void* argmax_workspace, size_t argmax_workspace_bytes, void* stream);
+
+/*
  * Merged gate/up projection + SwiGLU: w_gate_up = [gate; up] ([N2, K], N2 = 2 * intermediate);
  * out[M, N2/2] = round(round(silu(round(x Wg^T))) * round(x Wu^T)).
  * Replaces silu_mul(F.linear(h, gate_up_w)) (nanoserve/model.py:257, fused.py:75).
@@ -261,7 +277,7 @@ int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void*
  * ld elements); NaN ranks above every number (torch.argmax semantics). int64 output.
  * Replaces logits.argmax(-1) of nanoserve/engine.py:239 / sampling.py:59-60.
  * workspace (optional, zero-initialised once by the caller, 256-byte aligned, at least
- * ns_argmax_workspace_bytes(rows, n) bytes, which is 0 above 65,536 rows): rows are split over several
+ * ns_argmax_workspace_bytes(rows, n) bytes, which is 0 above 65,280 rows): rows are split over several
  * workgroups merged in the same launch; every call leaves the counter region at zero, so calls with any row
  * count may share one workspace. NULL: one workgroup per row.
  */

@@ -65,6 +65,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "ns_gemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,   # x w bias y M N K dtype
                          _c_vp, _c_vp, _c_f32,                                      # x_sumsq x_norm_w x_eps
                          _c_vp, _c_sz, _c_vp]),                                     # ws ws_bytes stream
+    "ns_gemm_argmax_fused": (_c_int, [_c_int, _c_int, _c_int]),
+    "ns_gemm_argmax": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,   # x w y M N K dtype
+                                _c_vp, _c_vp, _c_f32, _c_vp,                       # x_sumsq x_norm_w x_eps tokens
+                                _c_vp, _c_sz, _c_vp]),                             # argmax ws, bytes, stream
     "ns_gemm_silu_mul": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
                                   _c_vp, _c_vp, _c_f32, _c_vp, _c_sz, _c_vp]),
     "ns_gemm_residual_norm_stats": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp,      # x w residual res_out sumsq

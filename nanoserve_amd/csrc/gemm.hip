@@ -96,6 +96,10 @@ struct GemmArgs {
   // workspace (zeroed once by the owner; every launch leaves the counters at zero)
   unsigned* cnt;    // [tiles] arrival counters + [1] finished-tile counter (start of the workspace)
   float* part;      // [(tiles - whole) * ks][64 rows][64] published partial tiles of the sliced tiles
+  // fused argmax of the persistent kernel: tokens [M], per-row keys [M] and the arrival counter (left zero)
+  int64_t* am_out;
+  unsigned long long* am_key;
+  unsigned* am_cnt;
 };
 
 // Weight row of n-tile j, row r (0..15) of tile t (clamped inside the matrix / its half).
@@ -599,9 +603,15 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
 // kernel), so the next tile's first chunks are in flight while a tile's partial sums are reduced and
 // stored; the reduction reuses the stage buffer of the tile's last chunk. CP: chunks per tile rounded up to
 // even (a padding chunk re-reads the last one and multiplies nothing).
-template <int TM, bool NX, int CP>
+// AM: the greedy argmax of every row is fused (the LM head of a decode step). The thread that stores
+// (row m, 8 columns) of a tile keeps the row's best (stored bf16 value, index) over its tiles; at the end
+// the 8 threads of a row combine, one 64-bit atomic max per (workgroup, row) folds it into the row's key
+// (argmax_key: the order of torch.argmax), and the last workgroup to arrive turns the keys into tokens and
+// clears them. The result is ns_argmax_rows' on the stored logits.
+template <int TM, bool NX, int CP, bool AM>
 __global__ __launch_bounds__(G_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void persist_gemm_kernel(GemmArgs a) {
   static_assert(TM <= 2 && CP % 2 == 0 && CP <= 8, "reduction in one stage buffer; K <= 2048");
+  static_assert(g_items8<TM>() == 1, "one (row, 8 columns) item per thread");
   __shared__ __align__(16) unsigned char lds[2 * G_STAGE];
   constexpr int R = 16 * TM;
   const int G = gridDim.x, K = a.K, N = a.N;
@@ -714,6 +724,8 @@ __global__ __launch_bounds__(G_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2,
     buf ^= 1;
   };
   const g_u32x4_t none[g_items8<4>()] = {};
+  float am_v = -INFINITY;   // AM: this thread's row best so far (row tid / 8, its 8 columns of every tile)
+  int am_i = 0x7fffffff;
   for (int i = 0; i < n_my; ++i) {
     step(Q0{}, std::integral_constant<int, 0>{}, i);
     step(Q1{}, std::integral_constant<int, 1>{}, i);
@@ -742,7 +754,61 @@ __global__ __launch_bounds__(G_WAVES * 64) __attribute__((amdgpu_waves_per_eu(2,
       }
     __syncthreads();
     TileSource src{red, R, false, 1, nullptr};
-    tile_epilogue<TM, EPI_STORE>(a, src, int(blockIdx.x) + i * G, none);
+    if constexpr (!AM) {
+      tile_epilogue<TM, EPI_STORE>(a, src, int(blockIdx.x) + i * G, none);
+    } else {   // the STORE epilogue (no bias), keeping the stored values' best per row
+      const int m = tid >> 3, cq = tid & 7, n0 = (int(blockIdx.x) + i * G) * 64 + 8 * cq;
+      if (m < a.M && n0 < N) {
+        float v[8];
+        tile_values(src, m, 8 * cq, v);
+        bf16_t* dst = a.y + int64_t(m) * N + n0;
+        if ((N & 7) == 0) {
+          store_bf16x8(dst, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float f = __uint_as_float(pack_bf16x2(v[e], 0.f) << 16);
+            if (better(f, n0 + e, am_v, am_i)) { am_v = f; am_i = n0 + e; }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n0 + e < N) {
+              const bf16_t b = f32_to_bf16(v[e]);
+              dst[e] = b;
+              const float f = bf16_to_f32(b);
+              if (better(f, n0 + e, am_v, am_i)) { am_v = f; am_i = n0 + e; }
+            }
+        }
+      }
+    }
+  }
+  if constexpr (AM) {
+    __shared__ unsigned s_am_last;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {   // the 8 threads of a row are 8 consecutive lanes
+      const float ov = __shfl_xor(am_v, o, 64);
+      const int oi = __shfl_xor(am_i, o, 64);
+      if (better(ov, oi, am_v, am_i)) { am_v = ov; am_i = oi; }
+    }
+    const int m = tid >> 3;
+    if ((tid & 7) == 0 && m < a.M && am_i != 0x7fffffff)
+      __hip_atomic_fetch_max(a.am_key + m, argmax_key(am_v, am_i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    publish_complete();
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = publish_count(a.am_cnt);
+      const unsigned last = prev == unsigned(G - 1);
+      if (last) publish_reset(a.am_cnt);
+      s_am_last = last;
+    }
+    __syncthreads();
+    if (s_am_last == 0u) return;
+    acquire_published();
+    if (tid < a.M) {
+      const unsigned long long key = __hip_atomic_load(a.am_key + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.am_key + tid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      a.am_out[tid] = key == 0ull ? 0 : int64_t(~uint32_t(key));
+    }
   }
 }
 
@@ -1472,33 +1538,41 @@ static int launch_t16(const GemmArgs& a, int tiles, hipStream_t st) {
 static bool persist_fits(int M, int K, int tiles, const void* bias) {
   return M <= 32 && K <= 2048 && tiles >= 4 * target_workgroups() && bias == nullptr;
 }
-template <bool NX, int CP>
+template <bool NX, int CP, bool AM>
 static void launch_persist_cp(const GemmArgs& a, int grid, hipStream_t st) {
   if (a.M <= 16)
-    hipLaunchKernelGGL((persist_gemm_kernel<1, NX, CP>), dim3(unsigned(grid)), dim3(G_WAVES * 64), 0, st, a);
+    hipLaunchKernelGGL((persist_gemm_kernel<1, NX, CP, AM>), dim3(unsigned(grid)), dim3(G_WAVES * 64), 0, st, a);
   else
-    hipLaunchKernelGGL((persist_gemm_kernel<2, NX, CP>), dim3(unsigned(grid)), dim3(G_WAVES * 64), 0, st, a);
+    hipLaunchKernelGGL((persist_gemm_kernel<2, NX, CP, AM>), dim3(unsigned(grid)), dim3(G_WAVES * 64), 0, st, a);
 }
-template <bool NX>
+template <bool NX, bool AM>
 static void launch_persist_nx(const GemmArgs& a, int grid, hipStream_t st) {
   switch ((a.chunks + 1) & ~1) {
-    case 2: launch_persist_cp<NX, 2>(a, grid, st); break;
-    case 4: launch_persist_cp<NX, 4>(a, grid, st); break;
-    case 6: launch_persist_cp<NX, 6>(a, grid, st); break;
-    default: launch_persist_cp<NX, 8>(a, grid, st); break;
+    case 2: launch_persist_cp<NX, 2, AM>(a, grid, st); break;
+    case 4: launch_persist_cp<NX, 4, AM>(a, grid, st); break;
+    case 6: launch_persist_cp<NX, 6, AM>(a, grid, st); break;
+    default: launch_persist_cp<NX, 8, AM>(a, grid, st); break;
   }
 }
-// Two resident workgroups per CU, each with the same number of tiles (the last one fewer).
+// Two resident workgroups per CU, each with the same number of tiles (the last one fewer). a.am_out set:
+// the argmax fused.
 static int launch_persist(GemmArgs a, int tiles, hipStream_t st) {
   a.tiles = tiles;
   a.chunks = (a.K + G_KC - 1) / G_KC;
   const int T = 2 * target_workgroups();
   const int per = (tiles + T - 1) / T;
   const int grid = (tiles + per - 1) / per;
-  if (a.xsq != nullptr)
-    launch_persist_nx<true>(a, grid, st);
-  else
-    launch_persist_nx<false>(a, grid, st);
+  if (a.am_out != nullptr) {
+    if (a.xsq != nullptr)
+      launch_persist_nx<true, true>(a, grid, st);
+    else
+      launch_persist_nx<false, true>(a, grid, st);
+  } else {
+    if (a.xsq != nullptr)
+      launch_persist_nx<true, false>(a, grid, st);
+    else
+      launch_persist_nx<false, false>(a, grid, st);
+  }
   return check_launch("gemm(persistent)");
 }
 
@@ -1667,6 +1741,34 @@ extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, 
   if (persist_fits(M, K, (N + 63) / 64, bias)) return launch_persist(a, (N + 63) / 64, reinterpret_cast<hipStream_t>(stream));
   if ((st = bind_workspace(a, make_plan((N + 63) / 64, K), ws, ws_bytes)) != NS_OK) return st;
   return launch<EPI_STORE>(a, reinterpret_cast<hipStream_t>(stream));
+}
+
+static_assert(WS_AM_FUSED_OFF % 2 == 0 && 2 + 2 * G_MAX_M <= WS_AM_FUSED_WORDS, "fused argmax words");
+extern "C" int ns_gemm_argmax_fused(int M, int N, int K) {
+  return M >= 1 && M <= G_MAX_M && N >= 1 && K >= 32 && K % 32 == 0 && persist_fits(M, K, (N + 63) / 64, nullptr) ? 1 : 0;
+}
+
+extern "C" int ns_gemm_argmax(const void* x, const void* w, void* y, int M, int N, int K, int dtype,
+                              const float* x_sumsq, const void* x_norm_w, float x_eps, int64_t* tokens,
+                              void* argmax_ws, size_t argmax_ws_bytes, void* stream) {
+  int st = check_common(x, w, M, N, K, dtype);
+  if (st != NS_OK) return st;
+  NS_REQUIRE(ns_gemm_argmax_fused(M, N, K) == 1,
+             "gemm_argmax: M=%d N=%d K=%d is not a persistent LM-head shape (ns_gemm_argmax_fused)", M, N, K);
+  NS_REQUIRE(y != nullptr && aligned16(y) && tokens != nullptr, "gemm_argmax: 16-byte aligned y and tokens needed");
+  if (argmax_ws == nullptr || argmax_ws_bytes < WS_COUNTER_BYTES || reinterpret_cast<uintptr_t>(argmax_ws) % 256 != 0) {
+    set_error("gemm_argmax: a zero-initialised, 256-byte aligned argmax workspace of at least %zu bytes is needed, got %zu",
+              WS_COUNTER_BYTES, argmax_ws == nullptr ? size_t(0) : argmax_ws_bytes);
+    return NS_E_WORKSPACE;
+  }
+  GemmArgs a = base_args(x, w, M, N, K);
+  a.y = static_cast<bf16_t*>(y);
+  if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
+  unsigned* words = static_cast<unsigned*>(argmax_ws);
+  a.am_out = tokens;
+  a.am_cnt = words + WS_AM_FUSED_OFF;
+  a.am_key = reinterpret_cast<unsigned long long*>(words + WS_AM_FUSED_OFF + 2);
+  return launch_persist(a, (N + 63) / 64, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int N2, int K, int dtype,

@@ -30,6 +30,21 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
 // Value of f rounded to bf16, kept in fp32.
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// torch.argmax order: a beats b for a larger value, or NaN over a number, or the same value (or both NaN)
+// and a smaller index.
+__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an || bn) return an && (!bn || ai < bi);
+  return av > bv || (av == bv && ai < bi);
+}
+// The same order as one unsigned 64-bit key (so an atomic max picks the winner): high word the value's
+// rank (every NaN highest, -0 equal to +0, then the IEEE order as unsigned bits), low word ~index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+  uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  u = v != v ? 0xffffffffu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+  return (static_cast<unsigned long long>(u) << 32) | static_cast<uint32_t>(~uint32_t(i));
+}
+
 // Sum / max over the 64 lanes of a wavefront (butterfly; every lane receives the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -103,6 +118,12 @@ __device__ __forceinline__ void acquire_published() {
 // partial results of any call start after it.
 constexpr size_t WS_COUNTER_BYTES = size_t(NS_WS_COUNTER_BYTES);
 constexpr int WS_MAX_COUNTERS = int(WS_COUNTER_BYTES / 4);
+// The last WS_AM_FUSED_WORDS words of an argmax workspace's counter region belong to the LM head with the
+// argmax fused (ns_gemm_argmax): its arrival counter (word WS_AM_FUSED_OFF) and one 8-byte key per row
+// (from word WS_AM_FUSED_OFF + 2), which that launch leaves at zero like the counters; the split argmax
+// kernel's per-row counters stay below WS_AM_FUSED_OFF.
+constexpr int WS_AM_FUSED_WORDS = 256;
+constexpr int WS_AM_FUSED_OFF = WS_MAX_COUNTERS - WS_AM_FUSED_WORDS;
 
 // Host side: error slot and launch checking.
 void set_error(const char* fmt, ...);

@@ -10,13 +10,6 @@
 
 namespace ns {
 
-// a beats b: larger value, or NaN over a number, or same value (or both NaN) and smaller index
-__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
-  const bool an = av != av, bn = bv != bv;
-  if (an || bn) return an && (!bn || ai < bi);
-  return av > bv || (av == bv && ai < bi);
-}
-
 template <typename T>
 __device__ __forceinline__ float ldf(const T* p, int64_t i);
 template <>
@@ -206,7 +199,7 @@ using namespace ns;
 // Workspace: the fixed counter region (one arrival counter per row; shared safely by calls with any row
 // count), then each row's per-split (value, index) partials.
 extern "C" size_t ns_argmax_workspace_bytes(int64_t rows, int n) {
-  if (rows <= 0 || n <= 0 || rows > WS_MAX_COUNTERS) return 0;
+  if (rows <= 0 || n <= 0 || rows > WS_AM_FUSED_OFF) return 0;
   return WS_COUNTER_BYTES + size_t(rows) * AM_MAX_SPLITS * 8;
 }
 
@@ -220,7 +213,7 @@ extern "C" int ns_argmax_rows(const void* x, int64_t ld, int64_t rows, int n, in
   const int esz = dtype == NS_DTYPE_BF16 ? 2 : 4;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ld * esz) % 16 == 0;
   const int splits = argmax_splits(rows, n);
-  if (workspace != nullptr && aligned && splits > 1 && rows <= WS_MAX_COUNTERS) {
+  if (workspace != nullptr && aligned && splits > 1 && rows <= WS_AM_FUSED_OFF) {
     NS_REQUIRE(workspace_bytes >= ns_argmax_workspace_bytes(rows, n) && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
                "argmax_rows: a zero-initialised, 256-byte aligned workspace of %zu bytes is needed, got %zu",
                ns_argmax_workspace_bytes(rows, n), workspace_bytes);

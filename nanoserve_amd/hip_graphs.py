@@ -10,8 +10,9 @@ Contract of nanoserve/cuda_graphs.py:42-126 (DecodeGraphRunner):
 Design (this build's own): every bucket is a StepGraph -- one packed device buffer holding all of a step's
 inputs (tokens, positions, slots int64 [B]; context lengths int32 [B]; block tables int32 [B, W]) with TWO
 pinned host twins, so a step is staged by numpy writes into the twin the previous step's copy is not
-reading and arrives in ONE host-to-device copy; the captured forward ends in the HIP argmax, which writes
-the greedy tokens straight into pinned host memory (no device-to-host copy after the replay). A table row
+reading and arrives in ONE host-to-device copy; the captured forward ends in the LM head with the argmax
+fused (one launch), which writes the greedy tokens straight into pinned host memory (no device-to-host copy
+after the replay). A table row
 is staged incrementally: block lists only grow between steps (truncation and release rebind them), so a
 row staged from the same list needs only its new tail. The next step can be staged while the current one
 runs (prestage / launch_prestaged), which the engine uses for steady greedy decode. Captures share one
@@ -104,11 +105,8 @@ class StepGraph:
         seqs = [SeqInput(1, ctx_len=1, use_kernel=True)] * B
 
         def forward():
-            from nanoserve_amd.kernels.sampling import argmax_rows
-            logits = runner.model.forward_batch(tok, pos, seqs, logits="all", paged=runner.pool,
-                                                slot_mapping=slots, decode_meta=meta)
-            argmax_rows(logits, self.greedy)
-            return logits
+            return runner.model.forward_batch(tok, pos, seqs, logits="all", paged=runner.pool, slot_mapping=slots,
+                                              decode_meta=meta, greedy_out=self.greedy)
 
         # warm-up and capture run on padding rows only: they read and write nothing but the garbage block
         self.graph, self.logits = capture(forward, runner.mempool)
@@ -252,7 +250,6 @@ class MixedStepGraph:
     """One mixed-step bucket: N + 1 rows, S prefill entries, D decode entries (see the module docstring)."""
 
     def __init__(self, runner: "MixedGraphRunner", N: int, S: int):
-        from nanoserve_amd.kernels.sampling import argmax_rows
         self.N, self.S, self.D, self.W = N, S, runner.max_decode, runner.max_blocks
         R, D, W = N + 1, self.D, self.W
         self.garbage_block = runner.garbage_block
@@ -278,10 +275,8 @@ class MixedStepGraph:
         seqs = [SeqInput(R)]
 
         def forward():
-            logits = runner.model.forward_batch(tok, pos, seqs, logits=rows, paged=runner.pool, slot_mapping=slots,
-                                                decode_meta=meta, prefill_meta=prefill)
-            argmax_rows(logits, self.greedy)
-            return logits
+            return runner.model.forward_batch(tok, pos, seqs, logits=rows, paged=runner.pool, slot_mapping=slots,
+                                              decode_meta=meta, prefill_meta=prefill, greedy_out=self.greedy)
 
         self.forward = forward
         self.graph, self.logits = None, None

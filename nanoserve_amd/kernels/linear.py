@@ -146,6 +146,29 @@ def linear(x, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
     return y
 
 
+def linear_argmax(x, w: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """LM head with the greedy choice: returns x W^T (the logits of `linear`) and writes their row-wise argmax
+    (first maximal index, NaN highest) into `tokens` (int64 [M], device or pinned host memory). One launch
+    where the persistent LM-head kernel takes the shape (ns_gemm_argmax_fused), else linear + argmax_rows."""
+    from nanoserve_amd.kernels.sampling import argmax_rows, argmax_workspace
+    t = x.r if isinstance(x, NormedRows) else x
+    M, K = t.shape
+    N = w.shape[0]
+    assert tokens.dtype == torch.int64 and tokens.shape == (M,) and tokens.is_contiguous()
+    if hip_ok(x, w) and _lib.lib().ns_gemm_argmax_fused(M, N, K) == 1:
+        ws = argmax_workspace(w.device)
+        if ws is not None:
+            y = torch.empty(M, N, device=t.device, dtype=t.dtype)
+            xp, sq, nw, eps = _x_args(x)
+            _lib.check(_lib.lib().ns_gemm_argmax(xp, w.data_ptr(), y.data_ptr(), M, N, K, 1, sq, nw, eps,
+                                                 tokens.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(w)),
+                       "linear_argmax")
+            return y
+    y = linear(x, w)
+    argmax_rows(y, tokens)
+    return y
+
+
 def linear_silu_mul(x, w_gate_up: torch.Tensor) -> torch.Tensor:
     if not hip_ok(x, w_gate_up):
         return silu_mul(F.linear(_dense(x), w_gate_up))

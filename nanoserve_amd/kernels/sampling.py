@@ -31,6 +31,12 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     return ws
 
 
+def argmax_workspace(device: torch.device) -> torch.Tensor | None:
+    """The argmax workspace of `device` (at least the counter region the LM head with the argmax fused keeps
+    its arrival counter and keys in); None inside a capture that would have to allocate it."""
+    return _workspace(device, _lib.lib().ns_argmax_workspace_bytes(_WS_MIN_ROWS, 1 << 20))
+
+
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """logits [R, V] (last dim contiguous) -> int64 [R]. `out` may be pinned host memory (the kernel writes
     it over the bus; read it after synchronising the stream)."""

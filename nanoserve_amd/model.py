@@ -362,13 +362,15 @@ class Qwen2Model:
     @torch.inference_mode()
     def forward_batch(self, token_ids: torch.Tensor, positions: torch.Tensor, seqs: list[SeqInput],
                       logits="last", paged=None, slot_mapping: torch.Tensor | None = None,
-                      decode_meta: DecodeMeta | None = None, prefill_meta: tuple | None = None) -> torch.Tensor:
+                      decode_meta: DecodeMeta | None = None, prefill_meta: tuple | None = None,
+                      greedy_out: torch.Tensor | None = None) -> torch.Tensor:
         """One forward pass over several sequences (prefilling, continuing a chunked prefill on a cached
         context, or decoding one token). token_ids/positions: [N] in `seqs` order. Returns logits
         [len(seqs), vocab] for each sequence's last token ("last"), [N, vocab] ("all"), or the rows of an
         index tensor. prefill_meta: the chunked-prefill kernel's inputs already on the device, ("chunks",
         tables int32 [S, W], seq_info int32 [S, 4], max_new, max_kv) -- the non-decode rows are then described
-        by them alone (a captured mixed step), and `seqs` only has to cover the rows."""
+        by them alone (a captured mixed step), and `seqs` only has to cover the rows. greedy_out (int64, one
+        entry per returned row; device or pinned host memory) receives the rows' argmax."""
         self._require_gpu()
         if paged is None:
             raise ValueError("the HIP path needs the paged KV cache (`paged` + `slot_mapping`)")
@@ -390,12 +392,13 @@ class Qwen2Model:
             next_norm = self.layers[i + 1].ln1 if i + 1 < L else self.norm
             h, x = self._mlp(i, x, o, next_norm)       # h: the next layer's normed input / the final norm
         self._rows_cache = None
-        return self.lm_head_rows(h, seqs, logits)
+        return self.lm_head_rows(h, seqs, logits, greedy_out)
 
-    def lm_head_rows(self, x, seqs: list[SeqInput], logits="last") -> torch.Tensor:
+    def lm_head_rows(self, x, seqs: list[SeqInput], logits="last", greedy_out: torch.Tensor | None = None) -> torch.Tensor:
         """Final-normed hidden states ([1, N, H] / [N, H] tensor, or a NormedRows) -> logits of the requested
-        rows."""
-        from nanoserve_amd.kernels.linear import NormedRows, linear
+        rows; with `greedy_out` (int64 [rows]) their argmax is written there too (fused into the LM head's
+        launch where the kernel takes the shape)."""
+        from nanoserve_amd.kernels.linear import NormedRows, linear, linear_argmax
         if isinstance(x, torch.Tensor) and x.dim() == 3:
             x = x[0]
         idx = None
@@ -412,8 +415,11 @@ class Qwen2Model:
         if isinstance(x, NormedRows):
             if x.r.shape[0] > 32 or x.r.shape[1] > 2048:
                 x = x.tensor()
-            return linear(x, self.lm_head)
-        return linear(x.contiguous(), self.lm_head)
+        else:
+            x = x.contiguous()
+        if greedy_out is not None:
+            return linear_argmax(x, self.lm_head, greedy_out)
+        return linear(x, self.lm_head)
 
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, cache=None, logits: str = "last"):
         raise NotImplementedError("the single-sequence contiguous-cache API (M1) is not part of the HIP path; "
