@@ -206,10 +206,11 @@ size_t ns_gemm_workspace_bytes(int M, int N, int K);
 /*
  * y = round(x W^T + bias); bias may be NULL.
  * Any M >= 1: above 64 rows (prefill chunks, mixed steps, speculative verify batches; nanoserve/model.py:231,
- * 256-257 on the large-token path) a tiled MFMA kernel computes the product (128 x 128 or 256 x 256 output
- * tiles, K sliced and the slices summed in a fixed order when there are few tiles); x_sumsq must then be NULL
- * (materialise a normalised input with ns_rms_norm_apply first), and the workspace is sized by
- * ns_gemm_workspace_bytes(M, N, K) as for the skinny kernels.
+ * 256-257 on the large-token path) x_sumsq must be NULL (materialise a normalised input with
+ * ns_rms_norm_apply first). Up to 192 rows a projection with K <= 2048 and at most 8,192 rows of W runs on the
+ * tile-16 kernel in 16-token blocks; otherwise a tiled MFMA kernel computes the product (128 x 128 or
+ * 256 x 256 output tiles, K sliced and the slices summed in a fixed order for long K and few tiles), its
+ * workspace sized by ns_gemm_workspace_bytes(M, N, K) as for the skinny kernels.
  */
 int ns_gemm(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, int dtype,
             const float* x_sumsq, const void* x_norm_w, float x_eps,
@@ -266,6 +267,10 @@ int ns_rms_norm_apply(const void* r, const float* row_sumsq, const void* norm_w,
  * ns_rope_qkv contract on it (q, k, v outputs; k/v stored at slots when k_cache is given).
  * head_dim 64 or 128. Replaces rope_qkv(F.linear(h, qkv_w, qkv_b), ...) (nanoserve/model.py:231-234).
  */
+/* 1 when ns_gemm_rope_qkv takes M rows (normed: a normalised input): any M <= 64, and above that a plain input
+ * with K <= 2048 up to 192 rows (the tile-16 kernel token-split: speculative verify batches). No counterpart
+ * in the reference; it tells the caller when to run the GEMM and ns_rope_qkv separately instead. */
+int ns_gemm_rope_qkv_fits(int M, int K, int n_heads, int n_kv_heads, int head_dim, int normed);
 int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void* cos, const void* sin,
                      void* q, void* k, void* v, void* k_cache, void* v_cache, const int64_t* slots, int M,
                      int K, int n_heads, int n_kv_heads, int head_dim, int dtype,

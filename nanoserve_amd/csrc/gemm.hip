@@ -72,6 +72,7 @@ struct GemmArgs {
   const bf16_t* w;
   int M, N, K;              // N: rows of w
   int tiles, chunks;        // tiles, 256-k chunks per tile
+  int mblocks;              // STORE above 64 rows: 64-row token blocks, each a whole plan of its own
   int whole, ks;            // tiles [0, whole) get one workgroup each; every later tile is cut into ks
                             // K slices, one workgroup each, summed by the last slice to finish
   // epilogue operands
@@ -411,7 +412,19 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   __shared__ unsigned s_flag;
   constexpr int R = 16 * TM;
   // this workgroup's segment: chunks [c0, c1) of tile t (slice s of ks)
-  const int b = blockIdx.x, C = a.chunks, K = a.K;
+  int b = blockIdx.x;
+  if constexpr (EPI == EPI_STORE) {
+    if (a.mblocks > 1) {   // token block mb: rows 64 mb .. 64 mb + 63, with its own counters and partials
+      const int per = a.whole + (a.tiles - a.whole) * a.ks, mb = b / per;
+      b -= mb * per;
+      a.x += int64_t(G_MAX_M) * mb * a.K;
+      a.y += int64_t(G_MAX_M) * mb * a.N;
+      a.M = min(G_MAX_M, a.M - G_MAX_M * mb);
+      a.cnt += mb * a.tiles;
+      a.part += int64_t(mb) * (a.tiles - a.whole) * a.ks * G_MAX_M * 64;
+    }
+  }
+  const int C = a.chunks, K = a.K;
   int t, s, ks;
   if (b < a.whole) {
     t = b;
@@ -1483,7 +1496,8 @@ static int bind_workspace(GemmArgs& a, const Plan& p, void* ws, size_t ws_bytes)
 
 template <int EPI, bool NX>
 static void launch_nx(const GemmArgs& a, hipStream_t st) {
-  const dim3 grid(unsigned(a.whole + (a.tiles - a.whole) * a.ks)), block(G_WAVES * 64);
+  const dim3 grid(unsigned((a.whole + (a.tiles - a.whole) * a.ks) * (a.mblocks > 1 ? a.mblocks : 1))),
+      block(G_WAVES * 64);
   if (a.M <= 16)
     hipLaunchKernelGGL((skinny_gemm_kernel<1, EPI, NX>), grid, block, 0, st, a);
   else if (a.M <= 32)
@@ -1505,10 +1519,26 @@ static bool t16_token_split(int M, int tiles) {
   }();
   return on && M > 16 && tiles * ((M + 15) / 16) <= T16_MAX_TILES;
 }
+// Above 64 rows a plain input on a projection the tile-16 kernel takes (K <= 2048, at most T16_MAX_TILES
+// tiles) runs it token-split (16-token blocks, the blocks of a tile re-reading its weights from L2), in as
+// many rounds as it needs, up to T16_LARGE_M rows (speculative verify batches); larger chunks go to the
+// tiled kernel. NS_T16_MAX_M overrides the bound, for experiments.
+constexpr int T16_LARGE_M = 192;
+static int t16_max_m() {
+  static const int v = [] {
+    const char* e = getenv("NS_T16_MAX_M");
+    const int x = e != nullptr ? atoi(e) : 0;
+    return x > 0 ? x : T16_LARGE_M;
+  }();
+  return v;
+}
+static bool t16_large_m(int M, int K, int tiles, bool normed) {
+  return M > G_MAX_M && M <= t16_max_m() && !normed && tile16_fits(K, tiles);
+}
 template <int EPI, bool NX>
 static void launch_t16_nx(const GemmArgs& a, int tiles, hipStream_t st) {
   const dim3 block{unsigned(T16_WAVES * 64)};
-  if (t16_token_split(a.M, tiles)) {
+  if (a.M > G_MAX_M || t16_token_split(a.M, tiles)) {
     hipLaunchKernelGGL((tile16_gemm_kernel<1, EPI, NX>), dim3(unsigned(tiles * ((a.M + 15) / 16))), block, 0, st, a);
     return;
   }
@@ -1714,10 +1744,24 @@ static bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 1
 using namespace ns;
 
 // Largest workspace any entry point needs for this shape (the SILU plan has at most as many tiles).
+// Above 64 rows a plain STORE projection too long for the tile-16 kernel (K > 2048: the down projection of a
+// verify batch) runs the skinny kernel in 64-row token blocks, up to T16_LARGE_M rows: every block a whole
+// plan with its own counters and partials, all in one launch (the later blocks find the weights in L2).
+static bool skinny_large_m(int M, int K, int N) {
+  return M > G_MAX_M && M <= t16_max_m() && K > T16_MAX_K && (M + G_MAX_M - 1) / G_MAX_M * ((N + 63) / 64) <= G_MAX_TILES;
+}
+static size_t skinny_large_m_bytes(const Plan& p, int mblocks) {
+  return p.part_off + size_t(mblocks) * (p.bytes - p.part_off);
+}
+
 extern "C" size_t ns_gemm_workspace_bytes(int M, int N, int K) {
   if (M < 1 || N < 1 || K < 32) return 0;
   if (M > G_MAX_M) {
-    const size_t a = tg_plan(M, N, K, false).bytes, b = tg_plan(M, N, K, true).bytes;
+    size_t a = tg_plan(M, N, K, false).bytes, b = tg_plan(M, N, K, true).bytes;
+    if (skinny_large_m(M, K, N)) {
+      const size_t c = skinny_large_m_bytes(make_plan((N + 63) / 64, K), (M + G_MAX_M - 1) / G_MAX_M);
+      a = a > c ? a : c;
+    }
     return a > b ? a : b;
   }
   return make_plan((N + 63) / 64, K).bytes;
@@ -1731,6 +1775,23 @@ extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, 
   NS_REQUIRE(y != nullptr && aligned16(y), "gemm: output must be 16-byte aligned");
   if (M > G_MAX_M) {
     NS_REQUIRE(x_sumsq == nullptr, "gemm: a normalised input (x_sumsq) needs M <= %d", G_MAX_M);
+    if (t16_large_m(M, K, (N + 15) / 16, false)) {
+      GemmArgs a = base_args(x, w, M, N, K);
+      a.bias = static_cast<const bf16_t*>(bias);
+      a.y = static_cast<bf16_t*>(y);
+      return launch_t16<EPI_STORE>(a, (N + 15) / 16, reinterpret_cast<hipStream_t>(stream));
+    }
+    if (skinny_large_m(M, K, N)) {
+      GemmArgs a = base_args(x, w, M, N, K);
+      a.bias = static_cast<const bf16_t*>(bias);
+      a.y = static_cast<bf16_t*>(y);
+      a.mblocks = (M + G_MAX_M - 1) / G_MAX_M;
+      const Plan p = make_plan((N + 63) / 64, K);
+      Plan pm = p;
+      pm.bytes = skinny_large_m_bytes(p, a.mblocks);
+      if ((st = bind_workspace(a, pm, ws, ws_bytes)) != NS_OK) return st;
+      return launch<EPI_STORE>(a, reinterpret_cast<hipStream_t>(stream));
+    }
     return launch_tiled<EPI_STORE>(x, w, bias, y, M, N, K, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
   }
   GemmArgs a = base_args(x, w, M, N, K);
@@ -1823,6 +1884,12 @@ extern "C" int ns_rms_norm_apply(const void* r, const float* row_sumsq, const vo
   return check_launch("rms_norm_apply");
 }
 
+extern "C" int ns_gemm_rope_qkv_fits(int M, int K, int n_heads, int n_kv_heads, int head_dim, int normed) {
+  const int N = (n_heads + 2 * n_kv_heads) * head_dim;
+  if (M < 1 || K < 32 || K % 32 != 0 || n_heads < 1 || n_kv_heads < 1 || (head_dim != 64 && head_dim != 128)) return 0;
+  return M <= G_MAX_M || t16_large_m(M, K, N / 16, normed != 0) ? 1 : 0;
+}
+
 extern "C" int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void* cos, const void* sin,
                                 void* q, void* k, void* v, void* k_cache, void* v_cache, const int64_t* slots, int M,
                                 int K, int n_heads, int n_kv_heads, int head_dim, int dtype, const float* x_sumsq,
@@ -1830,8 +1897,11 @@ extern "C" int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, 
   NS_REQUIRE(head_dim == 64 || head_dim == 128, "gemm_rope_qkv: head_dim %d (64 or 128)", head_dim);
   NS_REQUIRE(n_heads >= 1 && n_kv_heads >= 1, "gemm_rope_qkv: heads %d / %d", n_heads, n_kv_heads);
   const int N = (n_heads + 2 * n_kv_heads) * head_dim;
-  int st = check_common(x, w, M, N, K, dtype);
+  int st = check_common(x, w, M, N, K, dtype, INT_MAX);
   if (st != NS_OK) return st;
+  NS_REQUIRE(M <= G_MAX_M || t16_large_m(M, K, N / 16, x_sumsq != nullptr),
+             "gemm_rope_qkv: M=%d above %d needs a plain input, K <= %d and at most %d rows (ns_gemm_rope_qkv_fits)", M,
+             G_MAX_M, T16_MAX_K, t16_max_m());
   NS_REQUIRE((k_cache == nullptr) == (v_cache == nullptr) && (k_cache == nullptr || slots != nullptr),
              "gemm_rope_qkv: give both caches and slots, or none");
   NS_REQUIRE(cos != nullptr && sin != nullptr && q != nullptr && k != nullptr && v != nullptr,

@@ -208,7 +208,10 @@ def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.T
 
 def linear_rope_qkv(x, w: torch.Tensor, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
                     n_heads: int, n_kv_heads: int, head_dim: int, k_cache=None, v_cache=None, slots=None):
-    if not skinny_ok(x, w) or not (cos.is_contiguous() and sin.is_contiguous()) or head_dim not in (64, 128):
+    fits = (hip_ok(x, w) and head_dim in (64, 128) and cos.is_contiguous() and sin.is_contiguous()
+            and _lib.lib().ns_gemm_rope_qkv_fits(x.shape[0], x.shape[1], n_heads, n_kv_heads, head_dim,
+                                                 int(isinstance(x, NormedRows))) == 1)
+    if not fits:
         return rope_qkv(linear(x, w, b), cos, sin, n_heads, n_kv_heads, head_dim, k_cache, v_cache, slots)
     M, K = x.shape
     N = w.shape[0]

@@ -1,11 +1,13 @@
-"""Tiled HIP GEMM (csrc/gemm.hip, M > 64: prefill chunks, mixed steps, speculative verify batches) vs the
+"""HIP GEMMs above 64 rows (csrc/gemm.hip: prefill chunks, mixed steps, speculative verify batches) vs the
 CPU oracle, with the gate of the skinny-kernel tests: >= 99% bitwise identical to the fp32-accumulated,
 once-rounded product and every element within 1 bf16 ulp plus Higham's deterministic bound gamma_K * sum|x||w|
 (for both sides), propagated through the SiLU epilogue. The product replaces F.linear at
 nanoserve/model.py:231,256-257 on the large-token path. At 1552 rows the check covers every 128-row tile
-(its first, middle and last rows and the partial last tile) and every column; 1552 x 17920 runs the 256 x 256
-tiles, the rest the 128 x 128 ones, K-sliced where K is long (8960) and the tiles are few.
-Also: K-sliced tiles are deterministic and share the skinny kernels' workspace."""
+(its first, middle and last rows and the partial last tile) and every column. Routes: up to 192 rows the
+K <= 2048 projections run the tile-16 kernel in 16-token blocks and the 8960-long ones the skinny kernel in
+64-row token blocks; otherwise the tiled kernel (1552 x 17920 on 256 x 256 tiles, the rest on 128 x 128,
+K-sliced where K is long and the tiles are few).
+Also: K-sliced products are deterministic and share the skinny kernels' workspace."""
 import pytest
 import torch
 
@@ -54,8 +56,8 @@ def test_tiled_linear_silu_mul(hiplib, M, I, K):
 
 
 def test_tiled_split_k_is_deterministic_and_shares_the_workspace(hiplib):
-    """M = 96 on the 1536 x 8960 down projection: 12 tiles and 280 k-steps, so K is sliced; two calls agree
-    bitwise, also with skinny calls (which use the same workspace counters) in between."""
+    """M = 96 on the 1536 x 8960 down projection (64-row token blocks of the skinny kernel, K sliced); two
+    calls agree bitwise, also with skinny calls (which use the same workspace counters) in between."""
     from nanoserve_amd.kernels.linear import linear
     x, w = operands(96, 1536, 8960, seed=9)
     xd, wd = x.cuda(), w.cuda()
