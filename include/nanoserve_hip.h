@@ -77,6 +77,22 @@ int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
 size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype);
 
 /*
+ * ns_paged_attn_decode for decode rows scattered through a step's token rows (a mixed prefill + decode
+ * step: the gather q[0][decode_meta.token_idx] and index_copy_ of nanoserve/model.py:274-281): entry b reads its queries from
+ * row q_rows[b] of q and writes row q_rows[b] of out (int64, device memory, each a valid row of both), so
+ * the rows need no gather before and no scatter after. Everything else as ns_paged_attn_decode (block
+ * tables and context lengths per entry, same workspace).
+ */
+int ns_paged_attn_decode_rows(const void* q, int64_t q_sb, int64_t q_sh,
+                              const void* k_pool, const void* v_pool,
+                              int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                              const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                              const int64_t* q_rows, void* out, int64_t o_sb, int64_t o_sh,
+                              int B, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                              int max_blocks, int num_blocks, float scale, int dtype,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * ns_paged_attn_decode without the workspace argument, for callers that cannot allocate device memory
  * (code under hipGraph capture that must not call hipMalloc, tight serving loops, harnesses that forbid
  * allocation). No counterpart in the reference: nanoserve's Triton kernel needs no workspace.

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
     const bf16_t* __restrict__ vp, int64_t s_blk, int64_t s_pos, int64_t s_h, const int32_t* __restrict__ bt,
     int64_t bt_sb, const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G,
     int max_blocks, int num_blocks, float scale_log2, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    unsigned* __restrict__ ws_cnt, int B_, int nkv_, int n_parts) {
+    unsigned* __restrict__ ws_cnt, int B_, int nkv_, int n_parts, const int64_t* __restrict__ qrows) {
   constexpr int NW = DecodeCfg<HD>::NW, PPW = DecodeCfg<HD>::PPW, PART = NW * PPW;
   constexpr int KS = HD / 32;  // 32-dim k-steps of the QK^T product (8 bf16 per lane per step)
   constexpr int NT = HD / 16;  // 16-row output tiles of the PV product
@@ -104,6 +104,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
   const int part = L / rows;
   const int row = (L - part * rows + part) % rows;
   const int b = row / nkv_, g = row - (row / nkv_) * nkv_;
+  const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
   const int nkv = nkv_;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15;   // MFMA column (head) for B / D; MFMA row for A operands
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
   bf16x8_t qf[KS];  // B operand of S^T, k = dims 32s + 8*r4 + e; rows >= G zero
   {
     const bool hv = c16 < G;
-    const bf16_t* qrow = q + int64_t(b) * q_sb + int64_t(g * G + (hv ? c16 : 0)) * q_sh;
+    const bf16_t* qrow = q + qb * q_sb + int64_t(g * G + (hv ? c16 : 0)) * q_sh;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * r4);
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
   if (ctx <= 0) {  // no keys: zeros (the row is invalid; nothing to attend to)
     if (part == 0)
       for (int i = tid; i < G * HD; i += NW * 64)
-        out[int64_t(b) * o_sb + int64_t(g * G + i / HD) * o_sh + (i % HD)] = bf16_t(0);
+        out[qb * o_sb + int64_t(g * G + i / HD) * o_sh + (i % HD)] = bf16_t(0);
     return;
   }
   if (p0 >= n_pages) return;  // whole workgroup: this partition is past the row's context
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
       const int h = idx / (HD / 4), d4 = idx - h * (HD / 4);
       float M, L, A[4];
       part_state(h, d4, M, L, A);
-      bf16_t* o = out + int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + 4 * d4;
+      bf16_t* o = out + qb * o_sb + int64_t(g * G + h) * o_sh + 4 * d4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(A[e] / L);
     }
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
       }
     }
     const float inv = 1.0f / L;
-    bf16_t* o = out + int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + 4 * d4;
+    bf16_t* o = out + qb * o_sb + int64_t(g * G + h) * o_sh + 4 * d4;
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = f32_to_bf16(A[c] * inv);
   }
@@ -363,7 +364,8 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const bf16_t* __restrict__ vp, int64_t s_blk, const int32_t* __restrict__ bt, int64_t bt_sb,
     const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G, int nq,
     int max_blocks, int num_blocks, float scale_log2, unsigned* __restrict__ cnt, float* __restrict__ part_acc,
-    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h) {
+    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h,
+    const int64_t* __restrict__ qrows) {
   constexpr int pp = ROWK_PART;
   constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D;
   // A workgroup's token row: 128 elements (256 bytes) -- all KV heads of a token (nkv_grid == 1), or one
@@ -384,6 +386,7 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   const int L = blockIdx.x, part = L / R;
   const int row = (L - part * R + part) % R;
   const int b = row / nkv_grid, g = row - b * nkv_grid;
+  const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
   const int nq_w = nkv_grid > 1 ? G : nq;   // query heads of this workgroup: heads g G .. g G + nq_w - 1
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   const int gq = qlive ? c16 / G : NKV;   // KV head (within the token row) of this lane's query column
   bf16x8_t qf[KS];
   {
-    const bf16_t* qrow = q + int64_t(b) * q_sb + int64_t(g * G + (qlive ? c16 : 0)) * q_sh;
+    const bf16_t* qrow = q + qb * q_sb + int64_t(g * G + (qlive ? c16 : 0)) * q_sh;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       rk_u32x4_t u = *reinterpret_cast<const rk_u32x4_t*>(qrow + 32 * s + 8 * r4);
@@ -413,7 +416,7 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   if (ctx <= 0) {   // no keys: zeros
     if (part == 0)
       for (int i = tid; i < nq_w * HD; i += NW * 64)
-        out[int64_t(b) * o_sb + int64_t(g * G + i / HD) * o_sh + (i % HD)] = bf16_t(0);
+        out[qb * o_sb + int64_t(g * G + i / HD) * o_sh + (i % HD)] = bf16_t(0);
     return;
   }
   if (p0 >= n_pages) return;
@@ -580,7 +583,7 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
     const uint2 pk = make_uint2(uint32_t(f32_to_bf16(A[0] * inv)) | (uint32_t(f32_to_bf16(A[1] * inv)) << 16),
                                 uint32_t(f32_to_bf16(A[2] * inv)) | (uint32_t(f32_to_bf16(A[3] * inv)) << 16));
-    *reinterpret_cast<uint2*>(out + int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + 4 * d4) = pk;
+    *reinterpret_cast<uint2*>(out + qb * o_sb + int64_t(g * G + h) * o_sh + 4 * d4) = pk;
   };
   constexpr int ITEMS = (16 * (HD / 4) + NW * 64 - 1) / (NW * 64);
   const int n_items = nq_w * (HD / 4);
@@ -670,9 +673,10 @@ __global__ __launch_bounds__(64) void paged_decode_f32_kernel(
     const float* __restrict__ q, int64_t q_sb, int64_t q_sh, const float* __restrict__ kp,
     const float* __restrict__ vp, int64_t s_blk, int64_t s_pos, int64_t s_h, const int32_t* __restrict__ bt,
     int64_t bt_sb, const int32_t* __restrict__ ctxl, float* __restrict__ out, int64_t o_sb, int64_t o_sh, int G,
-    int max_blocks, int num_blocks, float scale) {
+    int max_blocks, int num_blocks, float scale, const int64_t* __restrict__ qrows) {
   constexpr int DL = HD / 64;  // dims per lane
   const int g = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
   const int ctx = ctxl[b];
   int n_pages = ctx > 0 ? (ctx + PAGE - 1) / PAGE : 0;
   if (n_pages > max_blocks) n_pages = max_blocks;
@@ -684,7 +688,7 @@ __global__ __launch_bounds__(64) void paged_decode_f32_kernel(
     l[h] = 0.f;
 #pragma unroll
     for (int e = 0; e < DL; ++e) {
-      qv[h][e] = h < G ? q[int64_t(b) * q_sb + int64_t(g * G + h) * q_sh + lane + 64 * e] : 0.f;
+      qv[h][e] = h < G ? q[qb * q_sb + int64_t(g * G + h) * q_sh + lane + 64 * e] : 0.f;
       acc[h][e] = 0.f;
     }
   }
@@ -720,7 +724,7 @@ __global__ __launch_bounds__(64) void paged_decode_f32_kernel(
     if (h < G)
 #pragma unroll
       for (int e = 0; e < DL; ++e)
-        out[int64_t(b) * o_sb + int64_t(g * G + h) * o_sh + lane + 64 * e] = n_tok > 0 ? acc[h][e] / l[h] : 0.f;
+        out[qb * o_sb + int64_t(g * G + h) * o_sh + lane + 64 * e] = n_tok > 0 ? acc[h][e] / l[h] : 0.f;
 }
 
 static inline int decode_parts(int head_dim, int max_blocks) {
@@ -777,7 +781,7 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
                                int64_t bt_sb, const int32_t* context_lens, void* out, int64_t o_sb, int64_t o_sh, int B,
                                int n_heads, int n_kv_heads, int head_dim, int block_size, int max_blocks,
                                int num_blocks, float scale, int dtype, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+                               void* stream, const int64_t* qrows = nullptr) {
   NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "paged_attention_decode: dtype %d not supported",
              dtype);
   NS_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention_decode: head_dim %d not in {64, 128}", head_dim);
@@ -797,12 +801,12 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
       hipLaunchKernelGGL(paged_decode_f32_kernel<64>, dim3(n_kv_heads, B), dim3(64), 0, s,
                          static_cast<const float*>(q), q_sb, q_sh, static_cast<const float*>(k_pool),
                          static_cast<const float*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
-                         static_cast<float*>(out), o_sb, o_sh, G, max_blocks, num_blocks, scale);
+                         static_cast<float*>(out), o_sb, o_sh, G, max_blocks, num_blocks, scale, qrows);
     else
       hipLaunchKernelGGL(paged_decode_f32_kernel<128>, dim3(n_kv_heads, B), dim3(64), 0, s,
                          static_cast<const float*>(q), q_sb, q_sh, static_cast<const float*>(k_pool),
                          static_cast<const float*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
-                         static_cast<float*>(out), o_sb, o_sh, G, max_blocks, num_blocks, scale);
+                         static_cast<float*>(out), o_sb, o_sh, G, max_blocks, num_blocks, scale, qrows);
     return check_launch("paged_attention_decode(f32)");
   }
   // bf16: 16-byte fragment loads need 8-element aligned strides and 16-byte aligned bases.
@@ -843,19 +847,19 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, rgh, kv_spos, kv_sh);
+                         rml, B, rparts, rgh, kv_spos, kv_sh, qrows);
     else if (head_dim == 64)
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh);
+                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows);
     else
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh);
+                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows);
     return check_launch("paged_attention_decode(bf16 rows)");
   }
   const int parts = decode_parts(head_dim, max_blocks);
@@ -887,14 +891,27 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
                        static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, ws_cnt, B,
-                       n_kv_heads, parts);
+                       n_kv_heads, parts, qrows);
   else
     hipLaunchKernelGGL(paged_decode_bf16_kernel<128>, grid, dim3(DecodeCfg<128>::NW * 64), 0, s,
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
                        static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, ws_cnt, B,
-                       n_kv_heads, parts);
+                       n_kv_heads, parts, qrows);
   return check_launch("paged_attention_decode(bf16)");
+}
+
+extern "C" int ns_paged_attn_decode_rows(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,
+                                         const void* v_pool, int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                                         const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                                         const int64_t* q_rows, void* out, int64_t o_sb, int64_t o_sh, int B,
+                                         int n_heads, int n_kv_heads, int head_dim, int block_size, int max_blocks,
+                                         int num_blocks, float scale, int dtype, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  NS_REQUIRE(q_rows != nullptr, "paged_attention_decode_rows: q_rows is NULL");
+  return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
+                             context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
+                             num_blocks, scale, dtype, workspace, workspace_bytes, stream, q_rows);
 }
 
 extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,

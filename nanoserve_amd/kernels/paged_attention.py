@@ -83,6 +83,37 @@ def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
     return out
 
 
+def paged_attention_decode_rows(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                                block_tables: torch.Tensor, context_lens: torch.Tensor, rows: torch.Tensor,
+                                scale: float, out: torch.Tensor) -> torch.Tensor:
+    """paged_attention_decode for entries whose query rows sit at `rows` (int64 [B], device) of q [N, nh, hd];
+    each entry's output goes to the same row of `out` [N, nh, hd] (other rows untouched). Replaces the gather
+    q[0][decode_meta.token_idx] and the index_copy_ of nanoserve/model.py:277-281."""
+    N, n_heads, head_dim = q.shape
+    B = rows.shape[0]
+    num_blocks, block_size, n_kv_heads, hd2 = k_pool.shape
+    assert hd2 == head_dim and q.dtype == k_pool.dtype == v_pool.dtype == out.dtype and out.shape == q.shape
+    assert q.stride(-1) == 1 and out.stride(-1) == 1 and k_pool.stride(-1) == 1 and v_pool.stride() == k_pool.stride()
+    assert v_pool.shape == k_pool.shape and rows.dtype == torch.int64 and rows.is_contiguous()
+    assert block_tables.dtype == torch.int32 and block_tables.dim() == 2 and block_tables.shape[0] == B
+    assert block_tables.stride(1) == 1 or block_tables.shape[1] == 1
+    assert context_lens.dtype == torch.int32 and context_lens.shape == (B,) and context_lens.is_contiguous()
+    _lib.require_gpu(q, k_pool, v_pool, block_tables, context_lens, rows, out)
+    if B == 0:
+        return out
+    max_blocks = block_tables.shape[1]
+    ws = decode_workspace(q.device, B, n_kv_heads, head_dim, max_blocks, q.dtype)
+    _lib.check(_lib.lib().ns_paged_attn_decode_rows(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), rows.data_ptr(),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, n_heads, n_kv_heads, head_dim, block_size, max_blocks, num_blocks, float(scale), _lib.dtype_code(q),
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _lib.stream_of(q)),
+        "paged_attention_decode_rows")
+    return out
+
+
 def prefill_seq_info(q_starts: list[int], n_new: list[int], ctx_lens: list[int], device) -> torch.Tensor:
     """int32 [S, 4] (q_start, n_new, ctx_len, 0) on `device`, from host lists."""
     rows = [[a, b, c, 0] for a, b, c in zip(q_starts, n_new, ctx_lens)]

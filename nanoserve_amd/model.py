@@ -278,7 +278,7 @@ class Qwen2Model:
         """Attention of layer i for the step's flattened tokens; q [1, N, nh, hd]. Returns [1, N, nh*hd]
         (written into `out` if given). Decode rows come from decode_meta; every other sequence's tokens are
         rows with causal-offset contexts (see the module docstring)."""
-        from nanoserve_amd.kernels.paged_attention import paged_attention_decode
+        from nanoserve_amd.kernels.paged_attention import paged_attention_decode, paged_attention_decode_rows
         if paged is None:
             raise ValueError("the HIP attention path reads the paged KV cache: pass `paged`")
         N, nh, hd = q.shape[1], q.shape[2], q.shape[3]
@@ -291,10 +291,10 @@ class Qwen2Model:
             out[0].copy_(o.view(N, nh * hd))
             return out
         o_all = out if out is not None else torch.empty(1, N, nh * hd, device=q.device, dtype=q.dtype)
-        if decode_meta is not None:
-            o_dec = paged_attention_decode(q[0][decode_meta.token_idx], paged.k[i], paged.v[i],
-                                           decode_meta.block_tables, decode_meta.context_lens, scale)
-            o_all[0].index_copy_(0, decode_meta.token_idx, o_dec.reshape(o_dec.shape[0], -1))
+        if decode_meta is not None:   # the decode rows' queries and outputs addressed in place
+            paged_attention_decode_rows(q[0], paged.k[i], paged.v[i], decode_meta.block_tables,
+                                        decode_meta.context_lens, decode_meta.token_idx, scale,
+                                        out=o_all[0].view(N, nh, hd))
         pre = self._prefill_meta(seqs, paged, slot_mapping, q.dtype)
         if pre is not None and pre[0] == "chunks":
             from nanoserve_amd.kernels.paged_attention import paged_attention_prefill

@@ -240,6 +240,35 @@ def test_graph_replay_matches_eager(hiplib):
         assert (got.float() - oracle).abs().max().item() <= 1e-2
 
 
+@pytest.mark.parametrize("dtype,n_heads,n_kv,hd,width", [(torch.bfloat16, 12, 2, 128, None),
+                                                          (torch.bfloat16, 14, 2, 64, None),
+                                                          (torch.bfloat16, 12, 2, 128, 1100),
+                                                          (torch.float32, 12, 2, 128, None)])
+def test_rows_entry_point_equals_gather_decode_scatter(hiplib, dtype, n_heads, n_kv, hd, width):
+    """ns_paged_attn_decode_rows (a mixed step's decode rows, nanoserve/model.py:274-281): entries read their
+    queries from rows `rows` of a larger q and write the same rows of out; the result equals decoding the
+    gathered rows, bitwise, and every other row of out keeps what it held (whole-row, per-head and fp32
+    kernels)."""
+    from nanoserve_amd.kernels.paged_attention import paged_attention_decode_rows
+    ctx = [1, 700, 2000, 17, 333, 64]
+    q, k, v, tables, lens = make_case(n_heads, n_kv, hd, ctx, dtype, seed=31, width=width)
+    g = cpu_gen(32)
+    N = 40
+    rows = torch.randperm(N, generator=g)[:len(ctx)]
+    qa = torch.randn(N, n_heads, hd, generator=g).to(dtype)
+    qa[rows] = q
+    sentinel = torch.full((N, n_heads, hd), 7.0, dtype=dtype)
+    out = sentinel.clone().cuda()
+    paged_attention_decode_rows(qa.cuda(), k.cuda(), v.cuda(), tables.cuda(), lens.cuda(), rows.cuda(), hd ** -0.5,
+                                out)
+    got = out.cpu()
+    ref = run(q, k, v, tables, lens, hd ** -0.5)
+    assert torch.equal(got[rows], ref)
+    others = torch.ones(N, dtype=torch.bool)
+    others[rows] = False
+    assert torch.equal(got[others], sentinel[others])
+
+
 def test_rejects_unsupported_shapes(hiplib):
     from nanoserve_amd.kernels.paged_attention import paged_attention_decode
     q, k, v, tables, lens = make_case(14, 2, 64, [20], torch.bfloat16)
