@@ -9,31 +9,36 @@
 // the decode kernel does (paged_attention.py:77).
 //
 // Design:
-//   * Work unit = (head, tile of QT = 64 queries, partition of the tile's keys). A workgroup is 4 waves;
-//     wave w owns queries 16w .. 16w+15, one per MFMA column. A tile's keys (64-key stages of 4 pages) are
-//     split into partitions of about PS stages, so a long prefill spreads over many workgroups instead
-//     of a few long ones; the grid axis runs over tiles from the last (longest) down.
+//   * Work unit = (head, tile of QT = 128 queries, partition of the tile's keys). A workgroup is 4 waves;
+//     wave w owns queries 32w .. 32w+31 as two 16-query MFMA tiles, so every K and V fragment it reads
+//     from LDS feeds two products. A tile's keys (64-key stages of 4 pages) are split into partitions of
+//     at most PS stages; the host picks PS so the whole launch fits the resident workgroup slots of the
+//     GPU (two per CU) in one round, with the fewest partitions that does.
 //   * K/V go straight from HBM into LDS (global_load_lds, 16 bytes per lane; wave w copies page w of a
-//     stage), double-buffered: the copy of stage n+1 runs while stage n is multiplied. Block ids come
-//     from a window of 64 table entries held one per lane and read with readlane. K rows are stored with
-//     XOR-swizzled 16-byte chunks so fragment reads are free of bank conflicts. Two workgroups fit a CU
-//     (64 KB of LDS each), two waves per SIMD, so one wave's softmax overlaps the other's products.
-//   * Per stage and wave, on the matrix cores (mfma 16x16x32 bf16 throughout):
-//       S^T[16 keys x 16 queries] = K_page[16 x hd] . Q^T[hd x 16]                      4 pages
-//       O^T[hd x 16 queries]    += V^T[hd x 32 keys] . P^T[32 keys x 16 queries]       2 key steps
+//     stage), double-buffered: the copy of stage n+1 runs while stage n is multiplied. The copies are
+//     inline asm with a scalar page base and per-lane 32-bit offsets fixed for the whole launch, so
+//     issuing one costs no vector arithmetic, and the compiler sees no LDS write in flight (it would
+//     otherwise wait for the whole next-stage copy before the current stage's first LDS read). Block ids
+//     come from a window of 64 table entries held one per lane and read with readlane. K rows are stored
+//     with XOR-swizzled 16-byte chunks so fragment reads are free of bank conflicts.
+//   * Per stage and wave, on the matrix cores (mfma 16x16x32 bf16 throughout), in two halves of 32 keys:
+//       S^T[16 keys x 16 queries] = K_page[16 x hd] . Q^T[hd x 16]         2 pages x 2 query tiles
+//       O^T[hd x 16 queries]    += V^T[hd x 32 keys] . P^T[32 keys x 16]   hd/16 tiles x 2 query tiles
 //     S^T comes out with lane = query and 4 consecutive keys per lane; two pages' worth is the 8-key
-//     B operand of P^T, so P never leaves registers. V^T fragments are built from LDS rows by a 4x4
-//     register transpose (v_perm), with the output rows relabelled so every LDS read is a contiguous
-//     row slice. The softmax reference point moves only when a score exceeds it by 2^8, so the
-//     accumulator is rescaled rarely.
+//     B operand of P^T, so P never leaves registers. V^T fragments come from LDS by transpose reads.
+//     The second half's scores are issued before the first half's softmax, so the matrix cores have
+//     work while the softmax runs. Row maxima over the four key groups of a query use the gfx950 lane
+//     swaps (v_permlane32_swap, v_permlane16_swap) instead of LDS shuffles. The softmax reference point
+//     moves only when a score exceeds it by 2^8, so the accumulator is rescaled rarely.
 //   * Masks are computed only on stages that cross a query's diagonal or the end of the keys: key k is
 //     visible to query j iff k <= ctx + j, and keys at or past ctx + T (unwritten slots of the last
 //     page, pages past the tile's reach) are zeroed in V as well, so garbage there can never turn 0 * x
 //     into NaN. Block ids outside [0, num_blocks) are masked pages.
 //   * A tile split over several partitions: each partition publishes its (m, l, acc) with agent-scope
 //     stores, waits for them to complete and bumps the tile's arrival counter; the last to arrive merges
-//     all partitions in partition order (the result does not depend on arrival order) and writes the
-//     output. One launch; the workspace counters are left at zero.
+//     all partitions in partition order (its own from registers, the others loaded PF_MB per round trip;
+//     the result does not depend on arrival order) and writes the output. One launch; the workspace
+//     counters are left at zero.
 #include "ns_common.h"
 
 #include <algorithm>
@@ -51,13 +56,16 @@ constexpr float PF_LOG2E = 1.4426950408889634f;
 constexpr int PF_PAGE = 16;
 constexpr int PF_NP = 4;                    // pages per stage
 constexpr int PF_KEYS = PF_NP * PF_PAGE;    // 64 keys per stage
-constexpr int PF_WAVES = 4;
+constexpr int PF_WAVES = 4;                 // waves of one group (one key range of a tile's queries)
 constexpr int PF_THREADS = PF_WAVES * 64;
-constexpr int PF_R = 1;                     // 16-query MFMA tiles per wave (2 halves the LDS reads per
-                                            // product but needs 2x the registers: one wave per SIMD)
+constexpr int PF_GROUPS = 2;                // groups per workgroup: two key ranges of the same queries
+constexpr int PF_WG_THREADS = PF_GROUPS * PF_THREADS;
+constexpr int PF_R = 2;                     // 16-query MFMA tiles per wave
 constexpr int PF_QT = 16 * PF_R * PF_WAVES; // queries per work unit
-constexpr int PF_PS = 8;                    // target stages per partition
-constexpr int PF_MB = 4;                    // partitions merged per memory round trip
+constexpr int PF_PS_MIN = 4;                // fewest stages per partition the plan picks
+constexpr int PF_SLOTS = 248;               // workgroups per launch the plan aims below: one resident per
+                                            // CU (128 KB of LDS) on the 256 CUs (32 per XCD), less a margin
+constexpr int PF_MB = 3;                    // partitions loaded per round trip of the merge
 constexpr float PF_SLACK = 8.0f;            // log2 headroom of the softmax reference point
 
 template <int HD>
@@ -78,9 +86,6 @@ struct PfLds {
 };
 static_assert(PF_NP == PF_WAVES, "each wave stages one page of a stage");
 
-__device__ __forceinline__ uint32_t pf_pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
-__device__ __forceinline__ uint32_t pf_pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
-
 // two fp32 -> packed bf16 (round to nearest even; v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pf_bf16x2(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
@@ -88,6 +93,35 @@ __device__ __forceinline__ uint32_t pf_bf16x2(float lo, float hi) {
   r[0] = static_cast<__bf16>(lo);
   r[1] = static_cast<__bf16>(hi);
   return __builtin_bit_cast(uint32_t, r);
+}
+
+// Maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four key groups of one S^T column), by the gfx950 lane
+// swaps: permlane32_swap of a register with itself leaves lanes l and l ^ 32 in the two results, and
+// permlane16_swap does the same for l and l ^ 16. Every lane of the four gets the same value.
+__device__ __forceinline__ float pf_max4(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+// The same four lanes' sum, (x_l + x_l^32) + (x_l^16 + x_l^48) in an order every lane of the four shares.
+__device__ __forceinline__ float pf_sum4(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// One wave-wide HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4; lane i fills lds + 16 i) from
+// base + off: base is wave-uniform (scalar registers), off the lane's byte offset. Inline asm, so the
+// compiler sees no LDS write in flight and puts no wait for it in front of the current stage's LDS reads;
+// the stage loop's explicit vmcnt(0) and barrier are the only wait the copies need. M0 holds the
+// wave-uniform LDS address; s_nop 0 is the wait state an LDS-DMA load needs after M0 is written.
+__device__ __forceinline__ void pf_dma16(const char* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ uint32_t pf_lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
 
 struct PrefillArgs {
@@ -101,43 +135,66 @@ struct PrefillArgs {
   const int32_t* info;              // [S, 4]: q_start, n_new, ctx_len, unused
   bf16_t* out;
   int64_t o_st, o_sh;
-  int G, max_blocks, num_blocks, n_heads;
+  int G, max_blocks, num_blocks, n_heads, n_seqs;
   float scale_log2;
-  int tiles_max, parts_max;
+  int tiles_max, parts_max, ps;     // query tiles, partitions per tile (grid), target stages per partition
   unsigned* cnt;                    // [S, n_heads, tiles_max] arrival counters (zero between calls)
-  float* ws_ml;                     // [unit][R][256 threads] (m, l)
-  float* ws_acc;                    // [unit][R * NT][256 threads] float4
+  float* ws_ml;                     // [unit][R][2][256 threads] (m, l)
+  float* ws_acc;                    // [unit][R][NT][256 threads] float4
 };
 
 template <int HD>
-__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_prefill_bf16_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_prefill_bf16_kernel(PrefillArgs a) {
   using L = PfLds<HD>;
   constexpr int KS = HD / 32;   // k-steps of Q.K^T
   constexpr int NT = HD / 16;   // output tiles of P.V
-  constexpr int VW = NT / 2;    // dwords of a lane's V row slice
-  __shared__ __align__(16) unsigned char lds_a[L::STAGE];   // stages st0, st0 + 2, ...
-  __shared__ __align__(16) unsigned char lds_b[L::STAGE];   // stages st0 + 1, st0 + 3, ...
+  // per group, stage st0 + i in buffer i % 2; after the loop the same bytes carry group 1's state to group 0
+  __shared__ __align__(16) unsigned char lds[PF_GROUPS * 2 * L::STAGE];
   __shared__ unsigned s_last;
 
-  const int h = blockIdx.x, seq = blockIdx.z;
-  const int tile_rev = int(blockIdx.y) / a.parts_max, part = int(blockIdx.y) - tile_rev * a.parts_max;
+  // ---- this workgroup's work unit. The launch's units -- sequence by sequence, a sequence's query tiles
+  // from the last (longest) down, a tile's workgroups, then heads -- are numbered from 0, so the busy
+  // workgroups are the first of the grid and spread evenly over the XCDs (workgroup i runs on XCD i % 8);
+  // the grid is an upper bound and the rest exit at once. A tile's keys split into 2 n_parts key ranges
+  // of at most ps stages; workgroup `part` of the tile takes ranges 2 part (group 0) and 2 part + 1
+  // (group 1). A sequence with more new tokens than the caller's max_new is not computed.
+  int rem = int(blockIdx.x), seq = -1, tile = 0, part = 0, h = 0, n_st = 0, n_parts = 0, n_pages = 0;
+  for (int sq = 0; sq < a.n_seqs && seq < 0; ++sq) {
+    const int Tq = a.info[4 * sq + 1], cq = a.info[4 * sq + 2];
+    const int nt = (Tq + PF_QT - 1) / PF_QT;
+    if (Tq <= 0 || nt > a.tiles_max) continue;
+    for (int tr = 0; tr < nt; ++tr) {
+      const int tl = nt - 1 - tr;
+      const int np = min((cq + min(PF_QT * (tl + 1), Tq) + PF_PAGE - 1) / PF_PAGE, a.max_blocks);
+      const int ns = (np + PF_NP - 1) / PF_NP;
+      const int npt = min((ns + 2 * a.ps - 1) / (2 * a.ps), a.parts_max);
+      if (rem < npt * a.n_heads) {
+        seq = sq;
+        tile = tl;
+        part = rem / a.n_heads;
+        h = rem - part * a.n_heads;
+        n_st = ns;
+        n_parts = npt;
+        n_pages = np;
+        break;
+      }
+      rem -= npt * a.n_heads;
+    }
+  }
+  if (seq < 0) return;
   const int q_start = a.info[4 * seq + 0], T = a.info[4 * seq + 1], ctx = a.info[4 * seq + 2];
-  const int n_tiles = (T + PF_QT - 1) / PF_QT;
-  if (tile_rev >= n_tiles || n_tiles > a.tiles_max) return;   // the second: n_new above the caller's max_new
-  const int tile = n_tiles - 1 - tile_rev;
   const int qbase = tile * PF_QT;
-  const int j_last_wg = min(qbase + PF_QT - 1, T - 1);
-  const int kv_end = ctx + j_last_wg + 1;   // keys this tile can see
   const int kv_total = ctx + T;             // keys that exist
-  int n_pages = (kv_end + PF_PAGE - 1) / PF_PAGE;
-  if (n_pages > a.max_blocks) n_pages = a.max_blocks;
-  const int n_st = (n_pages + PF_NP - 1) / PF_NP;
-  const int n_parts = min((n_st + PF_PS - 1) / PF_PS, a.parts_max);
-  if (part >= n_parts) return;
-  const int st0 = part * n_st / n_parts, st1 = (part + 1) * n_st / n_parts;
+  const int n_sub = 2 * n_parts;
+  const int tid_wg = threadIdx.x, gi = tid_wg >> 8;   // group
+  const int sub = 2 * part + gi;
+  const int st0 = sub * n_st / n_sub, st1 = (sub + 1) * n_st / n_sub;
+  // both groups run the same number of stage-loop iterations (their barriers are the workgroup's)
+  const int n_iter = max(((2 * part + 1) * n_st / n_sub) - (2 * part * n_st / n_sub),
+                         ((2 * part + 2) * n_st / n_sub) - ((2 * part + 1) * n_st / n_sub));
   const int g = h / a.G;
   const int32_t* table = a.bt + int64_t(seq) * a.bt_sb;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = tid_wg & (PF_THREADS - 1), lane = tid & 63, w = tid >> 6;   // thread and wave in the group
   const int c16 = lane & 15, r4 = lane >> 4;
 
   // this lane's queries (rows past T mirror row T-1 and are not stored)
@@ -169,20 +226,25 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
   };
   // validity bits of stage n's 4 pages (n inside the current window)
   auto stage_ok = [&](int n) __attribute__((always_inline)) { return unsigned(pok >> (PF_NP * (n - win0))) & 0xFu; };
-  auto dma_stage = [&](int n, unsigned char* buf) __attribute__((always_inline)) {
+  unsigned char* glds = lds + gi * (2 * L::STAGE);   // this group's two stage buffers
+  const uint32_t lds0 = pf_lds_addr(glds);
+  const uint32_t spos2 = uint32_t(a.s_pos) * 2u;   // token stride in bytes (checked < 2^26 by the host)
+  auto dma_stage = [&](int n, int buf) __attribute__((always_inline)) {
     const int id = __builtin_amdgcn_readlane(pid, PF_NP * (n - win0) + w);
-    const int64_t base = int64_t(id) * a.s_blk + int64_t(g) * a.s_h;
-    unsigned char* kd = buf + w * (PF_PAGE * L::ROW);
-    unsigned char* vd = kd + L::K_BYTES;
+    const int64_t base = (int64_t(id) * a.s_blk + int64_t(g) * a.s_h) * 2;
+    const char* kb = reinterpret_cast<const char*>(a.kp) + base;
+    const char* vb = reinterpret_cast<const char*>(a.vp) + base;
+    const uint32_t kd = __builtin_amdgcn_readfirstlane(lds0 + uint32_t(buf * L::STAGE + w * (PF_PAGE * L::ROW)));
+    // Load i fills LDS slot (token row t, chunk cp) with the token's chunk cp ^ key(t) (K) or cp ^ vkey(t)
+    // (V). The lane's byte offsets are the same for every page; they are recomputed here from an opaque
+    // copy of the lane index rather than kept in registers across the stage loop.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int i = 0; i < L::IPP; ++i) {
-      const int t = L::TPI * i + lane / L::CH, cp = lane % L::CH;   // the LDS slot this lane fills
-      const int64_t row = base + int64_t(t) * a.s_pos;
-      __builtin_amdgcn_global_load_lds(
-          (__attribute__((address_space(1))) void*)(a.kp + row + 8 * (cp ^ L::key(t))),
-          (__attribute__((address_space(3))) void*)(kd + 1024 * i), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(a.vp + row + 8 * (cp ^ L::vkey(t))),
-                                       (__attribute__((address_space(3))) void*)(vd + 1024 * i), 16, 0, 0);
+      const int t = L::TPI * i + ln / L::CH, cp = ln % L::CH;
+      pf_dma16(kb, uint32_t(t) * spos2 + 16u * uint32_t(cp ^ L::key(t)), kd + 1024 * i);
+      pf_dma16(vb, uint32_t(t) * spos2 + 16u * uint32_t(cp ^ L::vkey(t)), kd + L::K_BYTES + 1024 * i);
     }
   };
 
@@ -196,48 +258,61 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int t = 0; t < NT; ++t) acc[rt][t] = pf_float4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  // One stage on the matrix cores. MASK: the stage crosses a diagonal or the end of the keys, or holds a
-  // bad block id; otherwise every key is visible to every query of the wave.
+  // One stage: S^T for all 64 keys (both halves of 32 keys: pages 2 hs, 2 hs + 1), one softmax update
+  // per query tile over the whole stage, then P and O^T += V^T . P^T half by half, with the second half's
+  // probabilities computed while the first half's products run. MASK: the stage crosses a diagonal or the
+  // end of the keys, or holds a bad block id; otherwise every key is visible to every query of the wave.
+  // (Every array lives inside this one function: passed by reference between helpers, the compiler kept
+  // some of them in scratch memory.)
   auto compute = [&](const unsigned char* st, int kb0, unsigned okm, auto mask_c) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_c)::value;
-    bool okp[PF_NP];
+    pf_float4_t sc[2][PF_R][2];   // [half][query tile][page of the half]
+    pf_bf16x8_t kf[2][KS];
 #pragma unroll
-    for (int pp = 0; pp < PF_NP; ++pp) okp[pp] = MASK ? ((okm >> pp) & 1u) != 0 : true;
-    // ---- scores of both query tiles, page by page (each K fragment read once, used twice)
-    pf_float4_t sc[PF_R][PF_NP];
+    for (int hs = 0; hs < 2; ++hs) {
+      // ---- K fragments of the half (A operands of S^T: lane (c16, r4) holds key c16 of the page, dims
+      // 32 s + 8 r4 .. +7), then S^T for both query tiles, the k-step loop outermost so consecutive MFMAs
+      // accumulate into different tiles
 #pragma unroll
-    for (int pp = 0; pp < PF_NP; ++pp) {
-      const unsigned char* krow = st + (PF_PAGE * pp + c16) * L::ROW;
-      const int kk = L::key(c16);
-      pf_bf16x8_t kf[KS];
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        kf[s] = __builtin_bit_cast(pf_bf16x8_t, *reinterpret_cast<const uint4*>(krow + 16 * ((4 * s + r4) ^ kk)));
-#pragma unroll
-      for (int rt = 0; rt < PF_R; ++rt) {
-        sc[rt][pp] = pf_float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int hp = 0; hp < 2; ++hp) {
+        const unsigned char* krow = st + (PF_PAGE * (2 * hs + hp) + c16) * L::ROW;
+        const int kk = L::key(c16);
 #pragma unroll
         for (int s = 0; s < KS; ++s)
-          sc[rt][pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s], qf[rt][s], sc[rt][pp], 0, 0, 0);
+          kf[hp][s] = __builtin_bit_cast(pf_bf16x8_t, *reinterpret_cast<const uint4*>(krow + 16 * ((4 * s + r4) ^ kk)));
       }
+#pragma unroll
+      for (int rt = 0; rt < PF_R; ++rt)
+#pragma unroll
+        for (int hp = 0; hp < 2; ++hp) sc[hs][rt][hp] = pf_float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int hp = 0; hp < 2; ++hp)
+#pragma unroll
+          for (int rt = 0; rt < PF_R; ++rt)
+            sc[hs][rt][hp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[hp][s], qf[rt][s], sc[hs][rt][hp], 0, 0, 0);
     }
-    // ---- probabilities: P^T as B operands, k-slot e = key 4*r4 + e of each page
-    uint32_t pb[PF_R][PF_NP][2];
+    // ---- softmax statistics over the stage: masked scores -> -inf, the stage maximum per query, the
+    // reference point and the rescale factor
+    float mc[PF_R];
 #pragma unroll
     for (int rt = 0; rt < PF_R; ++rt) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int pp = 0; pp < PF_NP; ++pp)
+      for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (MASK) {
-            const int key = kb0 + PF_PAGE * pp + 4 * r4 + e;
-            if (!(okp[pp] && key <= ctx + jrow[rt])) sc[rt][pp][e] = -INFINITY;
+        for (int hp = 0; hp < 2; ++hp)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (MASK) {
+              const int pp = 2 * hs + hp;
+              const int key = kb0 + PF_PAGE * pp + 4 * r4 + e;
+              if (!(((okm >> pp) & 1u) != 0 && key <= ctx + jrow[rt])) sc[hs][rt][hp][e] = -INFINITY;
+            }
+            mx = fmaxf(mx, sc[hs][rt][hp][e]);
           }
-          mx = fmaxf(mx, sc[rt][pp][e]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = pf_max4(mx);
       // Reference point m (scaled units, c = scale * log2(e)): weights are exp2(s * c - m). It moves
       // only when a score exceeds it by more than PF_SLACK, so weights stay below 2^PF_SLACK and the
       // accumulator is rescaled rarely. The normalised result is the same function of the scores; only
@@ -245,44 +320,32 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
       const float mxc = mx * a.scale_log2;
       const bool move = mxc > m_run[rt] + PF_SLACK;
       const float m_new = move ? mxc : m_run[rt];
-      const float mc = m_new == -INFINITY ? 0.f : m_new;   // nothing visible yet: weights 0
-      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - mc);
+      mc[rt] = m_new == -INFINITY ? 0.f : m_new;   // nothing visible yet: weights 0
+      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - mc[rt]);
       m_run[rt] = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int pp = 0; pp < PF_NP; ++pp) {
-        float pv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[rt][pp][e], a.scale_log2, -mc));
-          psum += pv[e];
-        }
-        pb[rt][pp][0] = pf_bf16x2(pv[0], pv[1]);
-        pb[rt][pp][1] = pf_bf16x2(pv[2], pv[3]);
-      }
-      l_run[rt] = l_run[rt] * alpha + psum;
+      l_run[rt] *= alpha;
       if (__ballot(move)) {   // the reference point moved for some query of the wave
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[rt][t] *= alpha;
       }
     }
-    // ---- P.V over two 32-key steps: k-slots 0..3 = page 2*ks2 keys 4*r4 + e, 4..7 = page 2*ks2 + 1.
-    // V^T fragments come straight from LDS by transpose reads (ds_read_b64_tr_b16): within each group of
-    // 16 lanes, lane j addresses 4 dims (16t + 4 (j % 4) ..) of key row kb + j / 4, and lane i receives
-    // dim 16t + i of keys kb .. kb + 3 -- its A-operand slots for one page. Built once per step, they feed
-    // every query tile.
+    // ---- per half: V^T fragments by transpose reads (ds_read_b64_tr_b16): within each group of 16 lanes,
+    // lane j addresses 4 dims (16t + 4 (j % 4) ..) of key row kb + j / 4, and lane i receives dim 16t + i
+    // of keys kb .. kb + 3 -- its A-operand slots for one page; k-slots 0..3 = page 2 hs keys 4 r4 + e,
+    // 4..7 = page 2 hs + 1 (MASK: keys that do not exist, past ctx + T or on a bad page, read as 0).
+    // Probabilities P^T (B operands, k-slot e = key 4 r4 + e of each page), then O^T += V^T . P^T.
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
+    for (int hs = 0; hs < 2; ++hs) {
       v4i16_t va[2][NT];
 #pragma unroll
       for (int hp = 0; hp < 2; ++hp) {
-        const int pp = 2 * ks2 + hp;
+        const int pp = 2 * hs + hp;
         const int vr = PF_PAGE * pp + 4 * r4 + (c16 >> 2);   // the key row this lane addresses
         const unsigned char* vrow = st + L::K_BYTES + vr * L::ROW;
         uint32_t m01 = 0xffffffffu, m23 = 0xffffffffu;
-        if constexpr (MASK) {   // keys that do not exist read as 0
+        if constexpr (MASK) {
           const int key0 = kb0 + PF_PAGE * pp + 4 * r4;
-          const bool ok = okp[pp];
+          const bool ok = ((okm >> pp) & 1u) != 0;
           m01 = (ok && key0 + 0 < kv_total ? 0x0000ffffu : 0u) | (ok && key0 + 1 < kv_total ? 0xffff0000u : 0u);
           m23 = (ok && key0 + 2 < kv_total ? 0x0000ffffu : 0u) | (ok && key0 + 3 < kv_total ? 0xffff0000u : 0u);
         }
@@ -303,8 +366,21 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
       }
 #pragma unroll
       for (int rt = 0; rt < PF_R; ++rt) {
-        const pf_bf16x8_t pbv = __builtin_bit_cast(
-            pf_bf16x8_t, make_uint4(pb[rt][2 * ks2][0], pb[rt][2 * ks2][1], pb[rt][2 * ks2 + 1][0], pb[rt][2 * ks2 + 1][1]));
+        float psum = 0.f;
+        uint32_t pb[4];
+#pragma unroll
+        for (int hp = 0; hp < 2; ++hp) {
+          float pv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[hs][rt][hp][e], a.scale_log2, -mc[rt]));
+            psum += pv[e];
+          }
+          pb[2 * hp + 0] = pf_bf16x2(pv[0], pv[1]);
+          pb[2 * hp + 1] = pf_bf16x2(pv[2], pv[3]);
+        }
+        l_run[rt] += psum;
+        const pf_bf16x8_t pbv = __builtin_bit_cast(pf_bf16x8_t, make_uint4(pb[0], pb[1], pb[2], pb[3]));
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const uint2 lo = __builtin_bit_cast(uint2, va[0][t]), hi = __builtin_bit_cast(uint2, va[1][t]);
@@ -325,7 +401,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         compute(st, kb0, okm, std::true_type{});
     }
   };
-  auto issue = [&](int n, unsigned char* buf) __attribute__((always_inline)) {
+  auto issue = [&](int n, int buf) __attribute__((always_inline)) {
     unsigned okm = 0;
     if (n < st1) {
       if (n - win0 >= 16) load_window(n);
@@ -336,26 +412,54 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
   };
   // The copy of stage n+1 runs while stage n is multiplied; the barrier before a stage makes every wave's
   // copies of it visible and frees the other buffer. A window of 16 stages of block ids is refreshed
-  // between stages.
+  // between stages. A group whose key range is shorter idles through the last iteration.
   load_window(st0);
-  unsigned ok_a = issue(st0, lds_a), ok_b = 0;
-  for (int n = st0; n < st1; n += 2) {
+  unsigned ok_cur = issue(st0, 0);
+  for (int i = 0; i < n_iter; ++i) {
+    const int n = st0 + i;
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    ok_b = issue(n + 1, lds_b);
-    run_stage(n, lds_a, ok_a);
-    if (n + 1 >= st1) break;
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
-    ok_a = issue(n + 2, lds_a);
-    run_stage(n + 1, lds_b, ok_b);
+    const int buf = i & 1;
+    const unsigned ok_next = issue(n + 1, buf ^ 1);
+    if (n < st1) run_stage(n, glds + buf * L::STAGE, ok_cur);
+    ok_cur = ok_next;
   }
-  __syncthreads();
 
 #pragma unroll
-  for (int rt = 0; rt < PF_R; ++rt) {
-    l_run[rt] += __shfl_xor(l_run[rt], 16, 64);
-    l_run[rt] += __shfl_xor(l_run[rt], 32, 64);
+  for (int rt = 0; rt < PF_R; ++rt) l_run[rt] = pf_sum4(l_run[rt]);
+  // ---- the two groups' states meet in LDS: group 1 stores (m, l, acc) of each lane, group 0 folds them
+  // after its own (range order) -- the same running fold as across workgroups below
+  {
+    __syncthreads();   // every wave is done with the stage buffers
+    float* xml = reinterpret_cast<float*>(lds);                       // [rt][2][256 threads]
+    pf_float4_t* xacc = reinterpret_cast<pf_float4_t*>(lds + 8192);   // [rt][NT][256 threads]
+    if (gi == 1) {
+#pragma unroll
+      for (int rt = 0; rt < PF_R; ++rt) {
+        xml[(2 * rt) * PF_THREADS + tid] = m_run[rt];
+        xml[(2 * rt + 1) * PF_THREADS + tid] = l_run[rt];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) xacc[(rt * NT + t) * PF_THREADS + tid] = acc[rt][t];
+      }
+    }
+    __syncthreads();
+    if (gi == 0) {
+#pragma unroll
+      for (int rt = 0; rt < PF_R; ++rt) {
+        const float mb = xml[(2 * rt) * PF_THREADS + tid], lb = xml[(2 * rt + 1) * PF_THREADS + tid];
+        const float Mn = fmaxf(m_run[rt], mb);
+        const float a_old = m_run[rt] == -INFINITY ? 0.f : exp2f(m_run[rt] - Mn);
+        const float a_new = mb == -INFINITY ? 0.f : exp2f(mb - Mn);
+        l_run[rt] = l_run[rt] * a_old + lb * a_new;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const pf_float4_t v = xacc[(rt * NT + t) * PF_THREADS + tid];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[rt][t][c] = acc[rt][t][c] * a_old + v[c] * a_new;
+        }
+        m_run[rt] = Mn;
+      }
+    }
   }
   // lane holds, for query tile rt, tile t and r = 0..3, query c16 at dim 16 t + 4 r4 + r
   auto write_out = [&](int rt, const pf_float4_t (&o)[NT], float inv) __attribute__((always_inline)) {
@@ -367,37 +471,82 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
           make_uint2(pf_bf16x2(o[t][0] * inv, o[t][1] * inv), pf_bf16x2(o[t][2] * inv, o[t][3] * inv));
   };
   if (n_parts == 1) {
+    if (gi == 0) {
 #pragma unroll
-    for (int rt = 0; rt < PF_R; ++rt) write_out(rt, acc[rt], 1.0f / l_run[rt]);
+      for (int rt = 0; rt < PF_R; ++rt) write_out(rt, acc[rt], 1.0f / l_run[rt]);
+    }
     return;
   }
 
   // ---- several partitions: publish, count, and the last to arrive merges in partition order
   const int64_t tile_id = (int64_t(seq) * a.n_heads + h) * a.tiles_max + tile;
   const int64_t unit0 = tile_id * a.parts_max;
+  auto ml_of = [&](int x, int rt) __attribute__((always_inline)) {
+    return a.ws_ml + ((unit0 + x) * PF_R + rt) * (2 * PF_THREADS);
+  };
+  auto acc_of = [&](int x, int rt, int t) __attribute__((always_inline)) {
+    return a.ws_acc + (((unit0 + x) * PF_R + rt) * NT + t) * (4 * PF_THREADS) + 4 * tid;
+  };
+  if (gi == 0) {   // group 0 holds the workgroup's state; group 1 only meets the barriers
 #pragma unroll
   for (int rt = 0; rt < PF_R; ++rt) {
-    float* ml = a.ws_ml + ((unit0 + part) * PF_R + rt) * (2 * PF_THREADS);
-    publish_store(ml + tid, m_run[rt]);
-    publish_store(ml + PF_THREADS + tid, l_run[rt]);
+    publish_store(ml_of(part, rt) + tid, m_run[rt]);
+    publish_store(ml_of(part, rt) + PF_THREADS + tid, l_run[rt]);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const pub_u32x4_t bits = {__float_as_uint(acc[rt][t][0]), __float_as_uint(acc[rt][t][1]),
                                 __float_as_uint(acc[rt][t][2]), __float_as_uint(acc[rt][t][3])};
-      publish_store16(a.ws_acc + (((unit0 + part) * PF_R + rt) * NT + t) * (4 * PF_THREADS) + 4 * tid, bits);
+      publish_store16(acc_of(part, rt, t), bits);
     }
+  }
   }
   publish_complete();
   __syncthreads();
-  if (tid == 0) {
+  if (tid_wg == 0) {
     const unsigned prev = publish_count(a.cnt + tile_id);
     const unsigned last = prev == unsigned(n_parts - 1);
     if (last) publish_reset(a.cnt + tile_id);
     s_last = last;
   }
   __syncthreads();
-  if (s_last == 0u) return;
+  if (s_last == 0u || gi != 0) return;
   acquire_published();
+  if (n_parts == 2) {
+    // Two partitions (what the plan gives the longest tiles): the other one's state is loaded in one round
+    // trip and combined with this one's, kept in registers. The expression takes the partitions in order
+    // (p0 a0 + p1 a1), so the bits do not depend on which of the two merges.
+    const int other = part ^ 1;
+    float pm[PF_R], pl[PF_R];
+    pub_u32x4_t u[PF_R][NT];
+#pragma unroll
+    for (int rt = 0; rt < PF_R; ++rt) {
+      pm[rt] = publish_load(ml_of(other, rt) + tid);
+      pl[rt] = publish_load(ml_of(other, rt) + PF_THREADS + tid);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) u[rt][t] = publish_load16(acc_of(other, rt, t));
+    }
+#pragma unroll
+    for (int rt = 0; rt < PF_R; ++rt) {
+      const float m0 = part == 0 ? m_run[rt] : pm[rt], m1 = part == 0 ? pm[rt] : m_run[rt];
+      const float l0 = part == 0 ? l_run[rt] : pl[rt], l1 = part == 0 ? pl[rt] : l_run[rt];
+      const float Mx = fmaxf(m0, m1);
+      const float a0 = m0 == -INFINITY ? 0.f : exp2f(m0 - Mx), a1 = m1 == -INFINITY ? 0.f : exp2f(m1 - Mx);
+      const float Ls = l0 * a0 + l1 * a1;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float v = __uint_as_float(u[rt][t][c]);
+          const float x0 = part == 0 ? acc[rt][t][c] : v, x1 = part == 0 ? v : acc[rt][t][c];
+          acc[rt][t][c] = x0 * a0 + x1 * a1;
+        }
+      write_out(rt, acc[rt], 1.0f / Ls);
+    }
+    return;
+  }
+  // More partitions: fold them in partition order with a running maximum (the result does not depend on
+  // which partition merges), PF_MB per round trip; the own partition is read back like the others, so the
+  // accumulators are free for the loads.
 #pragma unroll
   for (int rt = 0; rt < PF_R; ++rt) {
     float M = -INFINITY, Lsum = 0.f;
@@ -405,17 +554,15 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
     for (int t = 0; t < NT; ++t) O[t] = pf_float4_t{0.f, 0.f, 0.f, 0.f};
     for (int x0 = 0; x0 < n_parts; x0 += PF_MB) {
-      pub_u32x4_t u[PF_MB * NT];
+      pub_u32x4_t u[PF_MB][NT];
       float pm[PF_MB], pl[PF_MB];
 #pragma unroll
       for (int e = 0; e < PF_MB; ++e) {
-        const int x = min(x0 + e, n_parts - 1);
-        const float* ml = a.ws_ml + ((unit0 + x) * PF_R + rt) * (2 * PF_THREADS);
-        pm[e] = publish_load(ml + tid);
-        pl[e] = publish_load(ml + PF_THREADS + tid);
+        const int x = min(x0 + e, n_parts - 1);   // slots past the end re-load the last partition (unused)
+        pm[e] = publish_load(ml_of(x, rt) + tid);
+        pl[e] = publish_load(ml_of(x, rt) + PF_THREADS + tid);
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-          u[e * NT + t] = publish_load16(a.ws_acc + (((unit0 + x) * PF_R + rt) * NT + t) * (4 * PF_THREADS) + 4 * tid);
+        for (int t = 0; t < NT; ++t) u[e][t] = publish_load16(acc_of(x, rt, t));
       }
 #pragma unroll
       for (int e = 0; e < PF_MB; ++e) {
@@ -427,7 +574,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
           for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) O[t][c] = O[t][c] * a_old + __uint_as_float(u[e * NT + t][c]) * a_new;
+            for (int c = 0; c < 4; ++c) O[t][c] = O[t][c] * a_old + __uint_as_float(u[e][t][c]) * a_new;
           M = Mn;
         }
       }
@@ -436,12 +583,37 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
   }
 }
 
-int prefill_parts_max(int max_kv) {
-  const int n_st = ((max_kv + PF_PAGE - 1) / PF_PAGE + PF_NP - 1) / PF_NP;
-  return std::max(1, (n_st + PF_PS - 1) / PF_PS);
-}
-
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Partition plan: ps, the most stages one group's key range may hold, and parts, the workgroups per tile (the
+// grid's and the workspace's stride; a workgroup takes two key ranges). ps is the smallest value >=
+// PF_PS_MIN whose workgroup count -- every tile of n_seqs sequences with max_new new tokens on
+// max_kv - max_new cached ones, split into ceil(stages / (2 ps)) workgroups -- stays within PF_SLOTS; with
+// none, one workgroup per tile. A function of the arguments only, so the workspace query and the launch
+// agree.
+struct PfPlan {
+  int ps, parts, tiles;
+};
+PfPlan prefill_plan(int n_seqs, int n_heads, int max_new, int max_kv) {
+  const int tiles = (max_new + PF_QT - 1) / PF_QT;
+  const int ctx = std::max(0, max_kv - max_new);
+  auto stages = [&](int kv) { return ((kv + PF_PAGE - 1) / PF_PAGE + PF_NP - 1) / PF_NP; };
+  const int n_st_max = std::max(1, stages(max_kv));
+  auto wgs = [&](int ps) {
+    int64_t n = 0;
+    for (int t = 0; t < tiles; ++t) n += (stages(ctx + std::min(PF_QT * (t + 1), max_new)) + 2 * ps - 1) / (2 * ps);
+    return n * n_seqs * n_heads;
+  };
+  int lo = std::min(PF_PS_MIN, n_st_max), hi = n_st_max;
+  if (wgs(lo) > PF_SLOTS) {   // smallest ps in (lo, hi] that fits, or hi
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) / 2;
+      if (wgs(mid) <= PF_SLOTS) hi = mid; else lo = mid;
+    }
+    lo = hi;
+  }
+  return PfPlan{lo, (n_st_max + 2 * lo - 1) / (2 * lo), tiles};
+}
 
 }  // namespace
 
@@ -455,10 +627,9 @@ using namespace ns;
 extern "C" size_t ns_prefill_workspace_bytes(int n_seqs, int n_heads, int head_dim, int max_new, int max_kv) {
   if (n_seqs <= 0 || n_heads <= 0 || max_new <= 0 || max_kv <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
-  const int parts = prefill_parts_max(max_kv);
-  if (parts <= 1) return 0;
-  const size_t tiles = size_t((max_new + PF_QT - 1) / PF_QT) * n_seqs * n_heads;
-  const size_t units = tiles * parts;
+  const PfPlan plan = prefill_plan(n_seqs, n_heads, max_new, max_kv);
+  if (plan.parts <= 1) return 0;
+  const size_t units = size_t(plan.tiles) * n_seqs * n_heads * plan.parts;
   return WS_COUNTER_BYTES + align256(units * PF_R * 2 * PF_THREADS * sizeof(float)) +
          align256(units * PF_R * (head_dim / 16) * 4 * PF_THREADS * sizeof(float));
 }
@@ -482,20 +653,19 @@ extern "C" int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh, 
   NS_REQUIRE(q_st % 8 == 0 && q_sh % 8 == 0 && kv_sblk % 8 == 0 && kv_spos % 8 == 0 && kv_sh % 8 == 0 &&
                  o_st % 8 == 0 && o_sh % 8 == 0,
              "paged_attention_prefill: strides must be multiples of 8 elements");
+  NS_REQUIRE(kv_spos >= 0 && kv_spos * 2 < (int64_t(1) << 26),
+             "paged_attention_prefill: token stride %lld too large for 32-bit page offsets", (long long)kv_spos);
   NS_REQUIRE((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool) |
               reinterpret_cast<uintptr_t>(out)) %
                      16 ==
                  0,
              "paged_attention_prefill: q / k_pool / v_pool / out must be 16-byte aligned");
   if (n_seqs == 0 || max_new == 0) return NS_OK;
-  const int tiles = (max_new + PF_QT - 1) / PF_QT;
-  const int parts = prefill_parts_max(max_kv);
-  NS_REQUIRE(int64_t(tiles) * parts <= 65535, "paged_attention_prefill: %d new tokens over %d keys is too many",
-             max_new, max_kv);
+  const PfPlan plan = prefill_plan(n_seqs, n_heads, max_new, max_kv);
   unsigned* cnt = nullptr;
   float* ws_ml = nullptr;
   float* ws_acc = nullptr;
-  if (parts > 1) {
+  if (plan.parts > 1) {
     const size_t need = ns_prefill_workspace_bytes(n_seqs, n_heads, head_dim, max_new, max_kv);
     if (workspace == nullptr || workspace_bytes < need) {
       set_error("paged_attention_prefill: zero-initialised workspace of %zu bytes needed, got %zu", need,
@@ -503,7 +673,7 @@ extern "C" int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh, 
       return NS_E_WORKSPACE;
     }
     NS_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "paged_attention_prefill: workspace not 256-byte aligned");
-    const size_t ntile = size_t(tiles) * n_seqs * n_heads, units = ntile * parts;
+    const size_t ntile = size_t(plan.tiles) * n_seqs * n_heads, units = ntile * plan.parts;
     NS_REQUIRE(ntile <= size_t(WS_MAX_COUNTERS), "paged_attention_prefill: %zu query tiles x heads exceed %d",
                ntile, WS_MAX_COUNTERS);
     char* wsb = static_cast<char*>(workspace);
@@ -514,12 +684,14 @@ extern "C" int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh, 
   PrefillArgs a{static_cast<const bf16_t*>(q), q_st, q_sh, static_cast<const bf16_t*>(k_pool),
                 static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, seq_info,
                 static_cast<bf16_t*>(out), o_st, o_sh, n_heads / n_kv_heads, max_blocks, num_blocks, n_heads,
-                scale * PF_LOG2E, tiles, parts, cnt, ws_ml, ws_acc};
-  const dim3 grid{unsigned(n_heads), unsigned(tiles * parts), unsigned(n_seqs)};
+                n_seqs, scale * PF_LOG2E, plan.tiles, plan.parts, plan.ps, cnt, ws_ml, ws_acc};
+  const int64_t n_wg = int64_t(n_heads) * plan.tiles * plan.parts * n_seqs;   // an upper bound on the units
+  NS_REQUIRE(n_wg < (int64_t(1) << 31), "paged_attention_prefill: %lld workgroups", (long long)n_wg);
+  const dim3 grid{unsigned(n_wg)};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (head_dim == 64)
-    hipLaunchKernelGGL(paged_prefill_bf16_kernel<64>, grid, dim3(PF_THREADS), 0, s, a);
+    hipLaunchKernelGGL(paged_prefill_bf16_kernel<64>, grid, dim3(PF_WG_THREADS), 0, s, a);
   else
-    hipLaunchKernelGGL(paged_prefill_bf16_kernel<128>, grid, dim3(PF_THREADS), 0, s, a);
+    hipLaunchKernelGGL(paged_prefill_bf16_kernel<128>, grid, dim3(PF_WG_THREADS), 0, s, a);
   return check_launch("paged_attention_prefill");
 }
