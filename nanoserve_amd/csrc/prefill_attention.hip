@@ -31,9 +31,11 @@
 //     swaps (v_permlane32_swap, v_permlane16_swap) instead of LDS shuffles. The softmax reference point
 //     moves only when a score exceeds it by 2^8, so the accumulator is rescaled rarely.
 //   * Masks are computed only on stages that cross a query's diagonal or the end of the keys: key k is
-//     visible to query j iff k <= ctx + j, and keys at or past ctx + T (unwritten slots of the last
-//     page, pages past the tile's reach) are zeroed in V as well, so garbage there can never turn 0 * x
-//     into NaN. Block ids outside [0, num_blocks) are masked pages.
+//     visible to query j iff k <= ctx + j. Only a stage that reaches keys at or past ctx + T (unwritten
+//     slots of the last page, pages past the tile's reach) or holds a bad block id also zeroes those V
+//     rows, so garbage there can never turn 0 * x into NaN; a stage that only crosses a diagonal reads
+//     written keys, whose weights past the diagonal are exact zeros. Block ids outside [0, num_blocks)
+//     are masked pages.
 //   * A tile split over several partitions: each partition publishes its (m, l, acc) with agent-scope
 //     stores, waits for them to complete and bumps the tile's arrival counter; the last to arrive merges
 //     all partitions in partition order (its own from registers, the others loaded PF_MB per round trip;
@@ -260,12 +262,13 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
 
   // One stage: S^T for all 64 keys (both halves of 32 keys: pages 2 hs, 2 hs + 1), one softmax update
   // per query tile over the whole stage, then P and O^T += V^T . P^T half by half, with the second half's
-  // probabilities computed while the first half's products run. MASK: the stage crosses a diagonal or the
-  // end of the keys, or holds a bad block id; otherwise every key is visible to every query of the wave.
+  // probabilities computed while the first half's products run. MODE 0: every key of the stage is visible
+  // to every query of the wave; 1: the stage crosses the wave's diagonal (scores masked); 2: it also reaches
+  // past the keys that exist or holds a bad block id (scores masked and those V rows zeroed).
   // (Every array lives inside this one function: passed by reference between helpers, the compiler kept
   // some of them in scratch memory.)
   auto compute = [&](const unsigned char* st, int kb0, unsigned okm, auto mask_c) __attribute__((always_inline)) {
-    constexpr bool MASK = decltype(mask_c)::value;
+    constexpr int MODE = decltype(mask_c)::value;
     pf_float4_t sc[2][PF_R][2];   // [half][query tile][page of the half]
     pf_bf16x8_t kf[2][KS];
 #pragma unroll
@@ -302,16 +305,18 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
       for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
-        for (int hp = 0; hp < 2; ++hp)
+        for (int hp = 0; hp < 2; ++hp) {
+          // key 4 r4 + e of page pp is visible iff e <= lim (keys past ctx + T lie past every query's
+          // diagonal, since jrow <= T - 1); a bad page hides all four
+          const int pp = 2 * hs + hp;
+          int lim = ctx + jrow[rt] - (kb0 + PF_PAGE * pp + 4 * r4);
+          if constexpr (MODE == 2) lim = ((okm >> pp) & 1u) != 0 ? lim : -1;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            if constexpr (MASK) {
-              const int pp = 2 * hs + hp;
-              const int key = kb0 + PF_PAGE * pp + 4 * r4 + e;
-              if (!(((okm >> pp) & 1u) != 0 && key <= ctx + jrow[rt])) sc[hs][rt][hp][e] = -INFINITY;
-            }
+            if constexpr (MODE != 0) sc[hs][rt][hp][e] = e <= lim ? sc[hs][rt][hp][e] : -INFINITY;
             mx = fmaxf(mx, sc[hs][rt][hp][e]);
           }
+        }
       mx = pf_max4(mx);
       // Reference point m (scaled units, c = scale * log2(e)): weights are exp2(s * c - m). It moves
       // only when a score exceeds it by more than PF_SLACK, so weights stay below 2^PF_SLACK and the
@@ -332,7 +337,7 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
     // ---- per half: V^T fragments by transpose reads (ds_read_b64_tr_b16): within each group of 16 lanes,
     // lane j addresses 4 dims (16t + 4 (j % 4) ..) of key row kb + j / 4, and lane i receives dim 16t + i
     // of keys kb .. kb + 3 -- its A-operand slots for one page; k-slots 0..3 = page 2 hs keys 4 r4 + e,
-    // 4..7 = page 2 hs + 1 (MASK: keys that do not exist, past ctx + T or on a bad page, read as 0).
+    // 4..7 = page 2 hs + 1 (MODE 2: keys that do not exist, past ctx + T or on a bad page, read as 0).
     // Probabilities P^T (B operands, k-slot e = key 4 r4 + e of each page), then O^T += V^T . P^T.
 #pragma unroll
     for (int hs = 0; hs < 2; ++hs) {
@@ -343,7 +348,7 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
         const int vr = PF_PAGE * pp + 4 * r4 + (c16 >> 2);   // the key row this lane addresses
         const unsigned char* vrow = st + L::K_BYTES + vr * L::ROW;
         uint32_t m01 = 0xffffffffu, m23 = 0xffffffffu;
-        if constexpr (MASK) {
+        if constexpr (MODE == 2) {
           const int key0 = kb0 + PF_PAGE * pp + 4 * r4;
           const bool ok = ((okm >> pp) & 1u) != 0;
           m01 = (ok && key0 + 0 < kv_total ? 0x0000ffffu : 0u) | (ok && key0 + 1 < kv_total ? 0xffff0000u : 0u);
@@ -355,7 +360,7 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
           const int chunk = dim >> 3;
           const unsigned char* src = vrow + 16 * (chunk ^ L::vkey(vr)) + 2 * (dim & 7);
           v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)(src));
-          if constexpr (MASK) {
+          if constexpr (MODE == 2) {
             uint2 u = __builtin_bit_cast(uint2, v);
             u.x &= m01;
             u.y &= m23;
@@ -395,10 +400,12 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
   auto run_stage = [&](int n, const unsigned char* st, unsigned okm) __attribute__((always_inline)) {
     const int kb0 = n * PF_KEYS;
     if (wave_live && kb0 <= ctx + j_last_w) {   // the wave sees at least one key of this stage
-      if (kb0 + PF_KEYS - 1 <= ctx + j_first_w && okm == 0xFu)
-        compute(st, kb0, okm, std::false_type{});
+      if (kb0 + PF_KEYS > kv_total || okm != 0xFu)
+        compute(st, kb0, okm, std::integral_constant<int, 2>{});
+      else if (kb0 + PF_KEYS - 1 > ctx + j_first_w)
+        compute(st, kb0, okm, std::integral_constant<int, 1>{});
       else
-        compute(st, kb0, okm, std::true_type{});
+        compute(st, kb0, okm, std::integral_constant<int, 0>{});
     }
   };
   auto issue = [&](int n, int buf) __attribute__((always_inline)) {
@@ -427,79 +434,124 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
 
 #pragma unroll
   for (int rt = 0; rt < PF_R; ++rt) l_run[rt] = pf_sum4(l_run[rt]);
-  // ---- the two groups' states meet in LDS: group 1 stores (m, l, acc) of each lane, group 0 folds them
-  // after its own (range order) -- the same running fold as across workgroups below
-  {
-    __syncthreads();   // every wave is done with the stage buffers
-    float* xml = reinterpret_cast<float*>(lds);                       // [rt][2][256 threads]
-    pf_float4_t* xacc = reinterpret_cast<pf_float4_t*>(lds + 8192);   // [rt][NT][256 threads]
-    if (gi == 1) {
+  // ---- the two groups' states meet in LDS. Group g keeps output tiles [g NT/2, (g + 1) NT/2) (its half):
+  // it hands its (m, l) and the other half of its accumulators to the other group and folds that group's
+  // values of its own half into its own. The fold takes key range 2 part (group 0) first, x0 a0 + x1 a1
+  // with one fixed rounding point, so both groups compute the same (m, l) and the bits do not depend on
+  // which group folds. From here on each group writes, publishes and merges its half only.
+  constexpr int NH2 = NT / 2;
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+  float* xml = reinterpret_cast<float*>(lds);                       // [group][rt][2][256 threads]
+  pf_float4_t* xacc = reinterpret_cast<pf_float4_t*>(lds + 8192);   // [group][rt][NT/2][256 threads]
+  auto hand_over = [&](auto g_c) __attribute__((always_inline)) {
+    constexpr int G = decltype(g_c)::value;
 #pragma unroll
-      for (int rt = 0; rt < PF_R; ++rt) {
-        xml[(2 * rt) * PF_THREADS + tid] = m_run[rt];
-        xml[(2 * rt + 1) * PF_THREADS + tid] = l_run[rt];
+    for (int rt = 0; rt < PF_R; ++rt) {
+      xml[((G * PF_R + rt) * 2) * PF_THREADS + tid] = m_run[rt];
+      xml[((G * PF_R + rt) * 2 + 1) * PF_THREADS + tid] = l_run[rt];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) xacc[(rt * NT + t) * PF_THREADS + tid] = acc[rt][t];
-      }
+      for (int j = 0; j < NH2; ++j) xacc[((G * PF_R + rt) * NH2 + j) * PF_THREADS + tid] = acc[rt][(1 - G) * NH2 + j];
     }
-    __syncthreads();
-    if (gi == 0) {
+  };
+  auto fold_half = [&](auto g_c) __attribute__((always_inline)) {
+    constexpr int G = decltype(g_c)::value;
 #pragma unroll
-      for (int rt = 0; rt < PF_R; ++rt) {
-        const float mb = xml[(2 * rt) * PF_THREADS + tid], lb = xml[(2 * rt + 1) * PF_THREADS + tid];
-        const float Mn = fmaxf(m_run[rt], mb);
-        const float a_old = m_run[rt] == -INFINITY ? 0.f : exp2f(m_run[rt] - Mn);
-        const float a_new = mb == -INFINITY ? 0.f : exp2f(mb - Mn);
-        l_run[rt] = l_run[rt] * a_old + lb * a_new;
+    for (int rt = 0; rt < PF_R; ++rt) {
+      const float mo = xml[(((1 - G) * PF_R + rt) * 2) * PF_THREADS + tid];
+      const float lo = xml[(((1 - G) * PF_R + rt) * 2 + 1) * PF_THREADS + tid];
+      const float m0 = G == 0 ? m_run[rt] : mo, m1 = G == 0 ? mo : m_run[rt];
+      const float l0 = G == 0 ? l_run[rt] : lo, l1 = G == 0 ? lo : l_run[rt];
+      const float Mn = fmaxf(m0, m1);
+      const float a0 = m0 == -INFINITY ? 0.f : exp2f(m0 - Mn), a1 = m1 == -INFINITY ? 0.f : exp2f(m1 - Mn);
+      l_run[rt] = __builtin_fmaf(l0, a0, l1 * a1);
+      m_run[rt] = Mn;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const pf_float4_t v = xacc[(rt * NT + t) * PF_THREADS + tid];
+      for (int j = 0; j < NH2; ++j) {
+        const pf_float4_t v = xacc[(((1 - G) * PF_R + rt) * NH2 + j) * PF_THREADS + tid];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) acc[rt][t][c] = acc[rt][t][c] * a_old + v[c] * a_new;
+        for (int c = 0; c < 4; ++c) {
+          const float own = acc[rt][G * NH2 + j][c];
+          acc[rt][G * NH2 + j][c] = __builtin_fmaf(G == 0 ? own : v[c], a0, (G == 0 ? v[c] : own) * a1);
         }
-        m_run[rt] = Mn;
       }
     }
-  }
-  // lane holds, for query tile rt, tile t and r = 0..3, query c16 at dim 16 t + 4 r4 + r
-  auto write_out = [&](int rt, const pf_float4_t (&o)[NT], float inv) __attribute__((always_inline)) {
-    if (jq[rt] >= T) return;
-    bf16_t* orow = a.out + int64_t(q_start + jq[rt]) * a.o_st + int64_t(h) * a.o_sh;
+  };
+  __syncthreads();   // every wave is done with the stage buffers
+  if (gi == 0) hand_over(G0{}); else hand_over(G1{});
+  __syncthreads();
+  if (gi == 0) fold_half(G0{}); else fold_half(G1{});
+
+  // The output tile goes out through LDS: each group stages its half of every query row (lane holds, for
+  // query tile rt and output tile t, query c16 at dims 16 t + 4 r4 .. + 3), then the workgroup stores whole
+  // rows, 16 bytes per lane (a wave instruction writes four rows of HD * 2 contiguous bytes), instead of
+  // 16 rows x 32 bytes per instruction from the fragments.
+  constexpr int OPITCH = HD + 16;   // bytes per staged half row (HD / 2 bf16 + 16 bytes of bank padding)
+  unsigned char* obuf = lds + 8192 + 2 * PF_R * NH2 * PF_THREADS * 16;   // [half][128 rows][OPITCH]
+  static_assert(8192 + 2 * PF_R * NH2 * PF_THREADS * 16 + 2 * PF_QT * OPITCH <= PF_GROUPS * 2 * L::STAGE,
+                "output staging fits the workgroup's LDS");
+  auto write_half = [&](auto g_c, int rt, const pf_float4_t* o, float inv) __attribute__((always_inline)) {
+    constexpr int G = decltype(g_c)::value;
+    unsigned char* orow = obuf + (G * PF_QT + 16 * PF_R * w + 16 * rt + c16) * OPITCH;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      *reinterpret_cast<uint2*>(orow + 16 * t + 4 * r4) =
-          make_uint2(pf_bf16x2(o[t][0] * inv, o[t][1] * inv), pf_bf16x2(o[t][2] * inv, o[t][3] * inv));
+    for (int j = 0; j < NH2; ++j)
+      *reinterpret_cast<uint2*>(orow + 32 * j + 8 * r4) =
+          make_uint2(pf_bf16x2(o[j][0] * inv, o[j][1] * inv), pf_bf16x2(o[j][2] * inv, o[j][3] * inv));
+  };
+  // after a barrier: rows qbase .. min(qbase + QT, T) - 1 of the staged tile to out, 16 bytes per lane
+  auto store_tile = [&]() __attribute__((always_inline)) {
+    constexpr int CPR = HD / 8;   // 16-byte chunks per row
+    const int rows = min(PF_QT, T - qbase);
+#pragma unroll
+    for (int i = 0; i < PF_QT * CPR / PF_WG_THREADS; ++i) {
+      const int c = tid_wg + PF_WG_THREADS * i, row = c / CPR, k = c % CPR;
+      const int half = k / (CPR / 2), ch = k % (CPR / 2);
+      const uint4 v = *reinterpret_cast<const uint4*>(obuf + (half * PF_QT + row) * OPITCH + 16 * ch);
+      if (row < rows)
+        *reinterpret_cast<uint4*>(a.out + int64_t(q_start + qbase + row) * a.o_st + int64_t(h) * a.o_sh + 8 * k) = v;
+    }
   };
   if (n_parts == 1) {
-    if (gi == 0) {
+    auto out_own = [&](auto g_c) __attribute__((always_inline)) {
+      constexpr int G = decltype(g_c)::value;
 #pragma unroll
-      for (int rt = 0; rt < PF_R; ++rt) write_out(rt, acc[rt], 1.0f / l_run[rt]);
-    }
+      for (int rt = 0; rt < PF_R; ++rt) write_half(g_c, rt, &acc[rt][G * NH2], 1.0f / l_run[rt]);
+    };
+    if (gi == 0) out_own(G0{}); else out_own(G1{});
+    __syncthreads();
+    store_tile();
     return;
   }
 
-  // ---- several partitions: publish, count, and the last to arrive merges in partition order
+  // ---- several partitions: each group publishes its half with 16-byte coherent (sc1) buffer stores, the
+  // tile's counter, and both groups of the last workgroup to arrive merge their halves in partition order
   const int64_t tile_id = (int64_t(seq) * a.n_heads + h) * a.tiles_max + tile;
   const int64_t unit0 = tile_id * a.parts_max;
-  auto ml_of = [&](int x, int rt) __attribute__((always_inline)) {
-    return a.ws_ml + ((unit0 + x) * PF_R + rt) * (2 * PF_THREADS);
-  };
-  auto acc_of = [&](int x, int rt, int t) __attribute__((always_inline)) {
-    return a.ws_acc + (((unit0 + x) * PF_R + rt) * NT + t) * (4 * PF_THREADS) + 4 * tid;
-  };
-  if (gi == 0) {   // group 0 holds the workgroup's state; group 1 only meets the barriers
+  constexpr int SC1 = 16;   // cache policy sc1: device-coherent, bypasses the XCD's L2
+  const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + unit0 * (PF_R * 2 * PF_THREADS), 0, n_parts * (PF_R * 2 * PF_THREADS * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t racc = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_acc + unit0 * (PF_R * NT * 4 * PF_THREADS), 0, n_parts * (PF_R * NT * 4 * PF_THREADS * 4), 0x00020000);
+  auto ml_off = [&](int x, int rt, int which) { return (((x * PF_R + rt) * 2 + which) * PF_THREADS + tid) * 4; };
+  auto acc_off = [&](int x, int rt, int t) { return (((x * PF_R + rt) * NT + t) * PF_THREADS + tid) * 16; };
+  auto publish_half = [&](auto g_c) __attribute__((always_inline)) {
+    constexpr int G = decltype(g_c)::value;
 #pragma unroll
-  for (int rt = 0; rt < PF_R; ++rt) {
-    publish_store(ml_of(part, rt) + tid, m_run[rt]);
-    publish_store(ml_of(part, rt) + PF_THREADS + tid, l_run[rt]);
+    for (int rt = 0; rt < PF_R; ++rt) {
+      if constexpr (G == 0) {   // both groups hold the same (m, l)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run[rt]), rml, ml_off(part, rt, 0), 0, SC1);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run[rt]), rml, ml_off(part, rt, 1), 0, SC1);
+      }
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const pub_u32x4_t bits = {__float_as_uint(acc[rt][t][0]), __float_as_uint(acc[rt][t][1]),
-                                __float_as_uint(acc[rt][t][2]), __float_as_uint(acc[rt][t][3])};
-      publish_store16(acc_of(part, rt, t), bits);
+      for (int j = 0; j < NH2; ++j) {
+        const pf_float4_t v = acc[rt][G * NH2 + j];
+        __builtin_amdgcn_raw_buffer_store_b128(
+            pub_u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+            racc, acc_off(part, rt, G * NH2 + j), 0, SC1);
+      }
     }
-  }
-  }
+  };
+  if (gi == 0) publish_half(G0{}); else publish_half(G1{});
   publish_complete();
   __syncthreads();
   if (tid_wg == 0) {
@@ -509,78 +561,85 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
     s_last = last;
   }
   __syncthreads();
-  if (s_last == 0u || gi != 0) return;
+  if (s_last == 0u) return;
   acquire_published();
-  if (n_parts == 2) {
-    // Two partitions (what the plan gives the longest tiles): the other one's state is loaded in one round
-    // trip and combined with this one's, kept in registers. The expression takes the partitions in order
-    // (p0 a0 + p1 a1), so the bits do not depend on which of the two merges.
-    const int other = part ^ 1;
-    float pm[PF_R], pl[PF_R];
-    pub_u32x4_t u[PF_R][NT];
+  auto merge_half = [&](auto g_c) __attribute__((always_inline)) {
+    constexpr int G = decltype(g_c)::value;
+    if (n_parts == 2) {
+      // Two partitions (what the plan gives the longest tiles): the other one's half is loaded in one round
+      // trip and combined with this one's, kept in registers, as p0 a0 + p1 a1 (the bits do not depend on
+      // which of the two merges).
+      const int other = part ^ 1;
+      float pm[PF_R], pl[PF_R];
+      pub_u32x4_t u[PF_R][NH2];
 #pragma unroll
-    for (int rt = 0; rt < PF_R; ++rt) {
-      pm[rt] = publish_load(ml_of(other, rt) + tid);
-      pl[rt] = publish_load(ml_of(other, rt) + PF_THREADS + tid);
+      for (int rt = 0; rt < PF_R; ++rt) {
+        pm[rt] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rml, ml_off(other, rt, 0), 0, SC1));
+        pl[rt] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rml, ml_off(other, rt, 1), 0, SC1));
 #pragma unroll
-      for (int t = 0; t < NT; ++t) u[rt][t] = publish_load16(acc_of(other, rt, t));
-    }
-#pragma unroll
-    for (int rt = 0; rt < PF_R; ++rt) {
-      const float m0 = part == 0 ? m_run[rt] : pm[rt], m1 = part == 0 ? pm[rt] : m_run[rt];
-      const float l0 = part == 0 ? l_run[rt] : pl[rt], l1 = part == 0 ? pl[rt] : l_run[rt];
-      const float Mx = fmaxf(m0, m1);
-      const float a0 = m0 == -INFINITY ? 0.f : exp2f(m0 - Mx), a1 = m1 == -INFINITY ? 0.f : exp2f(m1 - Mx);
-      const float Ls = l0 * a0 + l1 * a1;
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float v = __uint_as_float(u[rt][t][c]);
-          const float x0 = part == 0 ? acc[rt][t][c] : v, x1 = part == 0 ? v : acc[rt][t][c];
-          acc[rt][t][c] = x0 * a0 + x1 * a1;
-        }
-      write_out(rt, acc[rt], 1.0f / Ls);
-    }
-    return;
-  }
-  // More partitions: fold them in partition order with a running maximum (the result does not depend on
-  // which partition merges), PF_MB per round trip; the own partition is read back like the others, so the
-  // accumulators are free for the loads.
-#pragma unroll
-  for (int rt = 0; rt < PF_R; ++rt) {
-    float M = -INFINITY, Lsum = 0.f;
-    pf_float4_t O[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) O[t] = pf_float4_t{0.f, 0.f, 0.f, 0.f};
-    for (int x0 = 0; x0 < n_parts; x0 += PF_MB) {
-      pub_u32x4_t u[PF_MB][NT];
-      float pm[PF_MB], pl[PF_MB];
-#pragma unroll
-      for (int e = 0; e < PF_MB; ++e) {
-        const int x = min(x0 + e, n_parts - 1);   // slots past the end re-load the last partition (unused)
-        pm[e] = publish_load(ml_of(x, rt) + tid);
-        pl[e] = publish_load(ml_of(x, rt) + PF_THREADS + tid);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) u[e][t] = publish_load16(acc_of(x, rt, t));
+        for (int j = 0; j < NH2; ++j)
+          u[rt][j] = __builtin_amdgcn_raw_buffer_load_b128(racc, acc_off(other, rt, G * NH2 + j), 0, SC1);
       }
 #pragma unroll
-      for (int e = 0; e < PF_MB; ++e) {
-        if (x0 + e < n_parts) {
-          const float Mn = fmaxf(M, pm[e]);
-          const float a_old = M == -INFINITY ? 0.f : exp2f(M - Mn);
-          const float a_new = pm[e] == -INFINITY ? 0.f : exp2f(pm[e] - Mn);
-          Lsum = Lsum * a_old + pl[e] * a_new;
+      for (int rt = 0; rt < PF_R; ++rt) {
+        const float m0 = part == 0 ? m_run[rt] : pm[rt], m1 = part == 0 ? pm[rt] : m_run[rt];
+        const float l0 = part == 0 ? l_run[rt] : pl[rt], l1 = part == 0 ? pl[rt] : l_run[rt];
+        const float Mx = fmaxf(m0, m1);
+        const float a0 = m0 == -INFINITY ? 0.f : exp2f(m0 - Mx), a1 = m1 == -INFINITY ? 0.f : exp2f(m1 - Mx);
+        const float Ls = __builtin_fmaf(l0, a0, l1 * a1);
+        pf_float4_t o[NH2];
 #pragma unroll
-          for (int t = 0; t < NT; ++t)
+        for (int j = 0; j < NH2; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) O[t][c] = O[t][c] * a_old + __uint_as_float(u[e][t][c]) * a_new;
-          M = Mn;
+          for (int c = 0; c < 4; ++c) {
+            const float v = __uint_as_float(u[rt][j][c]), own = acc[rt][G * NH2 + j][c];
+            o[j][c] = __builtin_fmaf(part == 0 ? own : v, a0, (part == 0 ? v : own) * a1);
+          }
+        write_half(g_c, rt, o, 1.0f / Ls);
+      }
+      return;
+    }
+    // More partitions: fold them in partition order with a running maximum (the result does not depend on
+    // which partition merges), PF_MB per round trip; the own partition is read back like the others.
+#pragma unroll
+    for (int rt = 0; rt < PF_R; ++rt) {
+      float M = -INFINITY, Lsum = 0.f;
+      pf_float4_t O[NH2];
+#pragma unroll
+      for (int j = 0; j < NH2; ++j) O[j] = pf_float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int x0 = 0; x0 < n_parts; x0 += PF_MB) {
+        pub_u32x4_t u[PF_MB][NH2];
+        float pm[PF_MB], pl[PF_MB];
+#pragma unroll
+        for (int e = 0; e < PF_MB; ++e) {
+          const int x = min(x0 + e, n_parts - 1);   // slots past the end re-load the last partition (unused)
+          pm[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rml, ml_off(x, rt, 0), 0, SC1));
+          pl[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rml, ml_off(x, rt, 1), 0, SC1));
+#pragma unroll
+          for (int j = 0; j < NH2; ++j)
+            u[e][j] = __builtin_amdgcn_raw_buffer_load_b128(racc, acc_off(x, rt, G * NH2 + j), 0, SC1);
+        }
+#pragma unroll
+        for (int e = 0; e < PF_MB; ++e) {
+          if (x0 + e < n_parts) {
+            const float Mn = fmaxf(M, pm[e]);
+            const float a_old = M == -INFINITY ? 0.f : exp2f(M - Mn);
+            const float a_new = pm[e] == -INFINITY ? 0.f : exp2f(pm[e] - Mn);
+            Lsum = __builtin_fmaf(Lsum, a_old, pl[e] * a_new);
+#pragma unroll
+            for (int j = 0; j < NH2; ++j)
+#pragma unroll
+              for (int c = 0; c < 4; ++c) O[j][c] = __builtin_fmaf(O[j][c], a_old, __uint_as_float(u[e][j][c]) * a_new);
+            M = Mn;
+          }
         }
       }
+      write_half(g_c, rt, O, 1.0f / Lsum);
     }
-    write_out(rt, O, 1.0f / Lsum);
-  }
+  };
+  if (gi == 0) merge_half(G0{}); else merge_half(G1{});
+  __syncthreads();
+  store_tile();
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
