@@ -95,7 +95,8 @@ struct GemmArgs {
   const int64_t* slots;
   int nh, nkv, hd;
   // workspace (zeroed once by the owner; every launch leaves the counters at zero)
-  unsigned* cnt;    // [tiles] arrival counters + [1] finished-tile counter (start of the workspace)
+  unsigned* cnt;    // arrival counters of the sliced tiles, cstride words apart (start of the workspace)
+  int cstride;
   float* part;      // [(tiles - whole) * ks][64 rows][64] published partial tiles of the sliced tiles
   // fused argmax of the persistent kernel: tokens [M], per-row keys [M] and the arrival counter (left zero)
   int64_t* am_out;
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
       a.x += int64_t(G_MAX_M) * mb * a.K;
       a.y += int64_t(G_MAX_M) * mb * a.N;
       a.M = min(G_MAX_M, a.M - G_MAX_M * mb);
-      a.cnt += mb * a.tiles;
+      a.cnt += mb * (a.tiles - a.whole) * a.cstride;
       a.part += int64_t(mb) * (a.tiles - a.whole) * a.ks * G_MAX_M * 64;
     }
   }
@@ -592,9 +593,9 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   publish_complete();
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = publish_count(a.cnt + t);
+    const unsigned prev = publish_count(a.cnt + (t - a.whole) * a.cstride);
     const unsigned last = prev == unsigned(ks - 1);
-    if (last) publish_reset(a.cnt + t);
+    if (last) publish_reset(a.cnt + (t - a.whole) * a.cstride);
     s_flag = last;
   }
   __syncthreads();
@@ -1486,6 +1487,10 @@ static int bind_workspace(GemmArgs& a, const Plan& p, void* ws, size_t ws_bytes)
   }
   unsigned char* b = static_cast<unsigned char*>(ws);
   a.cnt = reinterpret_cast<unsigned*>(b + p.cnt_off);
+  const size_t n_ctr = size_t(p.tiles - p.whole) * size_t(a.mblocks > 1 ? a.mblocks : 1);
+  a.cstride = ws_counter_stride(n_ctr, size_t(G_MAX_TILES + 1));
+  NS_REQUIRE(n_ctr * a.cstride <= size_t(G_MAX_TILES + 1), "skinny gemm: %zu split tiles exceed the %d counters", n_ctr,
+             G_MAX_TILES + 1);
   a.part = reinterpret_cast<float*>(b + p.part_off);
   a.tiles = p.tiles;
   a.chunks = p.chunks;

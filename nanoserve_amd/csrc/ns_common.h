@@ -118,6 +118,13 @@ __device__ __forceinline__ void acquire_published() {
 // partial results of any call start after it.
 constexpr size_t WS_COUNTER_BYTES = size_t(NS_WS_COUNTER_BYTES);
 constexpr int WS_MAX_COUNTERS = int(WS_COUNTER_BYTES / 4);
+// Words between two arrival counters of one launch: a 128-byte line each when the region holds them so,
+// since the atomics of many workgroups on one line queue behind each other at the memory side (measured:
+// 0.25 us per decode-attention launch); packed otherwise.
+constexpr int WS_COUNTER_LINE = 32;
+static inline int ws_counter_stride(size_t n_counters, size_t capacity_words) {
+  return n_counters * WS_COUNTER_LINE <= capacity_words ? WS_COUNTER_LINE : 1;
+}
 // The last WS_AM_FUSED_WORDS words of an argmax workspace's counter region belong to the LM head with the
 // argmax fused (ns_gemm_argmax): its arrival counter (word WS_AM_FUSED_OFF) and one 8-byte key per row
 // (from word WS_AM_FUSED_OFF + 2), which that launch leaves at zero like the counters; the split argmax

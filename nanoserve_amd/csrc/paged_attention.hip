@@ -90,7 +90,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
     const bf16_t* __restrict__ vp, int64_t s_blk, int64_t s_pos, int64_t s_h, const int32_t* __restrict__ bt,
     int64_t bt_sb, const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G,
     int max_blocks, int num_blocks, float scale_log2, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    unsigned* __restrict__ ws_cnt, int B_, int nkv_, int n_parts, const int64_t* __restrict__ qrows) {
+    unsigned* __restrict__ ws_cnt, int B_, int nkv_, int n_parts, const int64_t* __restrict__ qrows, int cstride) {
   constexpr int NW = DecodeCfg<HD>::NW, PPW = DecodeCfg<HD>::PPW, PART = NW * PPW;
   constexpr int KS = HD / 32;  // 32-dim k-steps of the QK^T product (8 bf16 per lane per step)
   constexpr int NT = HD / 16;  // 16-row output tiles of the PV product
@@ -286,9 +286,9 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
   __shared__ unsigned s_last;
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = publish_count(ws_cnt + bg);
+    const unsigned prev = publish_count(ws_cnt + bg * cstride);
     const unsigned last = prev == unsigned(n_active - 1);
-    if (last) publish_reset(ws_cnt + bg);
+    if (last) publish_reset(ws_cnt + bg * cstride);
     s_last = last;
   }
   __syncthreads();
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
     const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G, int nq,
     int max_blocks, int num_blocks, float scale_log2, unsigned* __restrict__ cnt, float* __restrict__ part_acc,
     float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h,
-    const int64_t* __restrict__ qrows) {
+    const int64_t* __restrict__ qrows, int cstride) {
   constexpr int pp = ROWK_PART;
   constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D;
   // A workgroup's token row: 128 elements (256 bytes) -- all KV heads of a token (nkv_grid == 1), or one
@@ -624,9 +624,9 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   publish_complete();
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = publish_count(cnt + row);
+    const unsigned prev = publish_count(cnt + row * cstride);
     const unsigned lst = prev == unsigned(n_active - 1);
-    if (lst) publish_reset(cnt + row);
+    if (lst) publish_reset(cnt + row * cstride);
     s_last = lst;
   }
   __syncthreads();
@@ -841,25 +841,26 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
       rml = reinterpret_cast<float*>(w + WS_COUNTER_BYTES);
       racc = reinterpret_cast<float*>(w + WS_COUNTER_BYTES + align256(size_t(rrows) * rparts * 32 * sizeof(float)));
     }
+    const int rstride = ws_counter_stride(size_t(rrows), size_t(WS_MAX_COUNTERS));
     const dim3 rgrid(unsigned(rparts) * unsigned(rrows));
     if (rgh > 1)
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, rgh, kv_spos, kv_sh, qrows);
+                         rml, B, rparts, rgh, kv_spos, kv_sh, qrows, rstride);
     else if (head_dim == 64)
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows);
+                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows, rstride);
     else
       hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
                          static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                          static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                          static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows);
+                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows, rstride);
     return check_launch("paged_attention_decode(bf16 rows)");
   }
   const int parts = decode_parts(head_dim, max_blocks);
@@ -885,19 +886,20 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
     ws_ml = reinterpret_cast<float*>(w + WS_COUNTER_BYTES);
     ws_acc = reinterpret_cast<float*>(w + WS_COUNTER_BYTES + align256(slots * 16 * 2 * sizeof(float)));
   }
+  const int pstride = ws_counter_stride(size_t(B) * n_kv_heads, size_t(WS_MAX_COUNTERS));
   const dim3 grid(unsigned(parts) * unsigned(n_kv_heads) * unsigned(B));
   if (head_dim == 64)
     hipLaunchKernelGGL(paged_decode_bf16_kernel<64>, grid, dim3(DecodeCfg<64>::NW * 64), 0, s,
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
                        static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, ws_cnt, B,
-                       n_kv_heads, parts, qrows);
+                       n_kv_heads, parts, qrows, pstride);
   else
     hipLaunchKernelGGL(paged_decode_bf16_kernel<128>, grid, dim3(DecodeCfg<128>::NW * 64), 0, s,
                        static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
                        static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, context_lens,
                        static_cast<bf16_t*>(out), o_sb, o_sh, G, max_blocks, num_blocks, sl2, ws_acc, ws_ml, ws_cnt, B,
-                       n_kv_heads, parts, qrows);
+                       n_kv_heads, parts, qrows, pstride);
   return check_launch("paged_attention_decode(bf16)");
 }
 

@@ -140,7 +140,8 @@ struct PrefillArgs {
   int G, max_blocks, num_blocks, n_heads, n_seqs;
   float scale_log2;
   int tiles_max, parts_max, ps;     // query tiles, partitions per tile (grid), target stages per partition
-  unsigned* cnt;                    // [S, n_heads, tiles_max] arrival counters (zero between calls)
+  unsigned* cnt;                    // [S, n_heads, tiles_max] arrival counters, cstride words apart (zero
+  int cstride;                      // between calls)
   float* ws_ml;                     // [unit][R][2][256 threads] (m, l)
   float* ws_acc;                    // [unit][R][NT][256 threads] float4
 };
@@ -555,9 +556,9 @@ __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2
   publish_complete();
   __syncthreads();
   if (tid_wg == 0) {
-    const unsigned prev = publish_count(a.cnt + tile_id);
+    const unsigned prev = publish_count(a.cnt + tile_id * a.cstride);
     const unsigned last = prev == unsigned(n_parts - 1);
-    if (last) publish_reset(a.cnt + tile_id);
+    if (last) publish_reset(a.cnt + tile_id * a.cstride);
     s_last = last;
   }
   __syncthreads();
@@ -722,6 +723,7 @@ extern "C" int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh, 
   if (n_seqs == 0 || max_new == 0) return NS_OK;
   const PfPlan plan = prefill_plan(n_seqs, n_heads, max_new, max_kv);
   unsigned* cnt = nullptr;
+  int cstride = 1;
   float* ws_ml = nullptr;
   float* ws_acc = nullptr;
   if (plan.parts > 1) {
@@ -737,13 +739,14 @@ extern "C" int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh, 
                ntile, WS_MAX_COUNTERS);
     char* wsb = static_cast<char*>(workspace);
     cnt = reinterpret_cast<unsigned*>(wsb);
+    cstride = ws_counter_stride(ntile, size_t(WS_MAX_COUNTERS));
     ws_ml = reinterpret_cast<float*>(wsb + WS_COUNTER_BYTES);
     ws_acc = reinterpret_cast<float*>(wsb + WS_COUNTER_BYTES + align256(units * PF_R * 2 * PF_THREADS * sizeof(float)));
   }
   PrefillArgs a{static_cast<const bf16_t*>(q), q_st, q_sh, static_cast<const bf16_t*>(k_pool),
                 static_cast<const bf16_t*>(v_pool), kv_sblk, kv_spos, kv_sh, block_tables, bt_sb, seq_info,
                 static_cast<bf16_t*>(out), o_st, o_sh, n_heads / n_kv_heads, max_blocks, num_blocks, n_heads,
-                n_seqs, scale * PF_LOG2E, plan.tiles, plan.parts, plan.ps, cnt, ws_ml, ws_acc};
+                n_seqs, scale * PF_LOG2E, plan.tiles, plan.parts, plan.ps, cnt, cstride, ws_ml, ws_acc};
   const int64_t n_wg = int64_t(n_heads) * plan.tiles * plan.parts * n_seqs;   // an upper bound on the units
   NS_REQUIRE(n_wg < (int64_t(1) << 31), "paged_attention_prefill: %lld workgroups", (long long)n_wg);
   const dim3 grid{unsigned(n_wg)};
