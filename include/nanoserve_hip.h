@@ -151,6 +151,26 @@ int ns_paged_attn_prefill(const void* q, int64_t q_st, int64_t q_sh,
 size_t ns_prefill_workspace_bytes(int n_seqs, int n_heads, int head_dim, int max_new, int max_kv);
 
 /*
+ * A mixed step's attention in one launch: ns_paged_attn_prefill over the chunk rows (pf_block_tables,
+ * seq_info, n_seqs, max_new, max_kv, pf_max_blocks, pf_workspace) and ns_paged_attn_decode_rows over the B
+ * decode rows (dec_block_tables, context_lens, q_rows, dec_max_blocks, dec_workspace), with the same
+ * arguments, limits, workspaces and results as those two calls (both write into out, at disjoint rows).
+ * Replaces the per-sequence attention loop of nanoserve/model.py:277-318 for a step holding both decode
+ * rows and chunks. When the decode rows take the whole-row kernel, the two kinds of workgroups share one
+ * grid, so the decode rows run beside the prefill instead of after it; otherwise the two are launched
+ * one after the other on `stream`. n_seqs or B may be 0.
+ */
+int ns_paged_attn_mixed(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool, const void* v_pool,
+                        int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh, const int32_t* pf_block_tables,
+                        int64_t pf_bt_sb, const int32_t* seq_info, int n_seqs, int max_new, int max_kv,
+                        int pf_max_blocks, void* pf_workspace, size_t pf_workspace_bytes,
+                        const int32_t* dec_block_tables, int64_t dec_bt_sb, const int32_t* context_lens,
+                        const int64_t* q_rows, int B, int dec_max_blocks, void* dec_workspace,
+                        size_t dec_workspace_bytes, void* out, int64_t o_sb, int64_t o_sh, int n_heads,
+                        int n_kv_heads, int head_dim, int block_size, int num_blocks, float scale, int dtype,
+                        void* stream);
+
+/*
  * RMSNorm over rows of length n (row-major, contiguous):
  *   if residual != NULL: r = round(residual + x) is stored to res_out and replaces x;
  *   out = round(w * round(x * rsqrt(mean(x^2) + eps)))     (statistics in fp32)

@@ -61,6 +61,16 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         _c_int, _c_int, _c_f32, _c_int,         # max_blocks, num_blocks, scale, dtype
         _c_vp, _c_sz, _c_vp]),                  # workspace, workspace_bytes, stream
     "ns_prefill_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ns_paged_attn_mixed": (_c_int, [
+        _c_vp, _c_i64, _c_i64,                  # q, q_sb, q_sh
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,   # k_pool, v_pool, kv_sblk, kv_spos, kv_sh
+        _c_vp, _c_i64, _c_vp, _c_int, _c_int, _c_int,   # pf_block_tables, pf_bt_sb, seq_info, n_seqs, max_new, max_kv
+        _c_int, _c_vp, _c_sz,                   # pf_max_blocks, pf_workspace, pf_workspace_bytes
+        _c_vp, _c_i64, _c_vp, _c_vp, _c_int, _c_int,   # dec_block_tables, dec_bt_sb, context_lens, q_rows, B, dec_max_blocks
+        _c_vp, _c_sz,                           # dec_workspace, dec_workspace_bytes
+        _c_vp, _c_i64, _c_i64,                  # out, o_sb, o_sh
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_f32, _c_int,   # n_heads n_kv head_dim block_size num_blocks scale dtype
+        _c_vp]),                                # stream
     "ns_rms_norm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_f32, _c_int, _c_vp]),
     "ns_silu_mul": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "ns_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,

@@ -29,6 +29,7 @@
 // fp32 design: one wave per (row, KV head), VALU dot products with wave reductions; kept simple,
 // it serves the fp32 correctness paths.
 #include "ns_common.h"
+#include "prefill_body.h"
 
 #include <mutex>
 #include <type_traits>
@@ -356,16 +357,58 @@ constexpr int ROWK_MAX_PARTS = 32;
 typedef __attribute__((ext_vector_type(4))) unsigned int rk_u32x4_t;
 typedef __attribute__((ext_vector_type(2))) unsigned int rk_u32x2_t;
 
+// Arguments of the whole-row kernel (one struct, so the body can also run inside the mixed launch).
+struct RowsArgs {
+  const bf16_t* q;
+  int64_t q_sb, q_sh;
+  const bf16_t* kp;
+  const bf16_t* vp;
+  int64_t s_blk;
+  const int32_t* bt;
+  int64_t bt_sb;
+  const int32_t* ctxl;
+  bf16_t* out;
+  int64_t o_sb, o_sh;
+  int G, nq, max_blocks, num_blocks;
+  float scale_log2;
+  unsigned* cnt;
+  float* part_acc;
+  float* part_ml;
+  int B, n_parts, nkv_grid;
+  int64_t s_tok, s_h;
+  const int64_t* qrows;
+  int cstride;
+};
+template <int HD>
+constexpr int rows_lds_bytes() {
+  return ROWK_NW * 16 * 256 > ROWK_NW * 16 * (HD + 4) * 4 ? ROWK_NW * 16 * 256 : ROWK_NW * 16 * (HD + 4) * 4;
+}
+
 // PH: each KV head is a workgroup row of its own (hd 128, several KV heads); otherwise a row is a token's
-// whole 256-byte K row.
+// whole 256-byte K row. bid: the workgroup's index among the launch's decode-row workgroups; lds (at least
+// rows_lds_bytes<HD>()), sm_m, sm_l, s_last: the launch's LDS.
 template <int HD, bool PH>
-__global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
-    const bf16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, const bf16_t* __restrict__ kp,
-    const bf16_t* __restrict__ vp, int64_t s_blk, const int32_t* __restrict__ bt, int64_t bt_sb,
-    const int32_t* __restrict__ ctxl, bf16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int G, int nq,
-    int max_blocks, int num_blocks, float scale_log2, unsigned* __restrict__ cnt, float* __restrict__ part_acc,
-    float* __restrict__ part_ml, int B, int n_parts, int nkv_grid_arg, int64_t s_tok_arg, int64_t s_h,
-    const int64_t* __restrict__ qrows, int cstride) {
+__device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, unsigned char* lds,
+                                                 float (*sm_m)[16], float (*sm_l)[16], unsigned& s_last) {
+  const bf16_t* __restrict__ q = ra.q;
+  const int64_t q_sb = ra.q_sb, q_sh = ra.q_sh;
+  const bf16_t* __restrict__ kp = ra.kp;
+  const bf16_t* __restrict__ vp = ra.vp;
+  const int64_t s_blk = ra.s_blk;
+  const int32_t* __restrict__ bt = ra.bt;
+  const int64_t bt_sb = ra.bt_sb;
+  const int32_t* __restrict__ ctxl = ra.ctxl;
+  bf16_t* __restrict__ out = ra.out;
+  const int64_t o_sb = ra.o_sb, o_sh = ra.o_sh;
+  const int G = ra.G, nq = ra.nq, max_blocks = ra.max_blocks, num_blocks = ra.num_blocks;
+  const float scale_log2 = ra.scale_log2;
+  unsigned* __restrict__ cnt = ra.cnt;
+  float* __restrict__ part_acc = ra.part_acc;
+  float* __restrict__ part_ml = ra.part_ml;
+  const int B = ra.B, n_parts = ra.n_parts, nkv_grid_arg = ra.nkv_grid;
+  const int64_t s_tok_arg = ra.s_tok, s_h = ra.s_h;
+  const int64_t* __restrict__ qrows = ra.qrows;
+  const int cstride = ra.cstride;
   constexpr int pp = ROWK_PART;
   constexpr int NW = ROWK_NW, PPW = ROWK_PPW, D = ROWK_D;
   // A workgroup's token row: 128 elements (256 bytes) -- all KV heads of a token (nkv_grid == 1), or one
@@ -373,17 +416,12 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   constexpr int NKV = 128 / HD;
   constexpr int KS = HD / 32;
   constexpr int AROW = HD + 4;
-  constexpr int K_LDS = NW * 16 * 256;
-  constexpr int M_LDS = NW * 16 * AROW * 4;
-  __shared__ __align__(16) unsigned char lds[K_LDS > M_LDS ? K_LDS : M_LDS];
-  __shared__ float sm_m[NW][16], sm_l[NW][16];
-  __shared__ unsigned s_last;
 
   // XCD-aware map as in the per-head kernel: a row's partitions rotate over the XCDs
   const int nkv_grid = PH ? nkv_grid_arg : 1;
   const int64_t s_tok = PH ? s_tok_arg : 128;
   const int R = B * nkv_grid;
-  const int L = blockIdx.x, part = L / R;
+  const int L = bid, part = L / R;
   const int row = (L - part * R + part) % R;
   const int b = row / nkv_grid, g = row - b * nkv_grid;
   const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
@@ -667,6 +705,36 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(
   }
 }
 
+template <int HD, bool PH>
+__global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(RowsArgs a) {
+  __shared__ __align__(16) unsigned char lds[rows_lds_bytes<HD>()];
+  __shared__ float sm_m[ROWK_NW][16], sm_l[ROWK_NW][16];
+  __shared__ unsigned s_last;
+  decode_rows_body<HD, PH>(a, int(blockIdx.x), lds, sm_m, sm_l, s_last);
+}
+
+// A mixed step's attention in one launch: workgroups [0, n_dec) are the whole-row decode kernel's for the
+// step's decode rows, the rest the chunked-prefill kernel's (prefill_body.h). The two write disjoint rows of
+// the output and keep their merges in separate workspaces. Issued as two kernels on one stream the second
+// would wait for the first's last workgroup. Here the decode workgroups are dispatched first (workgroups
+// start in index order) and finish while the prefill's longest work units, which the prefill numbers first,
+// run on the other CUs; the prefill's last, shortest units take the CUs they free. (Two streams overlap them
+// too, but a graph's cross-queue fork and join idle the GPU for longer than that saves.)
+template <int HD, bool PH>
+__global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void mixed_attn_kernel(
+    PrefillArgs pa, int n_dec, RowsArgs ra) {
+  static_assert(PF_WG_THREADS == ROWK_NW * 64, "one workgroup size for both kinds");
+  constexpr int PF_BYTES = PF_GROUPS * 2 * PfLds<HD>::STAGE;
+  constexpr int BYTES = PF_BYTES > rows_lds_bytes<HD>() ? PF_BYTES : rows_lds_bytes<HD>();
+  __shared__ __align__(16) unsigned char lds[BYTES];
+  __shared__ float sm_m[ROWK_NW][16], sm_l[ROWK_NW][16];
+  __shared__ unsigned s_last;
+  if (int(blockIdx.x) < n_dec)
+    decode_rows_body<HD, PH>(ra, int(blockIdx.x), lds, sm_m, sm_l, s_last);
+  else
+    prefill_body<HD>(pa, int(blockIdx.x) - n_dec, lds, s_last);
+}
+
 // fp32: one wave per (row, KV head). Lane owns dims lane and lane + 64 (hd 128).
 template <int HD>
 __global__ __launch_bounds__(64) void paged_decode_f32_kernel(
@@ -776,12 +844,29 @@ extern "C" size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim,
   return a > r ? a : r;
 }
 
+// A whole-row launch prepared but not issued (paged_decode_launch with `defer`).
+struct RowsLaunch {
+  RowsArgs a;
+  unsigned grid;
+  int rgh, head_dim;
+};
+static void launch_rows(const RowsArgs& a, unsigned grid, int rgh, int head_dim, hipStream_t s) {
+  if (rgh > 1)
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+}
+
+// defer: when the whole-row kernel takes the call, fill *defer instead of launching (other kernels launch
+// directly; defer->grid stays as the caller set it).
 static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool, const void* v_pool,
                                int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh, const int32_t* block_tables,
                                int64_t bt_sb, const int32_t* context_lens, void* out, int64_t o_sb, int64_t o_sh, int B,
                                int n_heads, int n_kv_heads, int head_dim, int block_size, int max_blocks,
                                int num_blocks, float scale, int dtype, void* workspace, size_t workspace_bytes,
-                               void* stream, const int64_t* qrows = nullptr) {
+                               void* stream, const int64_t* qrows = nullptr, RowsLaunch* defer = nullptr) {
   NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "paged_attention_decode: dtype %d not supported",
              dtype);
   NS_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention_decode: head_dim %d not in {64, 128}", head_dim);
@@ -842,25 +927,16 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
       racc = reinterpret_cast<float*>(w + WS_COUNTER_BYTES + align256(size_t(rrows) * rparts * 32 * sizeof(float)));
     }
     const int rstride = ws_counter_stride(size_t(rrows), size_t(WS_MAX_COUNTERS));
-    const dim3 rgrid(unsigned(rparts) * unsigned(rrows));
-    if (rgh > 1)
-      hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true>), rgrid, dim3(ROWK_NW * 64), 0, s,
-                         static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
-                         static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
-                         static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, rgh, kv_spos, kv_sh, qrows, rstride);
-    else if (head_dim == 64)
-      hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
-                         static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
-                         static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
-                         static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows, rstride);
-    else
-      hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), rgrid, dim3(ROWK_NW * 64), 0, s,
-                         static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
-                         static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
-                         static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc,
-                         rml, B, rparts, 1, int64_t(128), kv_sh, qrows, rstride);
+    RowsArgs ra{static_cast<const bf16_t*>(q), q_sb, q_sh, static_cast<const bf16_t*>(k_pool),
+                static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
+                static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc, rml, B,
+                rparts, rgh, rgh > 1 ? kv_spos : int64_t(128), kv_sh, qrows, rstride};
+    const unsigned rgrid = unsigned(rparts) * unsigned(rrows);
+    if (defer != nullptr) {   // the caller launches these workgroups (beside others)
+      *defer = RowsLaunch{ra, rgrid, rgh, head_dim};
+      return NS_OK;
+    }
+    launch_rows(ra, rgrid, rgh, head_dim, s);
     return check_launch("paged_attention_decode(bf16 rows)");
   }
   const int parts = decode_parts(head_dim, max_blocks);
@@ -914,6 +990,56 @@ extern "C" int ns_paged_attn_decode_rows(const void* q, int64_t q_sb, int64_t q_
   return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
                              context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
                              num_blocks, scale, dtype, workspace, workspace_bytes, stream, q_rows);
+}
+
+extern "C" int ns_paged_attn_mixed(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool, const void* v_pool,
+                                   int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh, const int32_t* pf_block_tables,
+                                   int64_t pf_bt_sb, const int32_t* seq_info, int n_seqs, int max_new, int max_kv,
+                                   int pf_max_blocks, void* pf_workspace, size_t pf_workspace_bytes,
+                                   const int32_t* dec_block_tables, int64_t dec_bt_sb, const int32_t* context_lens,
+                                   const int64_t* q_rows, int B, int dec_max_blocks, void* dec_workspace,
+                                   size_t dec_workspace_bytes, void* out, int64_t o_sb, int64_t o_sh, int n_heads,
+                                   int n_kv_heads, int head_dim, int block_size, int num_blocks, float scale, int dtype,
+                                   void* stream) {
+  NS_REQUIRE(q_rows != nullptr || B == 0, "paged_attention_mixed: q_rows is NULL");
+  PrefillArgs pa;
+  int64_t n_pf = 0;
+  int st = prefill_prepare(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, pf_block_tables, pf_bt_sb, seq_info,
+                           n_seqs, max_new, max_kv, out, o_sb, o_sh, n_heads, n_kv_heads, head_dim, block_size,
+                           pf_max_blocks, num_blocks, scale, dtype, pf_workspace, pf_workspace_bytes, &pa, &n_pf);
+  if (st != NS_OK) return st;
+  RowsLaunch rl{};
+  rl.grid = 0;
+  if (B > 0) {   // validates the decode rows; launches them itself unless the whole-row kernel takes them
+    st = paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, dec_block_tables, dec_bt_sb,
+                             context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size,
+                             dec_max_blocks, num_blocks, scale, dtype, dec_workspace, dec_workspace_bytes, stream,
+                             q_rows, &rl);
+    if (st != NS_OK) return st;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (n_pf == 0 || rl.grid == 0) {   // one side only: its own kernel
+    if (rl.grid > 0) launch_rows(rl.a, rl.grid, rl.rgh, rl.head_dim, s);
+    if (n_pf > 0) {
+      const dim3 grid{unsigned(n_pf)};
+      if (head_dim == 64)   // every workgroup a prefill one
+        hipLaunchKernelGGL((mixed_attn_kernel<64, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, 0, rl.a);
+      else
+        hipLaunchKernelGGL((mixed_attn_kernel<128, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, 0, rl.a);
+    }
+    return check_launch("paged_attention_mixed");
+  }
+  NS_REQUIRE(n_pf + int64_t(rl.grid) < (int64_t(1) << 31), "paged_attention_mixed: %lld workgroups",
+             (long long)(n_pf + rl.grid));
+  const dim3 grid{unsigned(n_pf + rl.grid)};
+  const int n_dec = int(rl.grid);
+  if (rl.rgh > 1)
+    hipLaunchKernelGGL((mixed_attn_kernel<128, true>), grid, dim3(PF_WG_THREADS), 0, s, pa, n_dec, rl.a);
+  else if (rl.head_dim == 64)
+    hipLaunchKernelGGL((mixed_attn_kernel<64, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, n_dec, rl.a);
+  else
+    hipLaunchKernelGGL((mixed_attn_kernel<128, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, n_dec, rl.a);
+  return check_launch("paged_attention_mixed");
 }
 
 extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,

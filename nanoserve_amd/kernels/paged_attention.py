@@ -114,6 +114,44 @@ def paged_attention_decode_rows(q: torch.Tensor, k_pool: torch.Tensor, v_pool: t
     return out
 
 
+def paged_attention_mixed(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, pf_tables: torch.Tensor,
+                          seq_info: torch.Tensor, max_new: int, max_kv: int, dec_tables: torch.Tensor,
+                          context_lens: torch.Tensor, rows: torch.Tensor, scale: float, out: torch.Tensor) -> torch.Tensor:
+    """A mixed step's attention in one launch: paged_attention_prefill(q, ..., pf_tables, seq_info, max_new, max_kv,
+    out=out) for the chunks' rows and paged_attention_decode_rows(q, ..., dec_tables, context_lens, rows, out=out)
+    for the decode rows (model.py:277-318), their workgroups in one grid so the decode rows run beside the
+    prefill instead of after it. bf16; the same arguments, workspaces and results as the two calls."""
+    N, n_heads, head_dim = q.shape
+    num_blocks, block_size, n_kv_heads, hd2 = k_pool.shape
+    assert hd2 == head_dim and q.dtype == k_pool.dtype == v_pool.dtype == out.dtype == torch.bfloat16
+    assert out.shape == q.shape and q.stride(-1) == 1 and out.stride(-1) == 1 and k_pool.stride(-1) == 1
+    assert v_pool.shape == k_pool.shape and v_pool.stride() == k_pool.stride()
+    S, B = seq_info.shape[0], rows.shape[0]
+    assert seq_info.dtype == torch.int32 and seq_info.shape == (S, 4) and seq_info.is_contiguous()
+    assert pf_tables.dtype == torch.int32 and pf_tables.dim() == 2 and pf_tables.shape[0] == S
+    assert pf_tables.stride(1) == 1 or pf_tables.shape[1] == 1
+    assert rows.dtype == torch.int64 and rows.is_contiguous()
+    assert dec_tables.dtype == torch.int32 and dec_tables.dim() == 2 and dec_tables.shape[0] == B
+    assert dec_tables.stride(1) == 1 or dec_tables.shape[1] == 1
+    assert context_lens.dtype == torch.int32 and context_lens.shape == (B,) and context_lens.is_contiguous()
+    _lib.require_gpu(q, k_pool, v_pool, pf_tables, seq_info, dec_tables, context_lens, rows, out)
+    L = _lib.lib()
+    pws = prefill_workspace(q.device, L.ns_prefill_workspace_bytes(S, n_heads, head_dim, int(max_new), int(max_kv))) \
+        if S > 0 and max_new > 0 else None
+    dws = decode_workspace(q.device, B, n_kv_heads, head_dim, dec_tables.shape[1], q.dtype) if B > 0 else None
+    _lib.check(L.ns_paged_attn_mixed(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        pf_tables.data_ptr(), pf_tables.stride(0), seq_info.data_ptr(), S, int(max_new), int(max_kv),
+        pf_tables.shape[1], None if pws is None else pws.data_ptr(), 0 if pws is None else pws.numel(),
+        dec_tables.data_ptr(), dec_tables.stride(0), context_lens.data_ptr(), rows.data_ptr(), B, dec_tables.shape[1],
+        None if dws is None else dws.data_ptr(), 0 if dws is None else dws.numel(),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        n_heads, n_kv_heads, head_dim, block_size, num_blocks, float(scale), _lib.dtype_code(q), _lib.stream_of(q)),
+        "paged_attention_mixed")
+    return out
+
+
 def prefill_seq_info(q_starts: list[int], n_new: list[int], ctx_lens: list[int], device) -> torch.Tensor:
     """int32 [S, 4] (q_start, n_new, ctx_len, 0) on `device`, from host lists."""
     rows = [[a, b, c, 0] for a, b, c in zip(q_starts, n_new, ctx_lens)]

@@ -291,11 +291,19 @@ class Qwen2Model:
             out[0].copy_(o.view(N, nh * hd))
             return out
         o_all = out if out is not None else torch.empty(1, N, nh * hd, device=q.device, dtype=q.dtype)
+        pre = self._prefill_meta(seqs, paged, slot_mapping, q.dtype)
+        if decode_meta is not None and pre is not None and pre[0] == "chunks":
+            # decode rows and chunks in one launch (their workgroups share the grid)
+            from nanoserve_amd.kernels.paged_attention import paged_attention_mixed
+            _, tables, info, max_new, max_kv = pre
+            paged_attention_mixed(q[0], paged.k[i], paged.v[i], tables, info, max_new, max_kv,
+                                  decode_meta.block_tables, decode_meta.context_lens, decode_meta.token_idx, scale,
+                                  out=o_all[0].view(N, nh, hd))
+            return o_all
         if decode_meta is not None:   # the decode rows' queries and outputs addressed in place
             paged_attention_decode_rows(q[0], paged.k[i], paged.v[i], decode_meta.block_tables,
                                         decode_meta.context_lens, decode_meta.token_idx, scale,
                                         out=o_all[0].view(N, nh, hd))
-        pre = self._prefill_meta(seqs, paged, slot_mapping, q.dtype)
         if pre is not None and pre[0] == "chunks":
             from nanoserve_amd.kernels.paged_attention import paged_attention_prefill
             _, tables, info, max_new, max_kv = pre
