@@ -9,13 +9,16 @@
 // the decode kernel does (paged_attention.py:77).
 //
 // Design:
-//   * Work unit = (head, tile of QT = 128 queries, partition of the tile's keys). A workgroup is 4 waves;
-//     wave w owns queries 32w .. 32w+31 as two 16-query MFMA tiles, so every K and V fragment it reads
-//     from LDS feeds two products. A tile's keys (64-key stages of 4 pages) are split into partitions of
-//     at most PS stages; the host picks PS so the whole launch fits the resident workgroup slots of the
-//     GPU (two per CU) in one round, with the fewest partitions that does.
-//   * K/V go straight from HBM into LDS (global_load_lds, 16 bytes per lane; wave w copies page w of a
-//     stage), double-buffered: the copy of stage n+1 runs while stage n is multiplied. The copies are
+//   * Work unit = (head, tile of QT = 128 queries, partition of the tile's keys). A workgroup is 8 waves
+//     in two groups of 4 that hold the same 128 queries and walk two key ranges of the partition (group
+//     g its half of the stages); wave w of a group owns queries 32w .. 32w+31 as two 16-query MFMA tiles,
+//     so every K and V fragment it reads from LDS feeds two products. A tile's keys (64-key stages of 4
+//     pages) are split into partitions of at most 2 PS stages; the host picks PS so the whole launch fits
+//     PF_SLOTS workgroups (one per CU: each holds 128 KB of LDS) in one round, with the fewest partitions
+//     that does.
+//   * K/V go straight from HBM into LDS (global_load_lds, 16 bytes per lane; wave w of a group copies
+//     page w of the group's stage), double-buffered per group: the copy of stage n+1 runs while stage n
+//     is multiplied. The copies are
 //     inline asm with a scalar page base and per-lane 32-bit offsets fixed for the whole launch, so
 //     issuing one costs no vector arithmetic, and the compiler sees no LDS write in flight (it would
 //     otherwise wait for the whole next-stage copy before the current stage's first LDS read). Block ids
@@ -36,11 +39,13 @@
 //     rows, so garbage there can never turn 0 * x into NaN; a stage that only crosses a diagonal reads
 //     written keys, whose weights past the diagonal are exact zeros. Block ids outside [0, num_blocks)
 //     are masked pages.
-//   * A tile split over several partitions: each partition publishes its (m, l, acc) with agent-scope
-//     stores, waits for them to complete and bumps the tile's arrival counter; the last to arrive merges
-//     all partitions in partition order (its own from registers, the others loaded PF_MB per round trip;
-//     the result does not depend on arrival order) and writes the output. One launch; the workspace
-//     counters are left at zero.
+//   * End of a workgroup: the two groups hand their states over through LDS and each folds half of the
+//     output tiles (dims), so both halves of a row are complete in one group each. The output rows are
+//     staged in LDS and stored whole, 16 bytes per lane. A tile split over several partitions: each
+//     group publishes its half's (m, l, acc) with 16-byte agent-scope stores, waits for them to complete,
+//     and the workgroup bumps the tile's arrival counter; in the last workgroup to arrive both groups
+//     merge their halves over all partitions in partition order (PF_MB partitions loaded per round trip;
+//     the result does not depend on arrival order). One launch; the workspace counters are left at zero.
 #pragma once
 
 #include "ns_common.h"
