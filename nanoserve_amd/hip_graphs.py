@@ -36,6 +36,7 @@ from __future__ import annotations
 
 import gc
 import math
+import time
 
 import torch
 
@@ -43,6 +44,7 @@ from nanoserve_amd.kv_cache import PagedKVCache
 from nanoserve_amd.model import DecodeMeta, Qwen2Model, SeqInput
 
 BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128)
+POLL_S = 0.05   # longest host poll for a decode replay's tokens before a stream synchronisation
 
 
 _SIDE: torch.cuda.Stream | None = None
@@ -96,6 +98,7 @@ class StepGraph:
         self.np = [self._views(t, numpy=True) for t in self.twins]
         self.staged_rows: list[list] = [[None] * B for _ in range(2)]
         self.greedy = torch.empty(B, dtype=torch.int64, pin_memory=True)
+        self.greedy_np = self.greedy.numpy()
         self.par = 1                                  # twin of the last staged step
         for v in self.np:
             self._pad(v, 0)
@@ -156,6 +159,7 @@ class StepGraph:
 
     def launch(self, par: int) -> None:
         self.par = par
+        self.greedy_np.fill(-1)                       # no token yet: the replay's argmax overwrites every row
         self.dev_buf.copy_(self.twins[par], non_blocking=True)
         self.graph.replay()
 
@@ -236,10 +240,19 @@ class DecodeGraphRunner:
         return g.logits[:n]
 
     def greedy_tokens(self, n: int) -> list[int]:
-        """Argmax of the first n rows of the last replay (written into pinned memory inside the graph):
-        waits for the replay, then reads the host buffer."""
-        torch.cuda.current_stream().synchronize()
-        return self.last.greedy[:n].tolist()
+        """Argmax of the first n rows of the last replay. The graph's last kernel (the LM head with the argmax)
+        stores each row's token once, as one 8-byte store, into pinned host memory that launch() filled with
+        -1; the host polls that memory instead of waiting for the stream, so it sees the tokens as soon as
+        they land. A value outside [0, vocab) is not a token yet. After POLL_S without every row the wait
+        falls back to a stream synchronisation."""
+        buf = self.last.greedy_np[:n]
+        vocab = self.model.cfg.vocab_size
+        deadline = time.perf_counter() + POLL_S
+        while not ((buf >= 0) & (buf < vocab)).all():
+            if time.perf_counter() > deadline:
+                torch.cuda.current_stream().synchronize()
+                break
+        return buf.tolist()
 
 
 MIXED_ROW_STEP = 128
