@@ -450,3 +450,26 @@ def test_overlapped_host_staging_matches_plain_steps(hiplib):
     (ta, fa), (tb, fb) = streams(fast), streams(plain)
     assert ta == tb and fa.keys() == fb.keys()
     assert all(0 <= fa[s][0] - fb[s][0] <= 1 for s in fa)
+
+
+def test_polled_greedy_tokens_equal_the_stream_wait(hiplib, monkeypatch):
+    """Decode graph steps hand their greedy tokens over by host polling of the pinned token buffer; with the
+    poll window at zero every read falls back to a stream synchronisation. Both give the same steps."""
+    from nanoserve_amd import hip_graphs
+    from nanoserve_amd.engine import LLMEngine
+    model, _ = gpu_model(SMALL, torch.bfloat16, seed=9)
+    ps = prompts(5, 33, SMALL.vocab_size, seed=10)
+
+    def drive():
+        eng = LLMEngine(model, [], max_seq_len=256, max_num_seqs=8, batch_wait_s=0.0, kv_cache_tokens=8192)
+        for p, n in zip(ps, [20, 7, 31, 16, 25]):
+            eng.add_request(p, n, ignore_eos=True)
+        log = []
+        while eng.has_unfinished():
+            log.append([(o.seq_id, o.token, o.finished) for o in eng.step()])
+        assert eng._stats["graph_steps"] > 10
+        return log
+
+    polled = drive()
+    monkeypatch.setattr(hip_graphs, "POLL_S", 0.0)
+    assert drive() == polled
