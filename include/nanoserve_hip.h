@@ -49,7 +49,9 @@ const char* ns_version(void);
  *   out[b, h, :] = softmax(q[b, h, :] . K[0:ctx_b]^T * scale) . V[0:ctx_b]
  * where token t of row b lives at pool block block_tables[b, t / block_size], position t % block_size.
  * Online softmax with fp32 running max / sum / accumulator; probabilities are rounded to the value
- * dtype before the P.V product. Table entries past ceil(ctx_b / block_size) are never read.
+ * dtype before the P.V product. Pages named by table entries past ceil(ctx_b / block_size) are never
+ * read; the entries themselves may be (block ids are loaded before the context length is known), so each
+ * row must hold max_blocks readable int32 entries, whatever their values.
  * Replaces nanoserve/kernels/paged_attention.py:85 paged_attention_decode (kernel :34-82).
  *
  * Limits: head_dim in {64, 128}; block_size == 16; n_heads / n_kv_heads <= 16; ctx_b >= 1

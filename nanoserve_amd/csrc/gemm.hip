@@ -1117,7 +1117,7 @@ __global__ __launch_bounds__(64) void rms_norm_apply_kernel(const bf16_t* __rest
 //     unit (within 2 ulp of fp32 division before the bf16 rounding).
 constexpr int TG_BK = 32;
 constexpr int TG_CROWS = 64;                  // output rows per STORE epilogue pass
-constexpr int TG_MAX_SPLITS = 16;            // K slices at most (forced plans included)
+constexpr int TG_MAX_SPLITS = 16;            // K slices at most
 constexpr int TG_PLAN_SPLITS = 6;             // K slices the plan chooses at most
 constexpr int TG_RSRC3 = 0x00020000;          // buffer resource word 3: raw (untyped) 32-bit accesses
 
@@ -1420,15 +1420,9 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW>::NT), (TgShape<FM, FN, NW>::WG
 }
 
 // ------------------------------------------------------------------------------------------- host side
-// Workgroups that stream at once: one per CU (NS_GEMM_WGS overrides, for experiments).
-static int target_workgroups() {
-  static int target = [] {
-    const char* e = getenv("NS_GEMM_WGS");
-    const int v = e != nullptr ? atoi(e) : 0;
-    return v > 0 ? v : 256;
-  }();
-  return target;
-}
+// Workgroups that stream at once: one per CU of the MI355X. The plans depend on the shape alone (no
+// environment or device query), so a given call always sums in the same order and gives the same bits.
+constexpr int target_workgroups() { return 256; }
 
 struct Plan {
   int tiles, chunks, whole, ks, grid;
@@ -1516,27 +1510,16 @@ constexpr int T16_MAX_TILES = 512;
 static bool tile16_fits(int K, int tiles) { return K <= T16_MAX_K && tiles <= T16_MAX_TILES; }
 
 // Token split: with at most T16_MAX_TILES workgroups in all, each tile's tokens are cut into blocks of 16,
-// one workgroup each (NS_T16_MSPLIT=0 turns it off, for experiments).
+// one workgroup each.
 static bool t16_token_split(int M, int tiles) {
-  static const bool on = [] {
-    const char* e = getenv("NS_T16_MSPLIT");
-    return e == nullptr || atoi(e) != 0;
-  }();
-  return on && M > 16 && tiles * ((M + 15) / 16) <= T16_MAX_TILES;
+  return M > 16 && tiles * ((M + 15) / 16) <= T16_MAX_TILES;
 }
 // Above 64 rows a plain input on a projection the tile-16 kernel takes (K <= 2048, at most T16_MAX_TILES
 // tiles) runs it token-split (16-token blocks, the blocks of a tile re-reading its weights from L2), in as
 // many rounds as it needs, up to T16_LARGE_M rows (speculative verify batches); larger chunks go to the
-// tiled kernel. NS_T16_MAX_M overrides the bound, for experiments.
+// tiled kernel.
 constexpr int T16_LARGE_M = 192;
-static int t16_max_m() {
-  static const int v = [] {
-    const char* e = getenv("NS_T16_MAX_M");
-    const int x = e != nullptr ? atoi(e) : 0;
-    return x > 0 ? x : T16_LARGE_M;
-  }();
-  return v;
-}
+constexpr int t16_max_m() { return T16_LARGE_M; }
 static bool t16_large_m(int M, int K, int tiles, bool normed) {
   return M > G_MAX_M && M <= t16_max_m() && !normed && tile16_fits(K, tiles);
 }
@@ -1649,18 +1632,6 @@ static void tg_tiles(TgPlan& p, int M, int N, bool silu) {
   p.tiles_m = (M + bm - 1) / bm;
   p.tiles_n = silu ? (N / 2 + bn / 2 - 1) / (bn / 2) : (N + bn - 1) / bn;
 }
-// NS_TG_PLAN="big,splits" fixes the plan (big 1: 256 x 256 tiles, 0: 128 x 128; splits 0: the rule
-// below), for experiments
-static const int* tg_forced() {
-  static int v[2] = {-1, 0};
-  static const bool once = [] {
-    const char* e = getenv("NS_TG_PLAN");
-    if (e == nullptr || sscanf(e, "%d,%d", &v[0], &v[1]) != 2) v[0] = -1;
-    return true;
-  }();
-  (void)once;
-  return v[0] >= 0 ? v : nullptr;
-}
 // 256 x 256 tiles (one workgroup per CU) when there is one for every CU; otherwise 128 x 128 tiles (two per
 // CU). K is sliced only when it is long (at least 128 steps) and the tiles leave workgroup slots free: as many
 // slices as keep every workgroup resident in one round, at most TG_PLAN_SPLITS (the last slice's merge reads
@@ -1670,18 +1641,15 @@ static const int* tg_forced() {
 static TgPlan tg_plan(int M, int N, int K, bool silu) {
   TgPlan p;
   const int T = target_workgroups(), steps = K / TG_BK;
-  const int* forced = tg_forced();
   p.big = 1;
   tg_tiles(p, M, N, silu);
-  if (forced != nullptr ? forced[0] == 0 : int64_t(p.tiles_m) * p.tiles_n < T) {
+  if (int64_t(p.tiles_m) * p.tiles_n < T) {
     p.big = 0;
     tg_tiles(p, M, N, silu);
   }
   const int tiles = p.tiles_m * p.tiles_n, slots = p.big ? T : 2 * T;
   int splits = 1;
-  if (forced != nullptr && forced[1] > 0) {
-    splits = forced[1];
-  } else if (steps >= 128 && tiles < slots) {
+  if (steps >= 128 && tiles < slots) {
     splits = slots / tiles;
     if (splits > TG_PLAN_SPLITS) splits = TG_PLAN_SPLITS;
     if (splits > steps / 8) splits = steps / 8;

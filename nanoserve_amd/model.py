@@ -14,8 +14,10 @@ For decode-sized bf16 batches (M <= 64) each projection is one skinny HIP GEMM w
 its epilogue (kernels/linear.py): QKV + bias + RoPE + KV write; O + residual + RMSNorm statistics;
 gate/up + SiLU*mul with ln2 applied on load; down + residual + statistics for the NEXT RMSNorm (the next
 layer's ln1, or the final norm after the last layer), applied on load by its consumer -- so a decode layer
-is 4 GEMM launches and 1 attention launch. Larger batches use the vendor GEMM
-and the standalone HIP kernels; both round where PyTorch's unfused ops round.
+is 4 GEMM launches and 1 attention launch. Larger bf16 batches (prefill chunks, mixed steps, verify
+batches) use the tiled MFMA GEMM (SiLU*mul fused into gate/up) or, up to 192 rows, the token-blocked
+skinny kernels, plus the standalone HIP RMSNorm and RoPE kernels; every one rounds where PyTorch's unfused
+ops round. fp32 (the correctness configuration) runs its projections through torch's F.linear.
 
 Attention reads K/V in place from the pages rope_qkv has just written. One-token decode rows (DecodeMeta)
 go through the paged decode kernel; the tokens of prefill / chunked-prefill sequences go through the paged
@@ -430,5 +432,20 @@ class Qwen2Model:
         return linear(x, self.lm_head)
 
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, cache=None, logits: str = "last"):
-        raise NotImplementedError("the single-sequence contiguous-cache API (M1) is not part of the HIP path; "
-                                  "use forward_batch with a PagedKVCache")
+        """ONE sequence, the single-request API (nanoserve/model.py:364-367), on the paged path. `cache` is a
+        kv_cache.SequenceKVCache whose `length` stored tokens precede token_ids (it advances by T), or None
+        for a fresh sequence, run in a temporary pool of its own. Returns what forward_batch returns for one
+        sequence: [1, vocab] ("last") or [T, vocab] ("all")."""
+        from nanoserve_amd.kv_cache import SequenceKVCache
+        T = int(token_ids.shape[0])
+        if cache is None:
+            cache = SequenceKVCache(self.cfg, T, self.device, self.dtype)
+        table = cache.table
+        if table.num_tokens + T > cache.max_seq_len:
+            raise ValueError(f"{table.num_tokens} cached + {T} new tokens exceed the cache's {cache.max_seq_len}")
+        slots = torch.tensor(table.slots(T), device=self.device)
+        seq = SeqInput(T, ctx_len=table.num_tokens, block_table=table.blocks)
+        out = self.forward_batch(token_ids.to(self.device), positions.to(self.device), [seq], logits=logits,
+                                 paged=cache.pool, slot_mapping=slots)
+        table.commit(T)
+        return out

@@ -66,8 +66,8 @@ class OracleModel:
         for li, (ln1, qw, qb, kw, kb, vw, vb, ow, ln2, gw, uw, dw) in enumerate(self.layers):
             h = ops.rms_norm(x, ln1, eps)
             N = h.shape[0]
-            q = ops.apply_rope(F.linear(h, qw, qb).view(N, nh, hd), cos, sin)
-            k = ops.apply_rope(F.linear(h, kw, kb).view(N, nkv, hd), cos, sin)
+            q = self.rope(li, F.linear(h, qw, qb).view(N, nh, hd), cos, sin)
+            k = self.rope(li, F.linear(h, kw, kb).view(N, nkv, hd), cos, sin)
             v = F.linear(h, vw, vb).view(N, nkv, hd)
             o = torch.empty(N, nh * hd, dtype=self.dtype)
             for (cache, _), (s0, T) in zip(batch, spans):
@@ -76,13 +76,7 @@ class OracleModel:
                 cache.v[li, :, L0:L0 + T] = v[s0:s0 + T].transpose(0, 1)
                 ks = cache.k[li, :, :L0 + T].transpose(0, 1)
                 vs = cache.v[li, :, :L0 + T].transpose(0, 1)
-                if T == 1:
-                    qs = q[s0:s0 + 1].transpose(0, 1)[None]
-                    a = F.scaled_dot_product_attention(qs, ks.transpose(0, 1)[None], vs.transpose(0, 1)[None],
-                                                       scale=hd ** -0.5, enable_gqa=True)[0].transpose(0, 1)
-                else:
-                    a = ops.causal_offset_attention(q[s0:s0 + T], ks, vs, L0, hd ** -0.5)
-                o[s0:s0 + T] = a.reshape(T, nh * hd)
+                o[s0:s0 + T] = self.attend(li, q[s0:s0 + T], ks, vs, L0).reshape(T, nh * hd)
             x = x + F.linear(o, ow)
             h = ops.rms_norm(x, ln2, eps)
             x = x + F.linear(F.silu(F.linear(h, gw)) * F.linear(h, uw), dw)
@@ -93,6 +87,41 @@ class OracleModel:
         if not all_logits:
             x = x[torch.tensor([s0 + T - 1 for s0, T in spans])]
         return F.linear(x, self.lm_head)
+
+    def rope(self, layer: int, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """q or k rotation of one layer (nanoserve/model.py:242-244). A method so that tests can plant a
+        mistake in one layer of the oracle."""
+        return ops.apply_rope(x, cos, sin)
+
+    def attend(self, layer: int, q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, ctx_len: int) -> torch.Tensor:
+        """One sequence's attention in one layer (nanoserve/model.py:283-318): q [T, nh, hd] at positions
+        ctx_len ..; ks, vs [ctx_len + T, nkv, hd]. One new token: SDPA with GQA and no mask; several: the
+        causal-offset mask. Returns [T, nh, hd]."""
+        hd = self.cfg.head_dim
+        if q.shape[0] == 1:
+            qs = q.transpose(0, 1)[None]
+            return F.scaled_dot_product_attention(qs, ks.transpose(0, 1)[None], vs.transpose(0, 1)[None],
+                                                  scale=hd ** -0.5, enable_gqa=True)[0].transpose(0, 1)
+        return ops.causal_offset_attention(q, ks, vs, ctx_len, hd ** -0.5)
+
+    @torch.inference_mode()
+    def teacher_forced(self, prompts: list[list[int]], streams: list[list[int]], max_len: int | None = None):
+        """Logits of every generated position of `streams` given their own history: step j of stream i is
+        computed on prompt i + streams[i][:j], whatever the oracle itself would have chosen before. Prefill
+        one prompt per step, then batched one-token steps (streams of unequal length drop out as they end).
+        Returns logits[i][j] ([V] each, the oracle's dtype)."""
+        max_len = max_len or max(len(p) + len(s) for p, s in zip(prompts, streams))
+        caches = [self.new_cache(max_len) for _ in prompts]
+        out: list[list[torch.Tensor]] = [[] for _ in prompts]
+        for i, p in enumerate(prompts):
+            if streams[i]:
+                out[i].append(self.step([(caches[i], list(p))])[0])
+        for j in range(1, max(len(s) for s in streams)):
+            live = [i for i, s in enumerate(streams) if len(s) > j]
+            lg = self.step([(caches[i], [streams[i][j - 1]]) for i in live])
+            for r, i in enumerate(live):
+                out[i].append(lg[r])
+        return out
 
     def generate_greedy(self, prompts: list[list[int]], n_new: int, max_len: int | None = None,
                         return_logits: bool = False):

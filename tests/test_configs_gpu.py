@@ -3,14 +3,15 @@
 Config 3 (1.5B shape, bf16, B=32, 1024-token prompts, bucket-32 graph): the graph step equals the eager
 forward bitwise (the reference's tests/test_cuda_graphs.py:58-64 gate at the exact bucket); 128 greedy steps
 give identical streams with the one-step-ahead launch on, off, and with graphs off; logits are finite. The
-same shape with fewer layers is checked against the fp32 CPU oracle on the same bf16 weights under the
-approved tie rule (tests/test_llm_engine.py:17,72-87).
+same shape with fewer layers is checked against the fp32 CPU oracle on the same bf16 weights, teacher-forced
+at every position with a stated logit-error bound (tests/parity.py: the reference's tie rule,
+tests/test_llm_engine.py:72-87, with its gap tied to the measured error).
 Config 4 (a 1536-token chunk on 512 cached tokens plus 16 decode rows, one 1552-row step): the chunked-
 prefill kernel path against the same step with every prefill token as a decode row, and both against the
-oracle, at reduced layers.
+oracle's logits within the same bound, at reduced layers.
 Config 5 (3B shape, 1024-token shared prefix, 211-token suffixes, 32 requests): the shared blocks sit at the
 head of every table with refcount 32, and the streams with and without prefix caching follow the oracle
-under the tie rule, at reduced layers.
+under the same checks, at reduced layers.
 """
 import dataclasses
 
@@ -19,37 +20,25 @@ import torch
 
 from nanoserve_amd.model import QWEN25_1_5B, QWEN25_3B, DecodeMeta, Qwen2Model, SeqInput, random_state_dict
 from oracle.model import OracleModel
+from tests.parity import DELTA_1P5B_2L, DELTA_3B_2L, LogitsRecorder, check_streams
 
 pytestmark = pytest.mark.gpu
 
-TIE_GAP_BF16 = 0.25
-
+# agreement floors of the reduced-layer checks against the fp32 oracle (teacher-forced positions and whole
+# streams); the reference algorithm in bf16 agrees at ~97 % of positions at these shapes (tests/parity.py)
+MIN_AGREE_1P5B = 0.93
+MIN_IDENTICAL_C3 = 4        # of 32 streams x 32 steps
+MIN_AGREE_3B = 0.93
+MIN_IDENTICAL_C5 = 1        # of 8 streams x 32 steps
 
 def prompts(n, length, vocab, seed):
     g = torch.Generator().manual_seed(seed)
     return [torch.randint(0, vocab, (length,), generator=g).tolist() for _ in range(n)]
 
 
-def first_divergence(a, b):
-    return next((k for k in range(min(len(a), len(b))) if a[k] != b[k]), None)
-
-
-def check_tie_rule(ours, ref, ref_logits, label):
-    same = 0
-    for i, (a, b) in enumerate(zip(ours, ref)):
-        j = first_divergence(a, b)
-        if j is None:
-            same += 1
-            continue
-        top2 = ref_logits[i][j].float().topk(2).values
-        gap = (top2[0] - top2[1]).item()
-        print(f"{label}: request {i} diverges at token {j}, oracle top-2 gap {gap:.3e}")
-        assert gap <= TIE_GAP_BF16, f"{label}: request {i} diverged at {j} with a top-2 gap of {gap}"
-    print(f"{label}: {same}/{len(ours)} streams identical to the fp32 oracle")
-
-
-def run_engine(eng, reqs, waves=None, on_step=None):
-    """Add requests (optionally in waves (step, count)) and step until done; tokens per request."""
+def run_engine(eng, reqs, waves=None, on_step=None, recorder=None):
+    """Add requests (optionally in waves (step, count)) and step until done; tokens per request. A
+    LogitsRecorder, if given, collects each emitted token's logits."""
     outs, idx, steps = {}, {}, 0
     pending = list(waves) if waves else [(0, len(reqs))]
     while pending or eng.has_unfinished():
@@ -59,7 +48,12 @@ def run_engine(eng, reqs, waves=None, on_step=None):
                 p, n = reqs[i]
                 idx[eng.add_request(p, n, ignore_eos=True)] = i
                 outs[i] = []
-        for o in eng.step():
+        if recorder is not None:
+            recorder.ids = idx
+        step_out = eng.step()
+        if recorder is not None:
+            recorder.commit(step_out)
+        for o in step_out:
             outs[idx[o.seq_id]].append(o.token)
         if on_step is not None:
             on_step(eng, steps)
@@ -157,14 +151,15 @@ def test_config3_reduced_layers_against_the_oracle(hiplib):
     model = Qwen2Model(cfg, {k: v.to("cuda") for k, v in sd.items()})
     eng = engine(model)
     eng.capture_graphs()
-    ours = run_engine(eng, [(p, 32) for p in ps])
+    rec = LogitsRecorder(eng)
+    ours = run_engine(eng, [(p, 32) for p in ps], recorder=rec)
     assert eng.stats["graph_steps"] >= 31
     del eng, model
     torch.cuda.empty_cache()
-    print("config 3 (2 layers): oracle", flush=True)
+    print("config 3 (2 layers): oracle, teacher-forced", flush=True)
     orc = OracleModel(cfg, sd, dtype=torch.float32)
-    ref, ref_logits = orc.generate_greedy(ps, 32, return_logits=True)
-    check_tie_rule(ours, ref, ref_logits, "config 3 (2 layers)")
+    check_streams("config 3 (2 layers)", ps, ours, orc, delta_max=DELTA_1P5B_2L, min_identical=MIN_IDENTICAL_C3,
+                  min_agree=MIN_AGREE_1P5B, ours_logits=rec.per_request(32))
 
 
 def test_config4_mixed_step_reduced_layers(hiplib, monkeypatch):
@@ -235,7 +230,11 @@ def test_config4_mixed_step_reduced_layers(hiplib, monkeypatch):
     print(f"config 4 (2 layers): chunks vs rows {d_paths:.3e}; vs oracle {d_chunks:.3e} (rows {d_rows:.3e}); "
           f"argmax equal {torch.equal(chunks.argmax(-1), ref.argmax(-1))}")
     assert d_paths <= 0.05
-    assert d_chunks <= max(2 * d_rows, 0.05)
+    assert d_chunks <= DELTA_1P5B_2L and d_rows <= DELTA_1P5B_2L
+    for out, d in ((chunks, d_chunks), (rows, d_rows)):     # a differing argmax only on a near-tie
+        for r in (out.argmax(-1) != ref.argmax(-1)).nonzero().flatten().tolist():
+            gap = (ref[r].max() - ref[r, out[r].argmax()]).item()
+            assert gap <= 2 * d, f"row {r}: argmax differs from the oracle's with a gap of {gap}"
 
 
 def test_config5_prefix_sharing_reduced_layers(hiplib):
@@ -267,22 +266,27 @@ def test_config5_prefix_sharing_reduced_layers(hiplib):
 
     eng = engine(model, max_seq_len=1235 + 64, prefix_caching=True, max_num_batched_tokens=2048)
     eng.capture_graphs()
-    shared = run_engine(eng, reqs, waves=((0, 1), (1, 32)), on_step=shared_blocks)
+    rec_shared = LogitsRecorder(eng)
+    shared = run_engine(eng, reqs, waves=((0, 1), (1, 32)), on_step=shared_blocks, recorder=rec_shared)
     st = eng.stats
     print(f"config 5 (2 layers): prefix hits {st['prefix_hit_tokens']} of {st['prefix_query_tokens']}; "
           f"shared-table check at step {checked}", flush=True)
     assert checked and st["prefix_hit_tokens"] == 31 * 1024
     assert eng.kv.num_free_blocks == eng.kv.pool.num_blocks - 1
     del eng
-    plain = run_engine(engine(model, max_seq_len=1235 + 64, max_num_batched_tokens=2048), reqs,
-                       waves=((0, 1), (1, 32)))
+    eng = engine(model, max_seq_len=1235 + 64, max_num_batched_tokens=2048)
+    rec_plain = LogitsRecorder(eng)
+    plain = run_engine(eng, reqs, waves=((0, 1), (1, 32)), recorder=rec_plain)
+    del eng
     print(f"config 5 (2 layers): {sum(a == b for a, b in zip(shared, plain))}/32 streams identical with and "
           "without prefix caching", flush=True)
     del model
     torch.cuda.empty_cache()
-    print("config 5 (2 layers): oracle on 8 of the 32 requests", flush=True)
+    print("config 5 (2 layers): oracle on 8 of the 32 requests, teacher-forced", flush=True)
     orc = OracleModel(cfg, sd, dtype=torch.float32)
     pick = [0, 1, 5, 11, 17, 23, 29, 31]
-    ref, ref_logits = orc.generate_greedy([ps[i] for i in pick], 32, return_logits=True)
-    check_tie_rule([shared[i] for i in pick], ref, ref_logits, "config 5 (2 layers), prefix caching")
-    check_tie_rule([plain[i] for i in pick], ref, ref_logits, "config 5 (2 layers), no prefix caching")
+    for label, outs, rec in (("prefix caching", shared, rec_shared), ("no prefix caching", plain, rec_plain)):
+        lg = rec.per_request(32)
+        check_streams(f"config 5 (2 layers), {label}", [ps[i] for i in pick], [outs[i] for i in pick], orc,
+                      delta_max=DELTA_3B_2L, min_identical=MIN_IDENTICAL_C5, min_agree=MIN_AGREE_3B,
+                      ours_logits=[lg[i] for i in pick])

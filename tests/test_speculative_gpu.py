@@ -4,7 +4,8 @@ own gates (tests/test_speculative.py:1-12):
     greedy decoding of the target;
   * a different draft model, fp32: output identical to plain greedy decoding of the target, which itself
     follows the CPU oracle;
-  * bf16: the approved tie rule against the fp32 oracle on the same weights;
+  * bf16: the fp32 oracle on the same weights, teacher-forced at every position, a disagreement allowed
+    only within twice the shape's logit-error bound (tests/parity.py);
   * batched requests give the same tokens as one request at a time.
 Random-init models (vocab 2048) stand in for the hub checkpoints, which are not available offline.
 """
@@ -13,6 +14,7 @@ import torch
 
 from nanoserve_amd.model import ModelConfig, Qwen2Model, random_state_dict
 from oracle.model import OracleModel
+from tests.parity import DELTA_SMALL128, check_streams
 
 pytestmark = pytest.mark.gpu
 
@@ -96,7 +98,7 @@ def test_batched_speculation_equals_one_request_at_a_time(hiplib):
     assert together == alone
 
 
-def test_bf16_speculation_follows_the_tie_rule(hiplib):
+def test_bf16_speculation_follows_the_oracle(hiplib):
     sd = random_state_dict(TARGET128, seed=8, dtype=torch.bfloat16)
     target = Qwen2Model(TARGET128, {k: v.cuda() for k, v in sd.items()})
     ps = prompts(4, 9)
@@ -104,11 +106,6 @@ def test_bf16_speculation_follows_the_tie_rule(hiplib):
     print(f"bf16 self-speculation: acceptance {st['acceptance_rate']:.3f}")
     assert st["acceptance_rate"] >= 0.8
     orc = OracleModel(TARGET128, sd, dtype=torch.float32)
-    for p, ours in zip(ps, out):
-        ref, lg = orc.generate_greedy([p], MAX_NEW, return_logits=True)
-        j = next((i for i in range(MAX_NEW) if ours[i] != ref[0][i]), None)
-        if j is not None:
-            top2 = lg[0][j].float().topk(2).values
-            gap = (top2[0] - top2[1]).item()
-            print(f"bf16 speculation diverges from the oracle at {j}, top-2 gap {gap:.3e}")
-            assert gap <= 0.25
+    # the verify steps' logits are not exposed: a disagreement passes only within 2x the shape's bound
+    check_streams("bf16 self-speculation", ps, out, orc, delta_max=DELTA_SMALL128, min_identical=len(ps) - 1,
+                  min_agree=0.98)

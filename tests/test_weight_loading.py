@@ -69,3 +69,59 @@ def test_loaded_model_runs_like_the_state_dict_model(hiplib, tmp_path):
             toks += [o.token for o in eng.step()]
         outs.append(toks)
     assert outs[0] == outs[1] and len(outs[0]) == 12
+
+
+def test_eos_ids_from_generation_config_with_config_fallback(tmp_path):
+    """nanoserve/engine.py:33-43: generation_config.json's eos_token_id (an int or a list) first, config.json's
+    when that file or key is missing or null; neither -> ValueError."""
+    from nanoserve_amd.engine import load_eos_token_ids
+    gen, cfg = tmp_path / "generation_config.json", tmp_path / "config.json"
+    cfg.write_text(json.dumps({"model_type": "qwen2", "eos_token_id": 151643}))
+    assert load_eos_token_ids(str(tmp_path)) == [151643]                     # no generation_config.json
+    gen.write_text(json.dumps({"eos_token_id": [151645, 151643], "bos_token_id": 151643}))
+    assert load_eos_token_ids(str(tmp_path)) == [151645, 151643]             # a list wins over config.json
+    gen.write_text(json.dumps({"eos_token_id": 7}))
+    assert load_eos_token_ids(str(tmp_path)) == [7]
+    gen.write_text(json.dumps({"do_sample": False}))                         # key missing -> config.json
+    assert load_eos_token_ids(str(tmp_path)) == [151643]
+    gen.write_text(json.dumps({"eos_token_id": None}))                       # null -> config.json
+    assert load_eos_token_ids(str(tmp_path)) == [151643]
+    cfg.write_text(json.dumps({"model_type": "qwen2"}))
+    with pytest.raises(ValueError):
+        load_eos_token_ids(str(tmp_path))
+    with pytest.raises(FileNotFoundError):
+        load_eos_token_ids(str(tmp_path / "missing"))
+
+
+@pytest.mark.gpu
+def test_engines_from_a_local_folder_stop_at_its_eos(hiplib, tmp_path):
+    """LLMEngine.from_pretrained / Engine.from_pretrained (nanoserve/engine.py:166-169, 311-314) on a local
+    folder: weights and stop tokens both come from it. The EOS is set to the token the model emits at its
+    5th step, so a request that does not ignore EOS ends there, that token included."""
+    from nanoserve_amd.engine import Engine, LLMEngine
+    sd = random_state_dict(CFG, seed=4, dtype=torch.bfloat16)
+    write_folder(tmp_path, CFG, sd)
+    prompt = torch.randint(0, CFG.vocab_size, (33,), generator=torch.Generator().manual_seed(5)).tolist()
+    kw = dict(max_seq_len=128, max_num_seqs=1, batch_wait_s=0.0, kv_cache_tokens=512)
+    (tmp_path / "generation_config.json").write_text(json.dumps({"eos_token_id": []}))
+    free = LLMEngine(Qwen2Model(CFG, {k: v.cuda() for k, v in sd.items()}), [], **kw)
+    free.add_request(prompt, 12, ignore_eos=True)
+    toks = []
+    while free.has_unfinished():
+        toks += [o.token for o in free.step()]
+    eos = toks[4]
+    stop = toks.index(eos) + 1
+    (tmp_path / "generation_config.json").write_text(json.dumps({"eos_token_id": [CFG.vocab_size + 1, eos]}))
+    eng = LLMEngine.from_pretrained(str(tmp_path), device="cuda", dtype=torch.bfloat16, **kw)
+    assert eng.eos_token_ids == [CFG.vocab_size + 1, eos]
+    sid = eng.add_request(prompt, 12)
+    got, finished = [], None
+    while eng.has_unfinished():
+        for o in eng.step():
+            assert o.seq_id == sid
+            got.append(o.token)
+            finished = o.finished
+    assert got == toks[:stop] and finished
+    single = Engine.from_pretrained(str(tmp_path), device="cuda", dtype=torch.bfloat16, max_seq_len=128)
+    assert list(single.generate(prompt, 12)) == toks[:stop]
+    assert list(single.generate(prompt, 12, ignore_eos=True)) == toks
