@@ -316,6 +316,53 @@ int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void*
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Fragment-packed weights for decode-sized products (M <= 64). The reference has no counterpart for the
+ * layout itself (its projections are cuBLAS calls on row-major weights); the products below replace the same
+ * F.linear calls as their row-major twins above (nanoserve/model.py:231,256-257,362), with the same epilogues
+ * and rounding points, and exist because the layout streams from HBM much faster.
+ * Layout: W [N, K] row-major taken in 16-row tiles (order 0: rows 16t .. 16t+15; order 1, a merged
+ * [gate; up] weight of N = 2I rows: gate rows 8t .. 8t+7 then the matching up rows; order 2, a merged QKV
+ * weight of head_dim-wide heads: dims 8f .. 8f+7 of a head then the dims head_dim/2 further), rows past the
+ * end clamped to the last one; block (t, s) = 1 KB holds, for lane l = 0..63, the 8 bf16
+ * W[row(t, l % 16)][32 s + 8 (l / 16) .. +7], blocks in (tile, k-step) order. K a multiple of 32.
+ * ns_packed_weight_bytes gives the size (0 for a shape that cannot be packed); ns_pack_weight writes it
+ * (one launch, 16-byte aligned pointers).
+ * Workspaces: ns_gemm_packed_workspace_bytes(M, N, K, order, head_dim) bytes, 256-byte aligned, zero-filled
+ * once, as for the row-major kernels (long-K and few-tile shapes split K over workgroups and merge in the
+ * same launch; every call leaves the counters at zero). Results are deterministic.
+ */
+size_t ns_packed_weight_bytes(int N, int K, int order, int head_dim);
+int ns_pack_weight(const void* w, void* packed, int N, int K, int order, int head_dim, void* stream);
+size_t ns_gemm_packed_workspace_bytes(int M, int N, int K, int order, int head_dim);
+/* 1 when the packed plan for this shape splits K over workgroups (K > 2048), whose merge in the same launch
+ * costs three dependent cross-XCD round trips: the row-major kernels are the faster choice there. */
+int ns_gemm_packed_sliced(int M, int N, int K, int order, int head_dim);
+/* As ns_gemm on a packed weight of order 0 (N a multiple of 8, bias NULL or 16-byte aligned). */
+int ns_gemm_packed(const void* x, const void* w_packed, const void* bias, void* y, int M, int N, int K, int dtype,
+                   const float* x_sumsq, const void* x_norm_w, float x_eps,
+                   void* workspace, size_t workspace_bytes, void* stream);
+/* As ns_gemm_argmax on a packed weight of order 0, where ns_gemm_argmax_packed_fits(M, N, K) is 1 (K unsplit,
+ * N a multiple of 8); workspace = the argmax workspace (ns_argmax_workspace_bytes), as for ns_gemm_argmax. */
+int ns_gemm_argmax_packed_fits(int M, int N, int K);
+int ns_gemm_argmax_packed(const void* x, const void* w_packed, void* y, int M, int N, int K, int dtype,
+                          const float* x_sumsq, const void* x_norm_w, float x_eps, int64_t* tokens,
+                          void* workspace, size_t workspace_bytes, void* stream);
+/* As ns_gemm_silu_mul on a packed weight of order 1. */
+int ns_gemm_silu_mul_packed(const void* x, const void* w_packed, void* out, int M, int N2, int K, int dtype,
+                            const float* x_sumsq, const void* x_norm_w, float x_eps,
+                            void* workspace, size_t workspace_bytes, void* stream);
+/* As ns_gemm_residual_norm_stats on a packed weight of order 0 (N a multiple of 8). */
+int ns_gemm_residual_norm_stats_packed(const void* x, const void* w_packed, const void* residual, void* res_out,
+                                       float* row_sumsq, int M, int N, int K, int dtype,
+                                       void* workspace, size_t workspace_bytes, void* stream);
+/* As ns_gemm_rope_qkv on a packed weight of order 2 (head_dim 64 or 128, 16-byte aligned operands). */
+int ns_gemm_rope_qkv_packed(const void* x, const void* w_packed, const void* bias, const void* cos, const void* sin,
+                            void* q, void* k, void* v, void* k_cache, void* v_cache, const int64_t* slots, int M,
+                            int K, int n_heads, int n_kv_heads, int head_dim, int dtype,
+                            const float* x_sumsq, const void* x_norm_w, float x_eps,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Greedy selection: out[r] = index of the first maximal element of row r of x (rows x n, row stride
  * ld elements); NaN ranks above every number (torch.argmax semantics). int64 output.
  * Replaces logits.argmax(-1) of nanoserve/engine.py:239 / sampling.py:59-60.

@@ -96,6 +96,23 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "ns_gemm_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                   _c_vp, _c_vp, _c_f32, _c_vp, _c_sz, _c_vp]),
+    # fragment-packed weights (decode-sized products)
+    "ns_packed_weight_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),             # N K order head_dim
+    "ns_pack_weight": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),   # w packed N K order hd stream
+    "ns_gemm_packed_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),   # M N K order hd
+    "ns_gemm_packed_sliced": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ns_gemm_packed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,   # x wp bias y M N K dtype
+                                _c_vp, _c_vp, _c_f32, _c_vp, _c_sz, _c_vp]),
+    "ns_gemm_argmax_packed_fits": (_c_int, [_c_int, _c_int, _c_int]),
+    "ns_gemm_argmax_packed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,   # x wp y M N K dtype
+                                       _c_vp, _c_vp, _c_f32, _c_vp, _c_vp, _c_sz, _c_vp]),
+    "ns_gemm_silu_mul_packed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
+                                         _c_vp, _c_vp, _c_f32, _c_vp, _c_sz, _c_vp]),
+    "ns_gemm_residual_norm_stats_packed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                                    _c_int, _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
+    "ns_gemm_rope_qkv_packed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                         _c_vp, _c_vp, _c_f32, _c_vp, _c_sz, _c_vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -13,6 +13,11 @@ the residual stream also writes per-16-column row sums of its square, and the pr
 rms_norm(residual) normalises its input fragments as it loads them ("norm on load"). Such an input is a
 NormedRows (r, row_sumsq, weight, eps); NormedRows.tensor() materialises h with the same arithmetic.
 
+Decode-sized products (M <= 64) run on fragment-packed weights where the caller hands a PackedWeight: the
+weight stored once more, at load, in the order the MFMA consumes it (csrc/packed_gemm.hip), which streams
+at a far higher rate than the row-major skinny kernels. A PackedWeight keeps the row-major tensor too, for
+the larger products.
+
 Fused entry points (each with the unfused composition it equals):
   linear(x, w, b)                                   F.linear(x, w, b)
   linear_silu_mul(x, w_gate_up)                     silu_mul(F.linear(x, w_gate_up))
@@ -92,6 +97,63 @@ class NormedRows:
         return NormedRows(self.r[idx].contiguous(), sq, self.weight, self.eps)
 
 
+PACK_ROWS, PACK_GATE_UP, PACK_ROPE = 0, 1, 2   # tile row orders of csrc/packed_gemm.hip
+
+
+class PackedWeight:
+    """A bf16 weight W [N, K] (row-major, `w`) with its fragment-packed copy (`p`, uint8) for decode-sized
+    products. order: PACK_ROWS (plain, residual and LM-head projections), PACK_GATE_UP (a merged [gate; up]
+    weight), PACK_ROPE (a merged QKV weight of head_dim-wide heads)."""
+
+    def __init__(self, w: torch.Tensor, order: int = PACK_ROWS, head_dim: int = 0):
+        assert w.dtype == torch.bfloat16 and w.dim() == 2 and w.is_cuda and w.is_contiguous()
+        N, K = w.shape
+        self.w, self.order, self.head_dim = w, order, head_dim
+        nbytes = _lib.lib().ns_packed_weight_bytes(N, K, order, head_dim)
+        if nbytes == 0:
+            raise ValueError(f"weight {tuple(w.shape)} cannot be packed (K must be a multiple of 32)")
+        self.p = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+        _lib.check(_lib.lib().ns_pack_weight(w.data_ptr(), self.p.data_ptr(), N, K, order, head_dim,
+                                             _lib.stream_of(w)), "pack_weight")
+
+    @property
+    def shape(self):
+        return self.w.shape
+
+
+_SLICED_OK = [False]   # tests switch this on to exercise the packed K-sliced plans (packed_sliced_plans())
+
+
+class packed_sliced_plans:
+    """Within this context, decode-sized products on a PackedWeight take the packed kernels even where
+    their plan slices K (by default those go to the row-major kernels, which are faster there)."""
+
+    def __enter__(self):
+        _SLICED_OK[0] = True
+
+    def __exit__(self, *exc):
+        _SLICED_OK[0] = False
+
+
+def _split(w, M: int | None = None):
+    """(row-major tensor, PackedWeight or None) of a weight argument; with M, the packed copy only where its
+    plan keeps K whole (a sliced plan's merge costs more than the row-major kernels' streaming)."""
+    if not isinstance(w, PackedWeight):
+        return w, None
+    if M is not None and 1 <= M <= SKINNY_MAX_M and not _SLICED_OK[0]:
+        N, K = w.w.shape
+        if _lib.lib().ns_gemm_packed_sliced(M, N, K, w.order, w.head_dim) == 1:
+            return w.w, None
+    return w.w, w
+
+
+def _pk_ws(x, pw: PackedWeight):
+    M, K = x.shape
+    N = pw.w.shape[0]
+    ws = _workspace(x.device, _lib.lib().ns_gemm_packed_workspace_bytes(M, N, K, pw.order, pw.head_dim))
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
+
+
 def _dense(x) -> torch.Tensor:
     return x.tensor() if isinstance(x, NormedRows) else x
 
@@ -131,7 +193,17 @@ def _ws_args(x, N: int):
     return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
 
-def linear(x, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
+def linear(x, w, b: torch.Tensor | None = None) -> torch.Tensor:
+    w, pw = _split(w, x.shape[0])
+    if pw is not None and skinny_ok(x, w) and w.shape[0] % 8 == 0 and (b is None or b.data_ptr() % 16 == 0):
+        M, K = x.shape
+        N = w.shape[0]
+        y = torch.empty(M, N, device=x.device, dtype=x.dtype)
+        wsp, wsn = _pk_ws(x, pw)
+        xp, sq, nw, eps = _x_args(x)
+        _lib.check(_lib.lib().ns_gemm_packed(xp, pw.p.data_ptr(), _lib.ptr(b), y.data_ptr(), M, N, K, 1, sq, nw, eps,
+                                             wsp, wsn, _lib.stream_of(w)), "linear (packed)")
+        return y
     if not hip_ok(x, w):
         return F.linear(_dense(x), w, b)
     if not skinny_ok(x, w):
@@ -146,15 +218,30 @@ def linear(x, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
     return y
 
 
-def linear_argmax(x, w: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+def linear_argmax(x, w, tokens: torch.Tensor) -> torch.Tensor:
     """LM head with the greedy choice: returns x W^T (the logits of `linear`) and writes their row-wise argmax
     (first maximal index, NaN highest) into `tokens` (int64 [M], device or pinned host memory). One launch
     where the persistent LM-head kernel takes the shape (ns_gemm_argmax_fused), else linear + argmax_rows."""
     from nanoserve_amd.kernels.sampling import argmax_rows, argmax_workspace
+    w, pw = _split(w)
     t = x.r if isinstance(x, NormedRows) else x
     M, K = t.shape
     N = w.shape[0]
     assert tokens.dtype == torch.int64 and tokens.shape == (M,) and tokens.is_contiguous()
+    if pw is not None and skinny_ok(x, w) and N % 8 == 0:
+        # the packed product, with the argmax fused where the plan keeps K whole; otherwise the same packed
+        # product (bitwise what `linear` returns for it) and the argmax kernel after it
+        ws = argmax_workspace(w.device)
+        if ws is not None and _lib.lib().ns_gemm_argmax_packed_fits(M, N, K) == 1:
+            y = torch.empty(M, N, device=t.device, dtype=t.dtype)
+            xp, sq, nw, eps = _x_args(x)
+            _lib.check(_lib.lib().ns_gemm_argmax_packed(xp, pw.p.data_ptr(), y.data_ptr(), M, N, K, 1, sq, nw, eps,
+                                                        tokens.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                        _lib.stream_of(w)), "linear_argmax (packed)")
+            return y
+        y = linear(x, pw)
+        argmax_rows(y, tokens)
+        return y
     if hip_ok(x, w) and _lib.lib().ns_gemm_argmax_fused(M, N, K) == 1:
         ws = argmax_workspace(w.device)
         if ws is not None:
@@ -169,7 +256,17 @@ def linear_argmax(x, w: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
     return y
 
 
-def linear_silu_mul(x, w_gate_up: torch.Tensor) -> torch.Tensor:
+def linear_silu_mul(x, w_gate_up) -> torch.Tensor:
+    w_gate_up, pw = _split(w_gate_up, x.shape[0])
+    if pw is not None and skinny_ok(x, w_gate_up):
+        M, K = x.shape
+        N2 = w_gate_up.shape[0]
+        out = torch.empty(M, N2 // 2, device=x.device, dtype=x.dtype)
+        wsp, wsn = _pk_ws(x, pw)
+        xp, sq, nw, eps = _x_args(x)
+        _lib.check(_lib.lib().ns_gemm_silu_mul_packed(xp, pw.p.data_ptr(), out.data_ptr(), M, N2, K, 1, sq, nw, eps,
+                                                      wsp, wsn, _lib.stream_of(w_gate_up)), "linear_silu_mul (packed)")
+        return out
     if not hip_ok(x, w_gate_up):
         return silu_mul(F.linear(_dense(x), w_gate_up))
     if not skinny_ok(x, w_gate_up):
@@ -184,10 +281,25 @@ def linear_silu_mul(x, w_gate_up: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor | None,
+def linear_residual_rms_norm(x: torch.Tensor, w, residual: torch.Tensor, norm_w: torch.Tensor | None,
                              eps: float):
     """(rms_norm(residual + x W^T), residual + x W^T) with the sum rounded to the dtype; norm_w None -> (None, sum).
     x [M, K], residual [M, N]. On the skinny route the first element is a NormedRows."""
+    w, pw = _split(w, x.shape[0])
+    if (pw is not None and skinny_ok(x, w) and residual.is_contiguous() and w.shape[0] % 8 == 0
+            and residual.data_ptr() % 16 == 0):
+        M, K = x.shape
+        N = w.shape[0]
+        res_out = torch.empty(M, N, device=x.device, dtype=x.dtype)
+        sumsq = (torch.empty(-(-N // NORM_COLS), NORM_ROWS, device=x.device, dtype=torch.float32)
+                 if norm_w is not None else None)
+        wsp, wsn = _pk_ws(x, pw)
+        _lib.check(_lib.lib().ns_gemm_residual_norm_stats_packed(
+            x.data_ptr(), pw.p.data_ptr(), residual.data_ptr(), res_out.data_ptr(), _lib.ptr(sumsq), M, N, K, 1, wsp, wsn,
+            _lib.stream_of(x)), "linear_residual_rms_norm (packed)")
+        if norm_w is None:
+            return None, res_out
+        return NormedRows(res_out, sumsq, norm_w, eps), res_out
     if not skinny_ok(x, w) or not residual.is_contiguous() or w.shape[0] % 8 != 0:
         y = linear(x, w)
         if norm_w is None:
@@ -206,8 +318,27 @@ def linear_residual_rms_norm(x: torch.Tensor, w: torch.Tensor, residual: torch.T
     return NormedRows(res_out, sumsq, norm_w, eps), res_out
 
 
-def linear_rope_qkv(x, w: torch.Tensor, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
+def linear_rope_qkv(x, w, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
                     n_heads: int, n_kv_heads: int, head_dim: int, k_cache=None, v_cache=None, slots=None):
+    w, pw = _split(w, x.shape[0])
+    if (pw is not None and skinny_ok(x, w) and head_dim in (64, 128) and cos.is_contiguous() and sin.is_contiguous()
+            and all(t is None or t.data_ptr() % 16 == 0 for t in (b, cos, sin, k_cache, v_cache))):
+        M, K = x.shape
+        N = w.shape[0]
+        assert N == (n_heads + 2 * n_kv_heads) * head_dim and cos.shape == (M, head_dim) and sin.shape == (M, head_dim)
+        if k_cache is not None:
+            assert k_cache.is_contiguous() and v_cache.is_contiguous() and slots.dtype == torch.int64
+            assert slots.shape == (M,) and slots.is_contiguous()
+        q = torch.empty(M, n_heads, head_dim, device=x.device, dtype=x.dtype)
+        k = torch.empty(M, n_kv_heads, head_dim, device=x.device, dtype=x.dtype)
+        v = torch.empty_like(k)
+        wsp, wsn = _pk_ws(x, pw)
+        xp, sq, nw, eps = _x_args(x)
+        _lib.check(_lib.lib().ns_gemm_rope_qkv_packed(
+            xp, pw.p.data_ptr(), _lib.ptr(b), cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr(),
+            v.data_ptr(), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(slots) if k_cache is not None else None,
+            M, K, n_heads, n_kv_heads, head_dim, 1, sq, nw, eps, wsp, wsn, _lib.stream_of(w)), "linear_rope_qkv (packed)")
+        return q, k, v
     fits = (hip_ok(x, w) and head_dim in (64, 128) and cos.is_contiguous() and sin.is_contiguous()
             and _lib.lib().ns_gemm_rope_qkv_fits(x.shape[0], x.shape[1], n_heads, n_kv_heads, head_dim,
                                                  int(isinstance(x, NormedRows))) == 1)

@@ -104,6 +104,11 @@ class LayerWeights:
     qkv_w: torch.Tensor | None = None     # merged [q; k; v] rows (per-matrix fields become views)
     qkv_b: torch.Tensor | None = None
     gate_up_w: torch.Tensor | None = None  # merged [gate; up] rows
+    # fragment-packed copies for decode-sized products (kernels/linear.py PackedWeight), bf16 on the GPU
+    qkv_p: object | None = None
+    o_p: object | None = None
+    gate_up_p: object | None = None
+    down_p: object | None = None
 
     HF_NAMES = {
         "ln1": "input_layernorm.weight",
@@ -190,7 +195,9 @@ class Qwen2Model:
 
     fused = True
 
-    def __init__(self, cfg: ModelConfig, state_dict: dict[str, torch.Tensor]):
+    def __init__(self, cfg: ModelConfig, state_dict: dict[str, torch.Tensor], pack: bool | None = None):
+        """pack: also store the projection weights fragment-packed for decode-sized steps (default: bf16 on the
+        GPU; the packed copies add the size of the layer and LM-head weights once more)."""
         self.cfg = cfg
         self.embed = state_dict["model.embed_tokens.weight"]
         self.norm = state_dict["model.norm.weight"]
@@ -203,6 +210,27 @@ class Qwen2Model:
         # RoPE inverse frequencies, fp32, computed on the CPU like HF, then moved
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float) / cfg.head_dim))
         self.inv_freq = inv.to(self.device)
+        self.lm_head_p = None
+        if pack is None:
+            pack = self.dtype == torch.bfloat16 and self.device.type == "cuda"
+        if pack:
+            self._pack()
+
+    def _pack(self) -> None:
+        """Fragment-packed copies of every projection weight (kernels/linear.py PackedWeight)."""
+        from nanoserve_amd.kernels.linear import PACK_GATE_UP, PACK_ROPE, PackedWeight
+        cfg = self.cfg
+        if cfg.hidden_size % 32 or cfg.intermediate_size % 32 or (cfg.n_heads * cfg.head_dim) % 32:
+            return
+        for layer in self.layers:
+            layer.qkv_p = PackedWeight(layer.qkv_w, PACK_ROPE, cfg.head_dim) if cfg.head_dim in (64, 128) else None
+            layer.o_p = PackedWeight(layer.o_w)
+            layer.gate_up_p = PackedWeight(layer.gate_up_w, PACK_GATE_UP)
+            # down (K = intermediate > 2048): its packed plan would slice K, and the slice merge costs more
+            # than the row-major kernel's streaming, so it stays row-major only
+            if cfg.intermediate_size <= 2048:
+                layer.down_p = PackedWeight(layer.down_w)
+        self.lm_head_p = PackedWeight(self.lm_head.contiguous())
 
     @classmethod
     def from_pretrained(cls, folder: str, device: str | torch.device = "cuda",
@@ -257,7 +285,7 @@ class Qwen2Model:
         """QKV projection (+ bias) of the normed activations h [N, H], RoPE, K/V stored at the slots."""
         from nanoserve_amd.kernels.linear import linear_rope_qkv
         layer, cfg = self.layers[i], self.cfg
-        q, k, v = linear_rope_qkv(h, layer.qkv_w, layer.qkv_b, cos[0], sin[0], cfg.n_heads, cfg.n_kv_heads,
+        q, k, v = linear_rope_qkv(h, layer.qkv_p or layer.qkv_w, layer.qkv_b, cos[0], sin[0], cfg.n_heads, cfg.n_kv_heads,
                                   cfg.head_dim, paged.k[i] if paged is not None else None,
                                   paged.v[i] if paged is not None else None, slot_mapping)
         return q[None], k[None], v[None]
@@ -267,9 +295,9 @@ class Qwen2Model:
         next layer's ln1 or the final norm) is applied in the same epilogue. x, o 2-D -> (h_next, x)."""
         from nanoserve_amd.kernels.linear import linear_residual_rms_norm, linear_silu_mul
         layer, eps = self.layers[i], self.cfg.rms_norm_eps
-        h, x = linear_residual_rms_norm(o, layer.o_w, x, layer.ln2, eps)
-        a = linear_silu_mul(h, layer.gate_up_w)
-        return linear_residual_rms_norm(a, layer.down_w, x, next_norm, eps)
+        h, x = linear_residual_rms_norm(o, layer.o_p or layer.o_w, x, layer.ln2, eps)
+        a = linear_silu_mul(h, layer.gate_up_p or layer.gate_up_w)
+        return linear_residual_rms_norm(a, layer.down_p or layer.down_w, x, next_norm, eps)
 
     def _post(self, i: int, x: torch.Tensor, o: torch.Tensor) -> torch.Tensor:
         """o_proj + residual (fused into the norm), RMSNorm, SwiGLU MLP + residual. x [1,N,H], o [1,N,nh*hd]."""
@@ -419,17 +447,20 @@ class Qwen2Model:
             idx = ends
         if idx is not None:
             x = x.rows(idx) if isinstance(x, NormedRows) else x[idx]
-        # Up to 32 rows (K <= 2048) the wide LM head runs on persistent workgroups that normalise their
-        # activation fragments once, so it takes the NormedRows itself; beyond that every 64-row tile would
-        # repeat the row-statistics prologue, so the final norm is materialised once instead.
+        # The packed LM head (up to 64 rows) and the row-major persistent one (up to 32 rows, K <= 2048) run on
+        # persistent workgroups that normalise their activation fragments once, so they take the NormedRows
+        # itself; beyond that every 64-row tile would repeat the row-statistics prologue, so the final norm is
+        # materialised once instead.
         if isinstance(x, NormedRows):
-            if x.r.shape[0] > 32 or x.r.shape[1] > 2048:
+            packed = self.lm_head_p is not None and x.r.shape[0] <= 64
+            if not packed and (x.r.shape[0] > 32 or x.r.shape[1] > 2048):
                 x = x.tensor()
         else:
             x = x.contiguous()
+        head = self.lm_head_p or self.lm_head
         if greedy_out is not None:
-            return linear_argmax(x, self.lm_head, greedy_out)
-        return linear(x, self.lm_head)
+            return linear_argmax(x, head, greedy_out)
+        return linear(x, head)
 
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, cache=None, logits: str = "last"):
         """ONE sequence, the single-request API (nanoserve/model.py:364-367), on the paged path. `cache` is a
