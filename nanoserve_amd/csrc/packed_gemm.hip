@@ -16,8 +16,10 @@
 // PK_GATE_UP 8 gate rows + the matching 8 up rows of a merged [gate; up] weight; PK_ROPE 8 dims of a head +
 // the 8 dims half a head further (the rotate-half partners). The same orders as the tile-16 kernel.
 //
-// Kernel (one workgroup per CU, persistent): a work unit is (tile, K slice). Workgroup g owns slice g % sl
-// and walks the units g, g + G, g + 2G, ... (G a multiple of sl). Wave w of the workgroup owns steps
+// Kernel (one workgroup per CU, persistent): a work unit is (tile, K slice). With K whole (sl = 1) workgroup
+// g walks a contiguous block of tiles, so its outputs fill whole lines of its own XCD's L2; with sl > 1 it
+// owns slice g % sl and walks the units g, g + G, g + 2G, ... (G a multiple of sl). Weights are read
+// non-temporally (streamed once). Wave w of the workgroup owns steps
 // [w S, w S + S) of the slice: it loads the matching X fragments once (B operand, 16 tokens x 32 k per
 // fragment; normalised on load for an rms_norm input) and keeps them in registers, then for each unit
 // issues its S weight blocks (S contiguous 1 KB loads), multiplies them as they arrive, and writes its
@@ -249,7 +251,7 @@ constexpr int PK_MERGE = 16;   // slices whose partials one merge round trip loa
 // the compiler's wait counts stay exact (a load guarded by a runtime test turns every later wait into a wait
 // for everything, the previous unit's epilogue stores included). Steps past the wave's share of its slice
 // re-read the slice's last block and multiply zero activations.
-template <int TM, int EPI, bool NX, int NW, int S>
+template <int TM, int EPI, bool NX, int NW, int S, bool BIAS>
 __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
   constexpr int NT = NW * 64;
   constexpr bool PAIR = pk_pair<EPI>();
@@ -322,12 +324,20 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
     for (int mb = 0; mb < TM; ++mb)
       xf[i][mb] = *reinterpret_cast<const g_u32x4_t*>(p.x + int64_t(min(16 * mb + c16, M - 1)) * K +
                                                        32 * min(kb + i, klast) + 8 * r4);
+  // units of this workgroup: a contiguous block of tiles when K is whole (consecutive tiles write adjacent
+  // 32-byte pieces of every output row, which then fill whole lines in this XCD's L2 instead of being
+  // written back piecemeal by eight XCDs; the weights stream contiguously too), else every G-th unit (one
+  // K slice per workgroup)
+  const int ub = p.sl == 1 ? int(int64_t(u0) * units / (p.tb > 1 ? units : G)) : u0;
+  const int ue = p.sl == 1 ? (p.tb > 1 ? u0 + 1 : int(int64_t(int(blockIdx.x) + 1) * units / G)) : units;
+  const int ustep = p.sl == 1 ? 1 : G;
+  const int ulast = p.sl == 1 ? ue - 1 : units - 1;
   g_u32x4_t wr[S];
   auto load_w = [&](int u) __attribute__((always_inline)) {
-    const int t = min(u, units - 1) / p.sl;
+    const int t = min(u, ulast) / p.sl;
     const g_u32x4_t* src = p.wp + int64_t(t) * steps * 64 + lane;
 #pragma unroll
-    for (int i = 0; i < S; ++i) wr[i] = src[int64_t(min(kb + i, klast)) * 64];
+    for (int i = 0; i < S; ++i) wr[i] = __builtin_nontemporal_load(src + int64_t(min(kb + i, klast)) * 64);
   };
   auto load_ops = [&](int u, PkOps (&o)[IPT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -336,9 +346,10 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
       pk_load_ops<EPI>(p, min(u, units - 1) / p.sl, min(it / JPR, M - 1), it % JPR, o[q]);
     }
   };
-  PkOps ops[IPT];
-  if constexpr (EPI != EPI_SILU) load_ops(u0, ops);
-  load_w(u0);
+  constexpr bool OPS = EPI != EPI_SILU && (EPI != EPI_STORE || BIAS);   // epilogue operands per unit
+  PkOps ops[IPT] = {};
+  if constexpr (OPS) load_ops(min(ub, units - 1), ops);
+  load_w(ub);
   if constexpr (NX) {
     if (wv < TM) pk_row_stats_finish(ptiles, M, K, p.xeps, rs, s_inv);
     __syncthreads();
@@ -383,7 +394,7 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
     }
   };
   int par = 0;
-  for (int u = u0; u < units; u += G) {
+  for (int u = ub; u < ue; u += ustep) {
     const int t = u / p.sl;
     g_float4_t acc[TM];
 #pragma unroll
@@ -400,8 +411,8 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
     PkOps cur[IPT];
 #pragma unroll
     for (int q = 0; q < IPT; ++q) cur[q] = ops[q];
-    if constexpr (EPI != EPI_SILU) load_ops(u + G, ops);
-    load_w(u + G);
+    if constexpr (OPS) load_ops(min(u + ustep, ulast), ops);
+    load_w(u + ustep);
     __syncthreads();   // every wave's partial tile of unit u is in red[par]
 #pragma unroll
     for (int q = 0; q < IPT; ++q) {
@@ -446,8 +457,8 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
     for (int jj = 0; jj < nmine; ++jj) {
       if (s_last[jj] == 0u) continue;   // uniform
       const int t = (u0 + jj * G) / p.sl;
-      PkOps o[IPT];
-      if constexpr (EPI != EPI_SILU) load_ops(t * p.sl, o);
+      PkOps o[IPT] = {};
+      if constexpr (OPS) load_ops(t * p.sl, o);
 #pragma unroll
       for (int q = 0; q < IPT; ++q) {
         const int it = tid + q * NT, m = it / JPR, j = it % JPR;
@@ -620,31 +631,43 @@ static int pk_bind(PkArgs& a, const PkPlan& pl, int tiles, void* ws, size_t ws_b
   return NS_OK;
 }
 
-template <int EPI, bool NX, int NW, int S>
+template <int EPI, bool NX, int NW, int S, bool BIAS>
 static void pk_launch_cfg(const PkArgs& a, int grid, hipStream_t st) {
   const dim3 g{unsigned(grid)}, b{unsigned(NW * 64)};
   if constexpr (NW == 8 && S != 7) {   // token-split plans run 16 tokens per workgroup
     if (a.tb > 1) {
-      hipLaunchKernelGGL((packed_gemm_kernel<1, EPI, NX, NW, S>), g, b, 0, st, a);
+      hipLaunchKernelGGL((packed_gemm_kernel<1, EPI, NX, NW, S, BIAS>), g, b, 0, st, a);
       return;
     }
   }
   if (a.M <= 32)
-    hipLaunchKernelGGL((packed_gemm_kernel<2, EPI, NX, NW, S>), g, b, 0, st, a);
+    hipLaunchKernelGGL((packed_gemm_kernel<2, EPI, NX, NW, S, BIAS>), g, b, 0, st, a);
   else
-    hipLaunchKernelGGL((packed_gemm_kernel<4, EPI, NX, NW, S>), g, b, 0, st, a);
+    hipLaunchKernelGGL((packed_gemm_kernel<4, EPI, NX, NW, S, BIAS>), g, b, 0, st, a);
 }
 
-template <int EPI, bool NX>
-static void pk_launch(const PkArgs& a, const PkPlan& pl, hipStream_t st) {
+template <int EPI, bool NX, bool BIAS>
+static void pk_launch_b(const PkArgs& a, const PkPlan& pl, hipStream_t st) {
   static_assert(PK_NCFG == 5, "one case per configuration");
   switch (pl.cfg) {
-    case 0: pk_launch_cfg<EPI, NX, 8, 8>(a, pl.grid, st); break;
-    case 1: pk_launch_cfg<EPI, NX, 8, 6>(a, pl.grid, st); break;
-    case 2: pk_launch_cfg<EPI, NX, 8, 4>(a, pl.grid, st); break;
-    case 3: pk_launch_cfg<EPI, NX, 4, 7>(a, pl.grid, st); break;
-    default: pk_launch_cfg<EPI, NX, 4, 6>(a, pl.grid, st); break;
+    case 0: pk_launch_cfg<EPI, NX, 8, 8, BIAS>(a, pl.grid, st); break;
+    case 1: pk_launch_cfg<EPI, NX, 8, 6, BIAS>(a, pl.grid, st); break;
+    case 2: pk_launch_cfg<EPI, NX, 8, 4, BIAS>(a, pl.grid, st); break;
+    case 3: pk_launch_cfg<EPI, NX, 4, 7, BIAS>(a, pl.grid, st); break;
+    default: pk_launch_cfg<EPI, NX, 4, 6, BIAS>(a, pl.grid, st); break;
   }
+}
+
+// STORE without a bias reads no epilogue operand per unit; every other epilogue reads its operands
+template <int EPI, bool NX>
+static void pk_launch(const PkArgs& a, const PkPlan& pl, hipStream_t st) {
+  if constexpr (EPI == EPI_STORE) {
+    if (a.bias == nullptr) {
+      pk_launch_b<EPI, NX, false>(a, pl, st);
+      return;
+    }
+  }
+  pk_launch_b<EPI, NX, true>(a, pl, st);
 }
 
 static PkArgs pk_args(const void* x, const void* wp, int M, int N, int K, const float* x_sumsq, const void* x_norm_w,
