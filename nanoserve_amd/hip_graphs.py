@@ -177,6 +177,8 @@ class DecodeGraphRunner:
         self._pending: tuple[StepGraph, int, int] | None = None    # prestaged step: (graph, twin, rows)
         self.last: StepGraph | None = None
         self.mempool = torch.cuda.graph_pool_handle()                 # shared by this runner's graphs
+        self.captured_up_front = False
+        self.captures_in_run = 0    # buckets captured by a step after capture_all (a step paid for a capture)
 
     @property
     def captured_buckets(self) -> list[int]:
@@ -195,6 +197,7 @@ class DecodeGraphRunner:
         g = self.graphs.get(B)
         if g is None:
             g = self.graphs[B] = StepGraph(self, B)
+            self.captures_in_run += self.captured_up_front
         return g
 
     def has_graph_for(self, n: int) -> bool:
@@ -207,6 +210,7 @@ class DecodeGraphRunner:
         for B in self.buckets:
             if B <= top:
                 self._graph(B)
+        self.captured_up_front = True
 
     def run(self, tokens: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
             context_lens: list[int]) -> torch.Tensor:
@@ -262,7 +266,7 @@ MIXED_SEQ_BUCKETS = (1, 2, 4, 8)
 class MixedStepGraph:
     """One mixed-step bucket: N + 1 rows, S prefill entries, D decode entries (see the module docstring)."""
 
-    def __init__(self, runner: "MixedGraphRunner", N: int, S: int):
+    def __init__(self, runner: "MixedGraphRunner", N: int, S: int, record: bool):
         self.N, self.S, self.D, self.W = N, S, runner.max_decode, runner.max_blocks
         R, D, W = N + 1, self.D, self.W
         self.garbage_block = runner.garbage_block
@@ -293,9 +297,13 @@ class MixedStepGraph:
 
         self.forward = forward
         self.graph, self.logits = None, None
-        if runner.capture:
+        if record:
             # warm-up and capture run on padding only: no new prefill tokens, decode entries on the garbage block
             self.graph, self.logits = capture(forward, runner.mempool)
+
+    @property
+    def host_bytes(self) -> int:
+        return 2 * self.nbytes + self.greedy.numel() * 8
 
     def _views(self, buf: torch.Tensor, numpy: bool = False):
         R, S, D, W = self.N + 1, self.S, self.D, self.W
@@ -359,26 +367,64 @@ class MixedStepGraph:
             self.logits = self.forward()
 
 
+MIXED_GRAPH_MAX_ROWS = 512   # default bound: mixed steps of more rows run staged, unrecorded (launches are a
+                             # small share of a step that size)
+
+
 class MixedGraphRunner:
-    """Mixed-step graphs of one model and pool, captured on first use per (row bucket, prefill capacity);
-    with capture=False the same staged steps run without being recorded."""
+    """Mixed-step graphs of one model and pool. The recorded set is bounded: row buckets up to
+    max_graph_rows times the prefill capacities a step of at most max_decode sequences can need
+    (graph_keys); capture_all records all of them up front (largest first, so the smaller ones reuse the shared
+    pool's segments), a key of that set met before capture_all is recorded on first use, and bigger steps run
+    the same staged forward without a graph. With capture=False nothing is recorded."""
 
     def __init__(self, model: Qwen2Model, pool: PagedKVCache, max_seq_len: int, max_decode: int,
-                 max_rows: int, garbage_block: int, capture: bool = True):
+                 max_rows: int, garbage_block: int, capture: bool = True, max_graph_rows: int = MIXED_GRAPH_MAX_ROWS):
         self.model, self.pool = model, pool
         self.capture = capture
+        self.max_graph_rows = max_graph_rows
         self.block_size = pool.block_size
         self.max_blocks = math.ceil(max_seq_len / pool.block_size)
         self.max_decode = max_decode
         self.max_rows = max_rows
         self.garbage_block = garbage_block
-        self.graphs: dict[tuple[int, int], MixedStepGraph] = {}
+        self.graphs: dict[tuple[int, int], MixedStepGraph] = {}    # recorded
+        self.staged: dict[tuple[int, int], MixedStepGraph] = {}    # run unrecorded
         self.mempool = torch.cuda.graph_pool_handle()
         self.last: MixedStepGraph | None = None
+        self.captured_up_front = False
+        self.captures_in_run = 0
+        self.device_bytes = 0    # device memory the recorded graphs took (pool segments and input buffers)
 
     @staticmethod
     def bucket(n_rows: int) -> int:
         return max(MIXED_ROW_STEP, -(-n_rows // MIXED_ROW_STEP) * MIXED_ROW_STEP)
+
+    def graph_keys(self) -> list[tuple[int, int]]:
+        """The (row bucket, prefill capacity) pairs this runner records, smallest first."""
+        top_rows = min(self.bucket(self.max_rows), self.max_graph_rows)
+        top_seqs = next(s for s in MIXED_SEQ_BUCKETS if s >= min(self.max_decode, MIXED_SEQ_BUCKETS[-1]))
+        return [(n, s) for n in range(MIXED_ROW_STEP, top_rows + 1, MIXED_ROW_STEP)
+                for s in MIXED_SEQ_BUCKETS if s <= top_seqs]
+
+    @property
+    def host_bytes(self) -> int:
+        """Pinned host memory of the recorded graphs' input twins and token outputs."""
+        return sum(g.host_bytes for g in self.graphs.values())
+
+    def _record(self, key: tuple[int, int]) -> MixedStepGraph:
+        before = torch.cuda.memory_reserved(self.model.device)
+        g = self.graphs[key] = MixedStepGraph(self, *key, record=True)
+        self.device_bytes += torch.cuda.memory_reserved(self.model.device) - before
+        return g
+
+    def capture_all(self) -> None:
+        """Record every key of graph_keys() not recorded yet (no-op with capture=False)."""
+        if self.capture:
+            for key in reversed(self.graph_keys()):
+                if key not in self.graphs:
+                    self._record(key)
+            self.captured_up_front = True
 
     def fits(self, sb) -> bool:
         n_pf = len(sb.seqs) - len(sb.dec_idx)
@@ -389,9 +435,13 @@ class MixedGraphRunner:
     def run(self, sb) -> torch.Tensor:
         n_pf = len(sb.seqs) - len(sb.dec_idx)
         key = (self.bucket(len(sb.token_ids)), next(s for s in MIXED_SEQ_BUCKETS if s >= n_pf))
-        g = self.graphs.get(key)
+        g = self.graphs.get(key) or self.staged.get(key)
         if g is None:
-            g = self.graphs[key] = MixedStepGraph(self, *key)
+            if self.capture and key[0] <= self.max_graph_rows:
+                g = self._record(key)
+                self.captures_in_run += self.captured_up_front
+            else:
+                g = self.staged[key] = MixedStepGraph(self, *key, record=False)
         par = g.par ^ 1
         torch.cuda.current_stream().synchronize()   # the twin about to be rewritten may still be copying
         g.stage(par, sb)

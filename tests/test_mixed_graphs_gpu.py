@@ -52,7 +52,7 @@ def test_config4_mixed_graph_equals_eager_and_follows_the_oracle(hiplib):
     sb.dec_idx = list(range(1536, 1552))
     sb.dec_tables = [t.blocks for t in tabs[1:]]
     sb.dec_lens = [c + 1 for c in ctxs]
-    runner = MixedGraphRunner(model, pool, 2048 + 16, 16, 2048, garbage)
+    runner = MixedGraphRunner(model, pool, 2048 + 16, 16, 2048, garbage, max_graph_rows=2048)
     assert runner.fits(sb)
     graph = runner.run(sb).float().cpu()
     greedy = runner.greedy_tokens(17)
@@ -111,9 +111,15 @@ def test_engine_mixed_graphs_equal_eager_steps(hiplib):
     reqs = [(torch.randint(0, 2048, (int(torch.randint(150, 700, (1,), generator=g)),), generator=g).tolist(), 24)
             for _ in range(10)]
 
-    def run(**kw):
+    def run(capture_first=False, **kw):
         eng = LLMEngine(model, [], max_seq_len=1024, max_num_seqs=8, batch_wait_s=0.0, max_num_batched_tokens=256,
                         kv_cache_tokens=16384, **kw)
+        if capture_first:
+            secs = eng.capture_graphs()
+            st0 = eng.stats
+            print(f"capture_graphs: {secs:.1f} s, decode buckets {st0['graph_buckets']}, mixed keys "
+                  f"{st0['piecewise_buckets']}, mixed graphs {st0['piecewise_graph_bytes'] / 2**20:.1f} MiB device + "
+                  f"{st0['piecewise_graph_host_bytes'] / 2**10:.0f} KiB pinned", flush=True)
         rec = LogitsRecorder(eng)
         ids, outs, steps = {}, {}, 0
         for i, (p, n) in enumerate(reqs[:5]):
@@ -134,6 +140,12 @@ def test_engine_mixed_graphs_equal_eager_steps(hiplib):
     graphed, st, lg_graphed = run()
     print(f"mixed-graph steps {st['piecewise_steps']} of {st['steps']}, buckets {st['piecewise_buckets']}", flush=True)
     assert st["piecewise_graphs"] and st["piecewise_steps"] > 0
+    # every graph captured at start-up: the same streams, and no step captured anything
+    upfront, stu, _ = run(capture_first=True)
+    assert stu["graph_captures_in_run"] == 0 and stu["piecewise_steps"] == st["piecewise_steps"]
+    assert set(st["piecewise_buckets"]) <= set(stu["piecewise_buckets"])
+    assert stu["piecewise_graph_bytes"] > 0 and stu["piecewise_graph_host_bytes"] > 0
+    assert upfront == graphed
     staged, st2, _ = run(cuda_graphs=False)
     assert st2["piecewise_steps"] == 0 and not st2["piecewise_graphs"]
     assert graphed == staged
