@@ -97,30 +97,37 @@ class StepPlan:
     n_decode: int = 0
 
 
+_POLICIES = ("continuous", "static")
+
+
 class Scheduler:
+    """Plans each step from two queues: `waiting` (FIFO, preempted requests re-enter at the front) and
+    `running` (admission order, so its tail is the newest). The constructor's parameters are the reference's
+    (scheduler.py:88-89); kv is the KV manager, or None for unlimited KV (host-logic tests)."""
+
     def __init__(self, policy: str = "continuous", max_num_seqs: int = 8, max_num_batched_tokens: int = 8192,
                  batch_wait_s: float = 0.02, kv=None, chunked_prefill: bool = False):
-        if policy not in ("static", "continuous"):
-            raise ValueError(f"unknown policy {policy!r}")
-        self.policy = policy
-        self.max_num_seqs = max_num_seqs
-        self.max_num_batched_tokens = max_num_batched_tokens
+        if policy not in _POLICIES:
+            raise ValueError(f"scheduler policy must be one of {', '.join(_POLICIES)}; got {policy!r}")
+        self.policy, self.kv, self.chunked_prefill = policy, kv, chunked_prefill
+        self.max_num_seqs, self.max_num_batched_tokens = max_num_seqs, max_num_batched_tokens
         self.batch_wait_s = batch_wait_s
-        self.kv = kv                  # KV manager, or None for unlimited KV (host-logic tests)
-        self.chunked_prefill = chunked_prefill
         self.waiting: deque[Sequence] = deque()
         self.running: list[Sequence] = []
         self.num_preemptions = 0
 
     # ---------------------------------------------------------------------------- request lifetime
     def add(self, seq: Sequence) -> None:
-        if not self.chunked_prefill and seq.n_prompt > self.max_num_batched_tokens:
-            raise ValueError(f"prompt of {seq.n_prompt} tokens exceeds the per-step token budget "
-                             f"({self.max_num_batched_tokens}) and chunked prefill is off")
-        worst = seq.n_prompt + seq.max_new_tokens
-        if self.kv is not None and not self.kv.can_ever_fit(worst):
-            raise ValueError(f"request needs up to {worst} tokens of KV, more than the whole KV budget: "
-                             "it could never finish")
+        """Queue a request; reject at once one that no step could take (a prompt over the token budget when
+        prompts cannot be split) or that could not finish even with the whole KV pool to itself."""
+        budget = self.max_num_batched_tokens
+        if seq.n_prompt > budget and not self.chunked_prefill:
+            raise ValueError(f"cannot schedule a {seq.n_prompt}-token prompt: steps carry at most {budget} tokens "
+                             "and prompts are not split (chunked_prefill=False)")
+        need = seq.n_prompt + seq.max_new_tokens
+        if self.kv is not None and not self.kv.can_ever_fit(need):
+            raise ValueError(f"cannot schedule a request that may reach {need} tokens: the KV pool holds fewer, "
+                             "so it could never finish")
         seq.status = SeqStatus.WAITING
         self.waiting.append(seq)
 
@@ -162,11 +169,13 @@ class Scheduler:
                 self._evict_newest()   # possibly running[i] itself: then i == len(running) and the loop ends
 
     def _admission_open(self, now: float) -> bool:
-        if self.policy == "continuous":
+        """Continuous batching admits every step. Static batching forms a batch only once the previous one has
+        drained, and only when a full batch is queued or its oldest request has waited batch_wait_s."""
+        if self.policy != "static":
             return True
-        if self.running or not self.waiting:
-            return False
-        return len(self.waiting) >= self.max_num_seqs or now - self.waiting[0].arrival_time >= self.batch_wait_s
+        idle = not self.running and bool(self.waiting)
+        full = len(self.waiting) >= self.max_num_seqs
+        return idle and (full or now - self.waiting[0].arrival_time >= self.batch_wait_s)
 
     def _head_fits(self, budget: int, n_admitted: int) -> bool:
         if not self.waiting or len(self.running) + n_admitted >= self.max_num_seqs:
