@@ -85,17 +85,19 @@ def gated_region_time(fn, n: int) -> float:
     return e0.elapsed_time(e1)
 
 
-def paged_attention_roofline() -> dict:
-    from nanoserve_amd.kernels.paged_attention import paged_attention_decode
-    B, NH, NKV, HD, NB, W, R = 32, 14, 2, 64, 65536, 256, 8
-    g = torch.Generator().manual_seed(2)
+def _attention_draws(B: int, NH: int, NKV: int, HD: int, ctx_lo: int, ctx_hi: int, W: int, R: int = 8,
+                     NB: int = 65536, seed: int = 2):
+    """R disjoint draws of a decode-attention call: contexts U[ctx_lo, ctx_hi], 16-token pages scattered by one
+    random permutation of an NB-block pool (the draws never share a page, so round-robin calls cannot be
+    served from the Infinity Cache). Returns the pools and [(q, tables, ctx, algorithmic bytes)]."""
+    g = torch.Generator().manual_seed(seed)
     dev = "cuda"
     k = torch.randn(NB, 16, NKV, HD, device=dev, dtype=torch.bfloat16)
     v = torch.randn(NB, 16, NKV, HD, device=dev, dtype=torch.bfloat16)
     perm = torch.randperm(NB, generator=g)
     draws, used = [], 0
     for _ in range(R):
-        ctx = torch.randint(512, 4097, (B,), generator=g).tolist()
+        ctx = torch.randint(ctx_lo, ctx_hi + 1, (B,), generator=g).tolist()
         t = torch.zeros(B, W, dtype=torch.int32)
         for i, c in enumerate(ctx):
             n = -(-c // 16)
@@ -104,25 +106,59 @@ def paged_attention_roofline() -> dict:
         q = torch.randn(B, NH, HD, generator=g).to(torch.bfloat16)
         nbytes = (sum(ctx) * NKV * HD * 2 * 2 + 2 * B * NH * HD * 2 + 4 * sum(-(-c // 16) for c in ctx) + 4 * B)
         draws.append((q.to(dev), t.to(dev), torch.tensor(ctx, dtype=torch.int32, device=dev), nbytes))
+    return k, v, draws
+
+
+def _attention_us(k, v, draws, HD: int, products: str = "mfma", n: int = 400) -> float:
+    """us per call of n back-to-back calls over the draws (round robin), after one warm pass."""
+    from nanoserve_amd.kernels.paged_attention import paged_attention_decode
     scale = HD ** -0.5
     for q, t, c, _ in draws:
-        paged_attention_decode(q, k, v, t, c, scale)
+        paged_attention_decode(q, k, v, t, c, scale, products=products)
     it = iter(range(10 ** 9))
 
     def call():
-        q, t, c, _ = draws[next(it) % R]
-        paged_attention_decode(q, k, v, t, c, scale)
+        q, t, c, _ = draws[next(it) % len(draws)]
+        paged_attention_decode(q, k, v, t, c, scale, products=products)
 
-    for _ in range(2 * R):                          # one warm pass over the draws
+    for _ in range(2 * len(draws)):
         call()
-    ms = gated_region_time(call, 400) / 400
-    avg_bytes = sum(d[3] for d in draws) / R
-    achieved = avg_bytes / (ms * 1e-3) / 1e9
+    return gated_region_time(call, n) / n * 1e3
+
+
+def paged_attention_roofline() -> dict:
+    HD = 64
+    k, v, draws = _attention_draws(32, 14, 2, HD, 512, 4096, 256)
+    us = _attention_us(k, v, draws, HD)
+    avg_bytes = sum(d[3] for d in draws) / len(draws)
+    achieved = avg_bytes / (us * 1e-6) / 1e9
     del k, v
     return {"bound": "hbm", "kernel": "paged_attention_decode (split-K partitions merged in the same launch), BASELINE config 2",
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": pmc_traffic(),
-            "bytes_per_launch": int(avg_bytes), "us_per_launch": round(ms * 1e3, 2)}
+            "bytes_per_launch": int(avg_bytes), "us_per_launch": round(us, 2)}
+
+
+def attention_ab() -> dict:
+    """The decode-attention kernel with its two products on the matrix cores (the product) and on the vector
+    ALUs (ns_paged_attn_decode_valu: same partitions, loads and merge), alternating three times (best of
+    three per side), at BASELINE config 2 (14 q / 2 kv heads, hd 64, ctx U[512, 4096], table width 256) and at
+    config 3's attention (the 1.5B decode step: 12 / 2 heads, hd 128, ctx U[1025, 1152], table width 73): us
+    per call and fraction of HBM peak."""
+    out = {}
+    for name, (NH, NKV, HD, lo, hi, W) in (("config2", (14, 2, 64, 512, 4096, 256)),
+                                           ("config3", (12, 2, 128, 1025, 1152, 73))):
+        k, v, draws = _attention_draws(32, NH, NKV, HD, lo, hi, W)
+        avg_bytes = sum(d[3] for d in draws) / len(draws)
+        t = {"mfma": [], "valu": []}
+        for _ in range(3):
+            for prod in ("mfma", "valu"):
+                t[prod].append(_attention_us(k, v, draws, HD, prod))
+        out[name] = {prod: {"us_per_call": round(min(x), 2),
+                            "frac": round(avg_bytes / (min(x) * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)} for prod, x in t.items()}
+        del k, v, draws
+        torch.cuda.empty_cache()
+    return out
 
 
 def decode_run(model, prompts: list[list[int]], K: int, W: int, prefix_caching: bool = False,
@@ -656,6 +692,8 @@ def main() -> int:
     ap.add_argument("--no-prefix-sharing", action="store_true", help="skip the config-5 prefix-sharing decode run")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the paged-attention roofline and the copy calibration (for rocprofv3 --pmc passes)")
+    ap.add_argument("--attention-ab", action="store_true",
+                    help="only the decode-attention kernel with MFMA vs VALU products at configs 2 and 3")
     ap.add_argument("--mixed-only", action="store_true",
                     help="only the config-4 mixed step, graphed and eager (for rocprofv3 kernel traces)")
     ap.add_argument("--ops-only", action="store_true",
@@ -667,6 +705,12 @@ def main() -> int:
               "scale the per-GPU number with no exchange); run it with --gpus 1", file=sys.stderr)
         return 2
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    if args.attention_ab:
+        ab = attention_ab()
+        log("attention A/B (us per call, mfma vs valu): " + ", ".join(
+            f"{k}: {v['mfma']['us_per_call']} vs {v['valu']['us_per_call']}" for k, v in ab.items()))
+        print(json.dumps({"attention_ab": ab}), flush=True)
+        return 0
     if args.attention_only:
         roof = paged_attention_roofline()
         log(f"paged attention: {roof['us_per_launch']} us/call, {roof['achieved']} GB/s")

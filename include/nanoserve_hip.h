@@ -76,6 +76,24 @@ int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                          int max_blocks, int num_blocks, float scale, int dtype,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * ns_paged_attn_decode with the two products on the vector ALUs instead of the matrix cores: same arguments,
+ * partitions, loads and merge; per lane fp32 FMAs over its 8 dims of a token and wave64 shuffle sums for the
+ * scores (probabilities rounded to bf16 before P.V as in the MFMA kernel). bf16 whole-row shapes only
+ * (n_kv * head_dim == 128, or head_dim 128 with several KV heads) with a GQA group of at most 8 (6 for
+ * head_dim 128 with several KV heads). No counterpart in the reference: it exists to measure the MFMA design
+ * choice against the VALU one on the same kernel (bench.py --attention-ab). Results agree with
+ * ns_paged_attn_decode within bf16 tolerances, not bitwise (another summation order).
+ */
+int ns_paged_attn_decode_valu(const void* q, int64_t q_sb, int64_t q_sh,
+                              const void* k_pool, const void* v_pool,
+                              int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                              const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                              void* out, int64_t o_sb, int64_t o_sh,
+                              int B, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                              int max_blocks, int num_blocks, float scale, int dtype,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 size_t ns_decode_workspace_bytes(int B, int n_kv_heads, int head_dim, int max_blocks, int dtype);
 
 /*

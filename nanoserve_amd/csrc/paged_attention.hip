@@ -353,6 +353,7 @@ __global__ __launch_bounds__(DecodeCfg<HD>::NW * 64) void paged_decode_bf16_kern
 //     to arrive loads MB partitions per round trip and folds them in partition order.
 constexpr int ROWK_NW = 8, ROWK_PPW = 4, ROWK_D = 2, ROWK_PART = ROWK_NW * ROWK_PPW;
 constexpr int ROWK_MB = 8;
+constexpr int ROWK_VALU_G = 8, ROWK_VALU_G_PH = 6;   // query heads per KV head the VALU variant takes
 constexpr int ROWK_MAX_PARTS = 32;
 typedef __attribute__((ext_vector_type(4))) unsigned int rk_u32x4_t;
 typedef __attribute__((ext_vector_type(2))) unsigned int rk_u32x2_t;
@@ -387,7 +388,7 @@ constexpr int rows_lds_bytes() {
 // PH: each KV head is a workgroup row of its own (hd 128, several KV heads); otherwise a row is a token's
 // whole 256-byte K row. bid: the workgroup's index among the launch's decode-row workgroups; lds (at least
 // rows_lds_bytes<HD>()), sm_m, sm_l, s_last: the launch's LDS.
-template <int HD, bool PH>
+template <int HD, bool PH, bool VALU = false>
 __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, unsigned char* lds,
                                                  float (*sm_m)[16], float (*sm_l)[16], unsigned& s_last) {
   const bf16_t* __restrict__ q = ra.q;
@@ -449,6 +450,26 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
       qf[s] = __builtin_bit_cast(bf16x8_t, u);
     }
   }
+  // VALU variant: lane (c16, r4) holds dims 8 c16 .. 8 c16 + 7 of the token row, i.e. of KV head gk, and takes
+  // those dims of each query head of gk from the wave's LDS page (staged once; registers go to the
+  // accumulators); whole scores come from a sum over the head's HD / 8 lanes
+  constexpr int GV = VALU ? (PH ? ROWK_VALU_G_PH : ROWK_VALU_G) : 1;
+  const int gk = (8 * c16) / HD;
+  if constexpr (VALU) {
+    unsigned char* qlds = lds + w * (16 * 256);
+    if (r4 < 2) {
+#pragma unroll
+      for (int j = 0; j < GV / 2; ++j) {
+        const int i = 2 * j + r4, hi = gk * G + i;
+        const bool live = i < G && hi < nq_w;
+        const rk_u32x4_t u = *reinterpret_cast<const rk_u32x4_t*>(q + qb * q_sb + int64_t(g * G + (live ? hi : 0)) * q_sh +
+                                                                 ((8 * c16) & (HD - 1)));
+        *reinterpret_cast<rk_u32x4_t*>(qlds + (c16 * GV + i) * 16) = live ? u : rk_u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's q rows are in LDS before any lane reads them
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  }
   int n_pages = ctx > 0 ? (ctx + PAGE - 1) / PAGE : 0;
   if (n_pages > max_blocks) n_pages = max_blocks;
   if (ctx <= 0) {   // no keys: zeros
@@ -485,12 +506,72 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   float4_t acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float vm[GV], vl[GV], vacc[GV][8];   // VALU variant: per query head of gk, this lane's 8 dims
+#pragma unroll
+  for (int i = 0; i < GV; ++i) {
+    vm[i] = -INFINITY;
+    vl[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vacc[i][e] = 0.f;
+  }
   const int tr = 4 * (c16 & 3) + (c16 >> 2);   // token of S^T row c16
   auto page = [&](int i, auto sc) __attribute__((always_inline)) {
     constexpr int sl = decltype(sc)::value;
     const int p = p0 + w + NW * i;
     const int bid = __builtin_amdgcn_readlane(blk_lane, i);
     const bool okp = bid >= 0 && bid < num_blocks;
+    if constexpr (VALU) {
+      // lane (c16, r4) has tokens 4 k + r4 (k < 4), dims 8 c16 .. 8 c16 + 7 of K and V
+      bool valid[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) valid[k] = okp && (p * PAGE + 4 * k + r4) < ctx;
+#pragma unroll
+      for (int h = 0; h < GV; ++h) {   // one query head at a time (its scores, softmax update and P.V)
+        const rk_u32x4_t qh = *reinterpret_cast<const rk_u32x4_t*>(kpg + (c16 * GV + h) * 16);
+        float s4[4], mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float a = 0.f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t kw = kr[sl][k][e], qw = qh[e];
+            a = fmaf(__uint_as_float(kw << 16), __uint_as_float(qw << 16), a);
+            a = fmaf(__uint_as_float(kw & 0xffff0000u), __uint_as_float(qw & 0xffff0000u), a);
+          }
+#pragma unroll
+          for (int o = 1; o < HD / 8; o <<= 1) a += __shfl_xor(a, o, 64);   // the head's HD / 8 chunks
+          s4[k] = valid[k] ? a * scale_log2 : -INFINITY;
+          mx = fmaxf(mx, s4[k]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(vm[h], mx);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(vm[h] - m_use);
+        float pb[4], psum = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float pv = exp2f(s4[k] - m_use);
+          psum += pv;
+          pb[k] = valid[k] ? __uint_as_float(uint32_t(f32_to_bf16(pv)) << 16) : 0.f;   // P rounded to bf16
+        }
+        vl[h] = vl[h] * alpha + psum;
+        vm[h] = m_new;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vacc[h][e] *= alpha;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t vw = vr[sl][k][e];
+            const float v0 = valid[k] ? __uint_as_float(vw << 16) : 0.f;
+            const float v1 = valid[k] ? __uint_as_float(vw & 0xffff0000u) : 0.f;
+            vacc[h][2 * e] = fmaf(pb[k], v0, vacc[h][2 * e]);
+            vacc[h][2 * e + 1] = fmaf(pb[k], v1, vacc[h][2 * e + 1]);
+          }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = 4 * j + r4;
@@ -582,15 +663,42 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   }
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
+  if constexpr (VALU) {   // sums over the four token groups r4
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      vl[h] += __shfl_xor(vl[h], 16, 64);
+      vl[h] += __shfl_xor(vl[h], 32, 64);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vacc[h][e] += __shfl_xor(vacc[h][e], 16, 64);
+        vacc[h][e] += __shfl_xor(vacc[h][e], 32, 64);
+      }
+    }
+  }
 
   // ---- merge the waves through LDS: [wave][query][dim]; a lane keeps the O^T rows of its query's head
   __syncthreads();   // every wave is done with its K page: the buffer is reused
   float* sm_acc = reinterpret_cast<float*>(lds);
-  if (r4 == 0) {
+  if constexpr (VALU) {
+    if (r4 == 0) {
+#pragma unroll
+      for (int h = 0; h < GV; ++h) {
+        const int hi = gk * G + h;
+        if (h < G && hi < nq_w) {
+          if ((c16 & (HD / 8 - 1)) == 0) {
+            sm_m[w][hi] = vm[h];
+            sm_l[w][hi] = vl[h];
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm_acc[(w * 16 + hi) * AROW + ((8 * c16) & (HD - 1)) + e] = vacc[h][e];
+        }
+      }
+    }
+  } else if (r4 == 0) {
     sm_m[w][c16] = m_run;
     sm_l[w][c16] = l_run;
   }
-  {
+  if constexpr (!VALU) {
     const int head = NKV == 2 ? (r4 >> 1) : 0;   // rows 4 r4 + k are chunks of head (4 r4 + k) / (HD / 8)
     if (head == gq) {
 #pragma unroll
@@ -705,12 +813,12 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   }
 }
 
-template <int HD, bool PH>
+template <int HD, bool PH, bool VALU>
 __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(RowsArgs a) {
   __shared__ __align__(16) unsigned char lds[rows_lds_bytes<HD>()];
   __shared__ float sm_m[ROWK_NW][16], sm_l[ROWK_NW][16];
   __shared__ unsigned s_last;
-  decode_rows_body<HD, PH>(a, int(blockIdx.x), lds, sm_m, sm_l, s_last);
+  decode_rows_body<HD, PH, VALU>(a, int(blockIdx.x), lds, sm_m, sm_l, s_last);
 }
 
 // A mixed step's attention in one launch: workgroups [0, n_dec) are the whole-row decode kernel's for the
@@ -850,13 +958,20 @@ struct RowsLaunch {
   unsigned grid;
   int rgh, head_dim;
 };
-static void launch_rows(const RowsArgs& a, unsigned grid, int rgh, int head_dim, hipStream_t s) {
+template <bool VALU>
+static void launch_rows_v(const RowsArgs& a, unsigned grid, int rgh, int head_dim, hipStream_t s) {
   if (rgh > 1)
-    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true, VALU>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
   else if (head_dim == 64)
-    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false, VALU>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false, VALU>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+}
+static void launch_rows(const RowsArgs& a, unsigned grid, int rgh, int head_dim, hipStream_t s, bool valu = false) {
+  if (valu)
+    launch_rows_v<true>(a, grid, rgh, head_dim, s);
+  else
+    launch_rows_v<false>(a, grid, rgh, head_dim, s);
 }
 
 // defer: when the whole-row kernel takes the call, fill *defer instead of launching (other kernels launch
@@ -866,7 +981,8 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
                                int64_t bt_sb, const int32_t* context_lens, void* out, int64_t o_sb, int64_t o_sh, int B,
                                int n_heads, int n_kv_heads, int head_dim, int block_size, int max_blocks,
                                int num_blocks, float scale, int dtype, void* workspace, size_t workspace_bytes,
-                               void* stream, const int64_t* qrows = nullptr, RowsLaunch* defer = nullptr) {
+                               void* stream, const int64_t* qrows = nullptr, RowsLaunch* defer = nullptr,
+                               bool valu = false) {
   NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "paged_attention_decode: dtype %d not supported",
              dtype);
   NS_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention_decode: head_dim %d not in {64, 128}", head_dim);
@@ -905,6 +1021,8 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
   const float sl2 = scale * LOG2E;
   const int rgh = rows_kernel_grid_heads(n_heads, n_kv_heads, head_dim, kv_spos, kv_sh, max_blocks);
   if (rgh > 0) {
+    NS_REQUIRE(!valu || G <= (rgh > 1 ? ROWK_VALU_G_PH : ROWK_VALU_G),
+               "paged_attention_decode_valu: GQA group %d above %d for this shape", G, rgh > 1 ? ROWK_VALU_G_PH : ROWK_VALU_G);
     const int rparts = rows_parts(max_blocks);
     const int rrows = B * rgh;
     NS_REQUIRE(rrows <= WS_MAX_COUNTERS, "paged_attention_decode: %d rows x KV heads exceed %d", rrows,
@@ -936,9 +1054,11 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
       *defer = RowsLaunch{ra, rgrid, rgh, head_dim};
       return NS_OK;
     }
-    launch_rows(ra, rgrid, rgh, head_dim, s);
+    launch_rows(ra, rgrid, rgh, head_dim, s, valu);
     return check_launch("paged_attention_decode(bf16 rows)");
   }
+  NS_REQUIRE(!valu, "paged_attention_decode_valu: not a whole-row shape (n_kv * head_dim == 128, or head_dim 128 "
+                    "with several KV heads)");
   const int parts = decode_parts(head_dim, max_blocks);
   const int max_parts = head_dim == 64 ? MERGE_MAX_PARTS<64> : MERGE_MAX_PARTS<128>;
   NS_REQUIRE(parts <= max_parts, "paged_attention_decode: %d partitions (table width %d) exceed %d", parts, max_blocks,
@@ -1051,6 +1171,20 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
   return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
                              context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
                              num_blocks, scale, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ns_paged_attn_decode_valu(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,
+                                         const void* v_pool, int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                                         const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                                         void* out, int64_t o_sb, int64_t o_sh, int B, int n_heads, int n_kv_heads,
+                                         int head_dim, int block_size, int max_blocks, int num_blocks, float scale,
+                                         int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  NS_REQUIRE(dtype == NS_DTYPE_BF16, "paged_attention_decode_valu: bf16 only (dtype %d)", dtype);
+  NS_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= ROWK_VALU_G,
+             "paged_attention_decode_valu: GQA group %d / %d above %d", n_heads, n_kv_heads, ROWK_VALU_G);
+  return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
+                             context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
+                             num_blocks, scale, dtype, workspace, workspace_bytes, stream, nullptr, nullptr, true);
 }
 
 // ---------------------------------------------------------------------------------------------------------

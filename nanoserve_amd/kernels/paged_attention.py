@@ -56,7 +56,12 @@ def decode_workspace(device: torch.device, B: int, n_kv_heads: int, head_dim: in
 
 
 def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
-                           block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float) -> torch.Tensor:
+                           block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                           products: str = "mfma") -> torch.Tensor:
+    """products="valu" runs the same kernel with the QK^T and P.V products on the vector ALUs
+    (ns_paged_attn_decode_valu: bf16 whole-row shapes only), for measuring the matrix-core design choice."""
+    if products not in ("mfma", "valu"):
+        raise ValueError(f"products must be 'mfma' or 'valu', got {products!r}")
     B, n_heads, head_dim = q.shape
     num_blocks, block_size, n_kv_heads, hd2 = k_pool.shape
     assert hd2 == head_dim and q.dtype == k_pool.dtype == v_pool.dtype
@@ -72,7 +77,8 @@ def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
     max_blocks = block_tables.shape[1]
     ws = decode_workspace(q.device, B, n_kv_heads, head_dim, max_blocks, q.dtype)
     L = _lib.lib()
-    _lib.check(L.ns_paged_attn_decode(
+    fn = L.ns_paged_attn_decode if products == "mfma" else L.ns_paged_attn_decode_valu
+    _lib.check(fn(
         q.data_ptr(), q.stride(0), q.stride(1),
         k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
         block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),

@@ -275,3 +275,33 @@ def test_rejects_unsupported_shapes(hiplib):
     k8 = k.view(-1, 8, 2, 64)   # block size 8: the kernels need 16
     with pytest.raises(RuntimeError, match="block_size"):
         paged_attention_decode(q.cuda(), k8.cuda(), k8.cuda(), tables.cuda(), lens.cuda(), 0.1)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,ctx_lens", [
+    (14, 2, 64, None),                      # BASELINE config 2 (whole-row: both KV heads in one 256-byte row)
+    (12, 2, 128, None),                     # the 1.5B decode step's shape (a workgroup row per KV head)
+    (12, 2, 128, CTX_LENS),                 # short and one-page contexts
+    (16, 2, 128, CTX_LENS)])                # group 8 with a row per KV head: beyond its registers -> error
+def test_valu_products_variant(hiplib, n_heads, n_kv, hd, ctx_lens):
+    """The A/B kernel with the QK^T and P.V products on the vector ALUs (ns_paged_attn_decode_valu): the same
+    partitions and merge as the MFMA kernel, so it meets the same fp32-oracle bound and stays within bf16
+    rounding of the MFMA kernel's output; shapes outside its register budget are refused."""
+    from nanoserve_amd.kernels.paged_attention import paged_attention_decode
+    if ctx_lens is None:
+        g = cpu_gen(8)
+        ctx_lens = torch.randint(512, 4097, (32,), generator=g).tolist()
+    q, k, v, tables, lens = make_case(n_heads, n_kv, hd, ctx_lens, torch.bfloat16, seed=9, extra_blocks=16)
+    scale = hd ** -0.5
+    dq, dk, dv, dt, dl = q.cuda(), k.cuda(), v.cuda(), tables.cuda(), lens.cuda()
+    if n_heads // n_kv > (6 if hd == 128 and n_kv > 1 else 8):
+        with pytest.raises(RuntimeError, match="GQA group"):
+            paged_attention_decode(dq, dk, dv, dt, dl, scale, products="valu")
+        return
+    valu = paged_attention_decode(dq, dk, dv, dt, dl, scale, products="valu").cpu().float()
+    valu2 = paged_attention_decode(dq, dk, dv, dt, dl, scale, products="valu").cpu().float()
+    mfma = paged_attention_decode(dq, dk, dv, dt, dl, scale).cpu().float()
+    ref = paged_attention_reference(q.float(), k.float(), v.float(), tables, lens, scale)
+    e_ref, e_mfma = (valu - ref).abs().max().item(), (valu - mfma).abs().max().item()
+    print(f"valu ({n_heads},{n_kv},{hd}) vs oracle {e_ref:.2e}, vs mfma {e_mfma:.2e}")
+    assert e_ref <= 1e-2 and e_mfma <= 1e-2
+    assert torch.equal(valu, valu2)
