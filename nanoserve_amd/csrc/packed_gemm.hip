@@ -327,9 +327,12 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
   // units of this workgroup: a contiguous block of tiles when K is whole (consecutive tiles write adjacent
   // 32-byte pieces of every output row, which then fill whole lines in this XCD's L2 instead of being
   // written back piecemeal by eight XCDs; the weights stream contiguously too), else every G-th unit (one
-  // K slice per workgroup)
-  const int ub = p.sl == 1 ? int(int64_t(u0) * units / (p.tb > 1 ? units : G)) : u0;
-  const int ue = p.sl == 1 ? (p.tb > 1 ? u0 + 1 : int(int64_t(int(blockIdx.x) + 1) * units / G)) : units;
+  // K slice per workgroup). Blocks go to XCDs in runs (workgroup g runs on XCD g % 8 and takes block
+  // (g % 8) G / 8 + g / 8), so each XCD gets an equal contiguous share of the tiles: numbered in launch
+  // order, the blocks one unit longer would all land on the same few XCDs.
+  const int gb = G % 8 == 0 ? (u0 & 7) * (G >> 3) + (u0 >> 3) : u0;
+  const int ub = p.sl == 1 ? (p.tb > 1 ? u0 : int(int64_t(gb) * units / G)) : u0;
+  const int ue = p.sl == 1 ? (p.tb > 1 ? u0 + 1 : int(int64_t(gb + 1) * units / G)) : units;
   const int ustep = p.sl == 1 ? 1 : G;
   const int ulast = p.sl == 1 ? ue - 1 : units - 1;
   g_u32x4_t wr[S];
