@@ -41,6 +41,7 @@ enum PackOrder { PK_ROWS = 0, PK_GATE_UP = 1, PK_ROPE = 2 };
 
 constexpr int PK_SMAX = 8;        // k-steps per wave per unit at most
 constexpr int PK_CU = 256;        // workgroups that stream at once: one per CU
+constexpr int PK_NX_MAX_K = 4 * RS_PRE * G_NORM_COLS;   // longest normalised input (its norm weight in LDS)
 constexpr int PK_MAX_TILES = 8191;
 constexpr int PK_MAX_UNITS_PER_WG = 256;   // sliced units one workgroup may own (merge flags in LDS)
 constexpr size_t PK_CNT_BYTES = sizeof(unsigned) * (PK_MAX_TILES + 1);
@@ -260,6 +261,7 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
   static_assert(TM <= NW && S <= PK_SMAX && NT % JPR == 0, "one statistics wave per 16 rows");
   __shared__ __align__(16) float red[2][NW][TM][256];   // partial tiles (MFMA output layout), double-buffered
   __shared__ float s_inv[G_MAX_M];
+  __shared__ __align__(16) uint32_t s_nw[NX ? 2 * PK_NX_MAX_K / 4 : 4];   // a normalised input's norm weight
   __shared__ unsigned s_last[PK_MAX_UNITS_PER_WG];
   const int G = gridDim.x, tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -307,15 +309,15 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
   const int klast = s0 + slen - 1;                          // last step of the slice (re-read past the share)
   const bool am = p.am_out != nullptr;
 
-  // a normalised input's row statistics and norm-weight fragments first, then X: all of them return
-  // before the weight stream that follows
+  // a normalised input's row statistics and norm weight first, then X: all of them return before the
+  // weight stream that follows. The norm weight goes to LDS once (16 bytes per thread) and each wave reads
+  // its fragments there: a fragment load from memory would be a 1 KB wave access for 64 distinct bytes.
   const int ptiles = (K + G_NORM_COLS - 1) / G_NORM_COLS;
   float rs[RS_PRE];
-  g_u32x4_t nwf[S];
+  g_u32x4_t nwf[S], nw_part = {};
   if constexpr (NX) {
     if (wv < TM) row_stats_issue(p.xsq, ptiles, M, rs);
-#pragma unroll
-    for (int i = 0; i < S; ++i) nwf[i] = *reinterpret_cast<const g_u32x4_t*>(p.xnw + 32 * min(kb + i, klast) + 8 * r4);
+    nw_part = *reinterpret_cast<const g_u32x4_t*>(p.xnw + min(8 * tid, K - 8));
   }
   g_u32x4_t xf[S][TM];
 #pragma unroll
@@ -355,7 +357,10 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
   load_w(ub);
   if constexpr (NX) {
     if (wv < TM) pk_row_stats_finish(ptiles, M, K, p.xeps, rs, s_inv);
+    if (8 * tid < K) *reinterpret_cast<g_u32x4_t*>(s_nw + 4 * tid) = nw_part;
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < S; ++i) nwf[i] = *reinterpret_cast<const g_u32x4_t*>(s_nw + ((32 * min(kb + i, klast) + 8 * r4) >> 1));
     float xinv[TM];
 #pragma unroll
     for (int mb = 0; mb < TM; ++mb) xinv[mb] = s_inv[min(16 * mb + c16, M - 1)];
@@ -691,8 +696,8 @@ static int pk_norm_check(int K, const float* x_sumsq, const void* x_norm_w) {
   NS_REQUIRE((x_sumsq == nullptr) == (x_norm_w == nullptr), "packed gemm: x_sumsq and x_norm_w go together");
   NS_REQUIRE(x_norm_w == nullptr || reinterpret_cast<uintptr_t>(x_norm_w) % 16 == 0,
              "packed gemm: norm weight must be 16-byte aligned");
-  NS_REQUIRE(x_sumsq == nullptr || K <= 4 * RS_PRE * G_NORM_COLS,
-             "packed gemm: a normalised input needs K <= %d (K=%d)", 4 * RS_PRE * G_NORM_COLS, K);
+  NS_REQUIRE(x_sumsq == nullptr || K <= PK_NX_MAX_K, "packed gemm: a normalised input needs K <= %d (K=%d)",
+             PK_NX_MAX_K, K);
   return NS_OK;
 }
 
