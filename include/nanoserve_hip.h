@@ -28,6 +28,10 @@ extern "C" {
 #define NS_DTYPE_F32 0
 #define NS_DTYPE_BF16 1
 
+/* Row statistics of an RMSNorm input (r and, per 16 columns, the row sums of r^2) are fp32
+ * [ceil(n / 16)][NS_NORM_ROWS]: row m of 16-column group p at p * NS_NORM_ROWS + m, for up to NS_NORM_ROWS rows. */
+#define NS_NORM_ROWS 128
+
 /* Split-K workspaces (ns_paged_attn_decode, ns_paged_attn_prefill, ns_argmax_rows) begin with this many
  * bytes of arrival counters. Every call leaves them at zero and nothing else is ever stored there, so one
  * zero-filled workspace may serve calls of any shape, in any order, on one stream. */
@@ -225,7 +229,8 @@ int ns_rope_qkv(const void* qkv, const void* cos, const void* sin, void* q, void
  * The first ops of a forward step in one launch: x[i] = embed[token_ids[i]] ([vocab, hidden], row-major;
  * an id outside [0, vocab) gives a zero row) and the RoPE tables cos/sin[i] = cat(f, f).cos() / .sin()
  * rounded to the dtype, f = float(positions[i]) * inv_freq (fp32 [head_dim / 2]); x_out [n_tokens, hidden],
- * cos/sin [n_tokens, head_dim]. row_sumsq (fp32 [ceil(hidden / 16)][64], may be NULL; n_tokens <= 64 then)
+ * cos/sin [n_tokens, head_dim]. row_sumsq (fp32 [ceil(hidden / 16)][NS_NORM_ROWS], may be NULL; n_tokens <=
+ * NS_NORM_ROWS then)
  * receives the first RMSNorm's statistics in the layout ns_gemm_residual_norm_stats writes, so the first
  * projection can normalise on load. hidden a multiple of 16.
  * Replaces F.embedding (nanoserve/model.py:341) and Qwen2Model.rope (model.py:212-217).
@@ -254,7 +259,7 @@ size_t ns_gemm_workspace_bytes(int M, int N, int K);
  * ln2, the LM head after the final norm) take the un-normalised r = residual + ... and normalise each
  * activation fragment as they load it: h = round(w * round(r * inv)), inv = rsqrt(sum / K + eps), where
  * sum adds the per-16-column row sums of r^2 that ns_gemm_residual_norm_stats wrote (x_sumsq, fp32
- * [ceil(K/16)][64], row m at column m) in one fixed order. So the RMSNorm never runs as a separate pass,
+ * [ceil(K/16)][NS_NORM_ROWS], row m at column m) in one fixed order. So the RMSNorm never runs as a separate pass,
  * and every consumer sees bitwise the same h; ns_rms_norm_apply materialises h where a tensor is needed.
  * x_sumsq == NULL: x is used as is (x_norm_w, x_eps ignored).
  */
@@ -301,7 +306,7 @@ int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int
 /*
  * Projection + residual add + the statistics of the RMSNorm that follows: o = round(x W^T);
  * res_out = round(residual + o); row_sumsq[p][m] = sum over columns 16p .. 16p+15 of res_out[m]^2 (fp32,
- * [ceil(N/16)][64], may be NULL). N a multiple of 8.
+ * [ceil(N/16)][NS_NORM_ROWS], may be NULL). N a multiple of 8.
  * With a normalised consumer (or ns_rms_norm_apply) this replaces rms_norm(F.linear(o, o_w), ln2, eps,
  * residual=x) (nanoserve/model.py:256, fused.py:45) and x + F.linear(a, down_w) followed by the next
  * layer's rms_norm (model.py:257, :227-231).

@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void rope_qkv_bf16x8_kernel(const bf16_t* __re
 // ------------------------------------------------------------------------- embedding + RoPE tables
 // The first ops of a forward step in one launch (nanoserve/model.py:337-342 F.embedding and :212-217
 // rope): x[i] = embed[token_ids[i]]; cos/sin[i] = cat(f, f).cos()/.sin() rounded to the dtype with
-// f = float(positions[i]) * inv_freq (fp32). With row_sumsq given (decode batches, <= 64 rows) it also
+// f = float(positions[i]) * inv_freq (fp32). With row_sumsq given (decode batches, <= NS_NORM_ROWS rows) it also
 // writes the statistics the first RMSNorm takes on load: row_sumsq[p][i] = sum over columns 16p .. 16p+15
 // of x[i]^2. A token id outside [0, vocab) yields a zero row. One workgroup of 256 threads per token.
 template <typename T>
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void embed_rope_kernel(const int64_t* __restri
     }
 #pragma unroll
     for (int o = 1; o < TPG; o <<= 1) ss += __shfl_xor(ss, o, 64);
-    if (row_sumsq != nullptr && c < hidden && (tid % TPG) == 0) row_sumsq[int64_t(c / 16) * 64 + i] = ss;
+    if (row_sumsq != nullptr && c < hidden && (tid % TPG) == 0) row_sumsq[int64_t(c / 16) * NS_NORM_ROWS + i] = ss;
   }
   const int half = head_dim >> 1;
   if (tid < half) {
@@ -456,7 +456,7 @@ extern "C" int ns_embed_rope(const int64_t* token_ids, const int64_t* positions,
   NS_REQUIRE(hidden > 0 && hidden % 16 == 0, "embed_rope: hidden %d must be a positive multiple of 16", hidden);
   NS_REQUIRE(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 512, "embed_rope: head_dim %d (even, <= 512)", head_dim);
   NS_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t(1) << 31), "embed_rope: n_tokens %lld", (long long)n_tokens);
-  NS_REQUIRE(row_sumsq == nullptr || n_tokens <= 64, "embed_rope: row statistics need <= 64 tokens, got %lld",
+  NS_REQUIRE(row_sumsq == nullptr || n_tokens <= NS_NORM_ROWS, "embed_rope: row statistics need <= %d tokens, got %lld", NS_NORM_ROWS,
              (long long)n_tokens);
   NS_REQUIRE((reinterpret_cast<uintptr_t>(embed) | reinterpret_cast<uintptr_t>(x_out)) % 16 == 0,
              "embed_rope: embed and x_out must be 16-byte aligned");

@@ -313,7 +313,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const TileSourc
       }
       ss += __shfl_xor(ss, 1, 64);   // columns 16p .. 16p+15 (two 8-column groups)
       if (live && (cq & 1) == 0 && n0 < N && a.sumsq_out != nullptr)
-        a.sumsq_out[int64_t(4 * t + (cq >> 1)) * G_MAX_M + m] = ss;
+        a.sumsq_out[int64_t(4 * t + (cq >> 1)) * G_NORM_ROWS + m] = ss;
     }
   }
 }
@@ -326,7 +326,7 @@ __device__ __forceinline__ float rms_norm_row_inv(const float* sumsq, int ptiles
   for (int p0 = r4; p0 < ptiles; p0 += 32) {   // 8 loads in flight, added in tile order
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = p0 + 4 * e < ptiles ? sumsq[int64_t(p0 + 4 * e) * G_MAX_M + m] : 0.f;
+    for (int e = 0; e < 8; ++e) v[e] = p0 + 4 * e < ptiles ? sumsq[int64_t(p0 + 4 * e) * G_NORM_ROWS + m] : 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) part += v[e];
   }
@@ -343,12 +343,18 @@ __global__ __launch_bounds__(G_WAVES * 64) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int R = 16 * TM;
   // this workgroup's segment: chunks [c0, c1) of tile t (slice s of ks)
   int b = blockIdx.x;
-  if constexpr (EPI == EPI_STORE) {
+  if constexpr (EPI == EPI_STORE || EPI == EPI_RESNORM) {
     if (a.mblocks > 1) {   // token block mb: rows 64 mb .. 64 mb + 63, with its own counters and partials
       const int per = a.whole + (a.tiles - a.whole) * a.ks, mb = b / per;
       b -= mb * per;
       a.x += int64_t(G_MAX_M) * mb * a.K;
-      a.y += int64_t(G_MAX_M) * mb * a.N;
+      if constexpr (EPI == EPI_STORE) {
+        a.y += int64_t(G_MAX_M) * mb * a.N;
+      } else {
+        a.residual += int64_t(G_MAX_M) * mb * a.N;
+        a.res_out += int64_t(G_MAX_M) * mb * a.N;
+        if (a.sumsq_out != nullptr) a.sumsq_out += G_MAX_M * mb;
+      }
       a.M = min(G_MAX_M, a.M - G_MAX_M * mb);
       a.cnt += mb * (a.tiles - a.whole) * a.cstride;
       a.part += int64_t(mb) * (a.tiles - a.whole) * a.ks * G_MAX_M * 64;
@@ -956,7 +962,7 @@ __global__ __launch_bounds__(T16_WAVES * 64) void tile16_gemm_kernel(GemmArgs a)
     ss += __shfl_xor(ss, 4, 64);
     ss += __shfl_xor(ss, 2, 64);
     ss += __shfl_xor(ss, 1, 64);
-    if (elive && en == 0 && a.sumsq_out != nullptr) a.sumsq_out[int64_t(t) * G_MAX_M + em] = ss;
+    if (elive && en == 0 && a.sumsq_out != nullptr) a.sumsq_out[int64_t(t) * G_NORM_ROWS + em] = ss;
   } else if constexpr (EPI == EPI_SILU) {
     const int half = a.N >> 1, oc = 8 * t + en;
     if (elive && oc < half) {
@@ -1450,7 +1456,7 @@ static bool t16_token_split(int M, int tiles) {
 constexpr int T16_LARGE_M = 192;
 constexpr int t16_max_m() { return T16_LARGE_M; }
 static bool t16_large_m(int M, int K, int tiles, bool normed) {
-  return M > G_MAX_M && M <= t16_max_m() && !normed && tile16_fits(K, tiles);
+  return M > G_MAX_M && M <= (normed ? G_NORM_ROWS : t16_max_m()) && tile16_fits(K, tiles);
 }
 template <int EPI, bool NX>
 static void launch_t16_nx(const GemmArgs& a, int tiles, hipStream_t st) {
@@ -1660,7 +1666,8 @@ extern "C" size_t ns_gemm_workspace_bytes(int M, int N, int K) {
   if (M < 1 || N < 1 || K < 32) return 0;
   if (M > G_MAX_M) {
     size_t a = tg_plan(M, N, K, false).bytes, b = tg_plan(M, N, K, true).bytes;
-    if (skinny_large_m(M, K, N)) {
+    // the 64-row token blocks of the skinny kernel (STORE with long K; residual + statistics at any K)
+    if (M <= t16_max_m() && (M + G_MAX_M - 1) / G_MAX_M * ((N + 63) / 64) <= G_MAX_TILES) {
       const size_t c = skinny_large_m_bytes(make_plan((N + 63) / 64, K), (M + G_MAX_M - 1) / G_MAX_M);
       a = a > c ? a : c;
     }
@@ -1676,13 +1683,15 @@ extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, 
   if (st != NS_OK) return st;
   NS_REQUIRE(y != nullptr && aligned16(y), "gemm: output must be 16-byte aligned");
   if (M > G_MAX_M) {
-    NS_REQUIRE(x_sumsq == nullptr, "gemm: a normalised input (x_sumsq) needs M <= %d", G_MAX_M);
-    if (t16_large_m(M, K, (N + 15) / 16, false)) {
+    if (t16_large_m(M, K, (N + 15) / 16, x_sumsq != nullptr)) {
       GemmArgs a = base_args(x, w, M, N, K);
       a.bias = static_cast<const bf16_t*>(bias);
       a.y = static_cast<bf16_t*>(y);
+      if ((st = bind_xnorm(a, x_sumsq, x_norm_w, x_eps)) != NS_OK) return st;
       return launch_t16<EPI_STORE>(a, (N + 15) / 16, reinterpret_cast<hipStream_t>(stream));
     }
+    NS_REQUIRE(x_sumsq == nullptr, "gemm: a normalised input (x_sumsq) above %d rows needs K <= %d and at most %d "
+                                   "rows", G_MAX_M, T16_MAX_K, G_NORM_ROWS);
     if (skinny_large_m(M, K, N)) {
       GemmArgs a = base_args(x, w, M, N, K);
       a.bias = static_cast<const bf16_t*>(bias);
@@ -1757,7 +1766,7 @@ extern "C" int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out,
 extern "C" int ns_gemm_residual_norm_stats(const void* x, const void* w, const void* residual, void* res_out,
                                            float* row_sumsq, int M, int N, int K, int dtype, void* ws,
                                            size_t ws_bytes, void* stream) {
-  int st = check_common(x, w, M, N, K, dtype);
+  int st = check_common(x, w, M, N, K, dtype, G_NORM_ROWS);
   if (st != NS_OK) return st;
   NS_REQUIRE(N % 8 == 0, "gemm_residual_norm_stats: row length %d must be a multiple of 8", N);
   NS_REQUIRE(residual != nullptr && res_out != nullptr, "gemm_residual_norm_stats: residual and res_out required");
@@ -1766,6 +1775,18 @@ extern "C" int ns_gemm_residual_norm_stats(const void* x, const void* w, const v
   a.residual = static_cast<const bf16_t*>(residual);
   a.res_out = static_cast<bf16_t*>(res_out);
   a.sumsq_out = row_sumsq;
+  if (M > G_MAX_M) {   // verify batches: 16-row blocks of the tile-16 kernel, or 64-row blocks of the skinny one
+    if (t16_large_m(M, K, (N + 15) / 16, false))
+      return launch_t16<EPI_RESNORM>(a, (N + 15) / 16, reinterpret_cast<hipStream_t>(stream));
+    NS_REQUIRE((M + G_MAX_M - 1) / G_MAX_M * ((N + 63) / 64) <= G_MAX_TILES,
+               "gemm_residual_norm_stats: M=%d N=%d: too many 64-row token blocks x tiles", M, N);
+    a.mblocks = (M + G_MAX_M - 1) / G_MAX_M;
+    const Plan p = make_plan((N + 63) / 64, K);
+    Plan pm = p;
+    pm.bytes = skinny_large_m_bytes(p, a.mblocks);
+    if ((st = bind_workspace(a, pm, ws, ws_bytes)) != NS_OK) return st;
+    return launch<EPI_RESNORM>(a, reinterpret_cast<hipStream_t>(stream));
+  }
   if (tile16_fits(K, (N + 15) / 16)) return launch_t16<EPI_RESNORM>(a, (N + 15) / 16, reinterpret_cast<hipStream_t>(stream));
   if ((st = bind_workspace(a, make_plan((N + 63) / 64, K), ws, ws_bytes)) != NS_OK) return st;
   return launch<EPI_RESNORM>(a, reinterpret_cast<hipStream_t>(stream));
@@ -1774,8 +1795,8 @@ extern "C" int ns_gemm_residual_norm_stats(const void* x, const void* w, const v
 extern "C" int ns_rms_norm_apply(const void* r, const float* row_sumsq, const void* norm_w, float eps, void* h,
                                  int64_t rows, int n, int dtype, void* stream) {
   NS_REQUIRE(dtype == NS_DTYPE_BF16, "rms_norm_apply: bf16 only (dtype %d)", dtype);
-  NS_REQUIRE(rows >= 0 && rows <= G_MAX_M && n >= 8 && n % 8 == 0, "rms_norm_apply: rows=%lld n=%d (rows <= %d, n %% 8 == 0)",
-             (long long)rows, n, G_MAX_M);
+  NS_REQUIRE(rows >= 0 && rows <= G_NORM_ROWS && n >= 8 && n % 8 == 0,
+             "rms_norm_apply: rows=%lld n=%d (rows <= %d, n %% 8 == 0)", (long long)rows, n, G_NORM_ROWS);
   NS_REQUIRE(r != nullptr && row_sumsq != nullptr && norm_w != nullptr && h != nullptr && aligned16(r) &&
                  aligned16(norm_w) && aligned16(h),
              "rms_norm_apply: null or misaligned operand");

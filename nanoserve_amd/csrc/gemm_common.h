@@ -14,6 +14,7 @@ typedef __attribute__((ext_vector_type(4))) unsigned int g_u32x4_t;   // native 
 enum GemmEpi { EPI_STORE = 0, EPI_SILU = 1, EPI_RESNORM = 2, EPI_ROPE = 3 };
 
 constexpr int G_MAX_M = 64;
+constexpr int G_NORM_ROWS = NS_NORM_ROWS;   // row stride of a row-statistics buffer
 constexpr int G_NORM_COLS = 16;   // columns per row-sum partial of the RMSNorm statistics
 
 // Two fp32 -> packed bf16, round to nearest even, by the hardware conversion (v_cvt_pk_bf16_f32): the same
@@ -53,7 +54,7 @@ constexpr int RS_PRE = 32;
 __device__ __forceinline__ void row_stats_issue(const float* sumsq, int ptiles, int M, float (&v)[RS_PRE]) {
   const int tid = threadIdx.x, m = min(tid >> 2, M - 1), g = tid & 3;
 #pragma unroll
-  for (int e = 0; e < RS_PRE; ++e) v[e] = sumsq[int64_t(min(g + 4 * e, ptiles - 1)) * G_MAX_M + m];
+  for (int e = 0; e < RS_PRE; ++e) v[e] = sumsq[int64_t(min(g + 4 * e, ptiles - 1)) * G_NORM_ROWS + m];
 }
 __device__ __forceinline__ void row_stats_finish(const float* sumsq, int ptiles, int M, int K, float eps,
                                                  const float (&v)[RS_PRE], float* s_inv) {
@@ -62,7 +63,7 @@ __device__ __forceinline__ void row_stats_finish(const float* sumsq, int ptiles,
 #pragma unroll
   for (int e = 0; e < RS_PRE; ++e)
     if (g + 4 * e < ptiles) part += v[e];
-  for (int p = g + 4 * RS_PRE; p < ptiles; p += 4) part += sumsq[int64_t(p) * G_MAX_M + min(m, M - 1)];
+  for (int p = g + 4 * RS_PRE; p < ptiles; p += 4) part += sumsq[int64_t(p) * G_NORM_ROWS + min(m, M - 1)];
   part += __shfl_xor(part, 1, 64);
   part += __shfl_xor(part, 2, 64);
   if (m < M && g == 0) s_inv[m] = rsqrtf(part / float(K) + eps);

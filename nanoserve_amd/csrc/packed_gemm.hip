@@ -441,7 +441,7 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
           ss += __shfl_xor(ss, 1, 64);
           ss += __shfl_xor(ss, 2, 64);
           ss += __shfl_xor(ss, 4, 64);
-          if (it < NI && m < M && j == 0 && p.sumsq_out != nullptr) p.sumsq_out[int64_t(t) * G_MAX_M + m] = ss;
+          if (it < NI && m < M && j == 0 && p.sumsq_out != nullptr) p.sumsq_out[int64_t(t) * G_NORM_ROWS + m] = ss;
         }
       }
     }
@@ -498,7 +498,7 @@ __global__ __launch_bounds__(NW * 64) void packed_gemm_kernel(PkArgs p) {
           ss += __shfl_xor(ss, 1, 64);
           ss += __shfl_xor(ss, 2, 64);
           ss += __shfl_xor(ss, 4, 64);
-          if (it < NI && m < M && j == 0 && p.sumsq_out != nullptr) p.sumsq_out[int64_t(t) * G_MAX_M + m] = ss;
+          if (it < NI && m < M && j == 0 && p.sumsq_out != nullptr) p.sumsq_out[int64_t(t) * G_NORM_ROWS + m] = ss;
         }
       }
     }

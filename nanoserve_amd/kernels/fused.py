@@ -89,8 +89,8 @@ def rope_qkv(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_heads: i
 def embed_rope(token_ids: torch.Tensor, positions: torch.Tensor, embed: torch.Tensor, inv_freq: torch.Tensor,
                head_dim: int, row_stats: bool = False):
     """x = embed[token_ids] [N, H]; cos/sin [N, head_dim] (cat(f, f).cos()/.sin() in the embedding dtype,
-    f = positions.float() * inv_freq); with row_stats (N <= 64) also the first RMSNorm's row statistics
-    sumsq (fp32 [ceil(H / 16), 64]) for a NormedRows, else None."""
+    f = positions.float() * inv_freq); with row_stats (N <= NORM_ROWS) also the first RMSNorm's row statistics
+    sumsq (fp32 [ceil(H / 16), NORM_ROWS]) for a NormedRows, else None."""
     N = token_ids.shape[0]
     V, H = embed.shape
     assert token_ids.dtype == torch.int64 and positions.dtype == torch.int64 and positions.shape == (N,)
@@ -101,7 +101,8 @@ def embed_rope(token_ids: torch.Tensor, positions: torch.Tensor, embed: torch.Te
     x = torch.empty(N, H, device=dev, dtype=dt)
     cos = torch.empty(N, head_dim, device=dev, dtype=dt)
     sin = torch.empty(N, head_dim, device=dev, dtype=dt)
-    sumsq = torch.empty(-(-H // 16), 64, device=dev, dtype=torch.float32) if row_stats else None
+    from nanoserve_amd.kernels.linear import NORM_ROWS
+    sumsq = torch.empty(-(-H // 16), NORM_ROWS, device=dev, dtype=torch.float32) if row_stats else None
     _lib.check(_lib.lib().ns_embed_rope(token_ids.data_ptr(), positions.data_ptr(), N, embed.data_ptr(), V, H,
                                         inv_freq.data_ptr(), head_dim, x.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                                         _lib.ptr(sumsq), _lib.dtype_code(embed), _lib.stream_of(embed)), "embed_rope")

@@ -36,7 +36,7 @@ from nanoserve_amd.kernels.fused import rms_norm, rope_qkv, silu_mul
 
 SKINNY_MAX_M = 64
 NORM_COLS = 16   # columns per row-sum partial of a NormedRows
-NORM_ROWS = 64   # rows the row-sum buffer holds (the skinny GEMMs' largest M)
+NORM_ROWS = 128  # rows the row-sum buffer holds (NS_NORM_ROWS: decode batches and verify batches)
 
 _WS: dict[int, torch.Tensor] = {}
 _WS_RETIRED: list[torch.Tensor] = []   # superseded buffers stay alive: captured graphs may point at them
@@ -59,7 +59,7 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
 
 
 class NormedRows:
-    """rms_norm(r) held as r (bf16 [M, K]) plus the row statistics of r: sumsq (fp32 [ceil(K/16), 64],
+    """rms_norm(r) held as r (bf16 [M, K]) plus the row statistics of r: sumsq (fp32 [ceil(K/16), NORM_ROWS],
     column m = row m, each entry the sum of r^2 over 16 columns), the norm weight [K] and eps."""
 
     def __init__(self, r: torch.Tensor, sumsq: torch.Tensor, weight: torch.Tensor, eps: float):
@@ -300,6 +300,8 @@ def linear_residual_rms_norm(x: torch.Tensor, w, residual: torch.Tensor, norm_w:
         if norm_w is None:
             return None, res_out
         return NormedRows(res_out, sumsq, norm_w, eps), res_out
+    # above 64 rows the plain product and the RMSNorm kernel: the GEMMs' residual epilogue plus a consumer that
+    # normalises on load (or the materialised norm) measured slower on verify batches than the separate pass
     if not skinny_ok(x, w) or not residual.is_contiguous() or w.shape[0] % 8 != 0:
         y = linear(x, w)
         if norm_w is None:
@@ -339,6 +341,8 @@ def linear_rope_qkv(x, w, b: torch.Tensor | None, cos: torch.Tensor, sin: torch.
             v.data_ptr(), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(slots) if k_cache is not None else None,
             M, K, n_heads, n_kv_heads, head_dim, 1, sq, nw, eps, wsp, wsn, _lib.stream_of(w)), "linear_rope_qkv (packed)")
         return q, k, v
+    if isinstance(x, NormedRows) and x.shape[0] > SKINNY_MAX_M:
+        x = _dense(x)   # 16-row token blocks would each normalise their rows again: materialise once
     fits = (hip_ok(x, w) and head_dim in (64, 128) and cos.is_contiguous() and sin.is_contiguous()
             and _lib.lib().ns_gemm_rope_qkv_fits(x.shape[0], x.shape[1], n_heads, n_kv_heads, head_dim,
                                                  int(isinstance(x, NormedRows))) == 1)

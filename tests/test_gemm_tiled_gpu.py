@@ -70,14 +70,58 @@ def test_tiled_split_k_is_deterministic_and_shares_the_workspace(hiplib):
     bf16_check(a.cpu(), ref_linear(x, w), "split-K tiled 96x1536x8960", dot_bound(x, w))
 
 
-def test_tiled_rejects_normalised_input_through_the_c_abi(hiplib):
-    """The C entry point refuses a normalised input above 64 rows (the Python layer materialises it)."""
+def test_normalised_input_above_64_rows_through_the_c_abi(hiplib):
+    """ns_gemm takes a normalised input (r + row statistics) up to NS_NORM_ROWS = 128 rows when the tile-16
+    kernel takes the shape (its 16-row token blocks normalise on load), bitwise equal to the product of the
+    materialised norm; above 128 rows it refuses (the Python layer materialises the input there)."""
     from nanoserve_amd import _lib
-    x, w = operands(65, 256, 256, seed=3)
-    xd, wd = x.cuda(), w.cuda()
-    y = torch.empty(65, 256, dtype=BF, device="cuda")
-    sq = torch.zeros(16, 64, device="cuda")
-    nw = torch.ones(256, dtype=BF, device="cuda")
-    rc = _lib.lib().ns_gemm(xd.data_ptr(), wd.data_ptr(), None, y.data_ptr(), 65, 256, 256, 1, sq.data_ptr(),
-                            nw.data_ptr(), 1e-6, None, 0, _lib.stream_of(xd))
-    assert rc != 0 and b"normalised" in _lib.lib().ns_last_error()
+    from nanoserve_amd.kernels.linear import NORM_ROWS, NormedRows
+    L = _lib.lib()
+    for M in (96, 129):
+        x, w = operands(M, 256, 256, seed=3)
+        xd, wd = x.cuda(), w.cuda()
+        y = torch.empty(M, 256, dtype=BF, device="cuda")
+        sq = torch.zeros(16, NORM_ROWS, device="cuda")
+        rows = min(M, NORM_ROWS)
+        sq[:, :rows] = xd[:rows].float().pow(2).view(rows, 16, 16).sum(-1).t()
+        nw = (1 + 0.1 * torch.randn(256, generator=cpu_gen(4))).to(BF).cuda()
+        rc = L.ns_gemm(xd.data_ptr(), wd.data_ptr(), None, y.data_ptr(), M, 256, 256, 1, sq.data_ptr(),
+                       nw.data_ptr(), 1e-6, None, 0, _lib.stream_of(xd))
+        if M > NORM_ROWS:
+            assert rc != 0 and b"normalised" in L.ns_last_error()
+            continue
+        assert rc == 0, L.ns_last_error()
+        h = NormedRows(xd, sq, nw, 1e-6).tensor()
+        y2 = torch.empty_like(y)
+        assert L.ns_gemm(h.data_ptr(), wd.data_ptr(), None, y2.data_ptr(), M, 256, 256, 1, None, None, 0.0, None, 0,
+                         _lib.stream_of(xd)) == 0
+        assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("M,N,K", [(96, 1536, 1536), (120, 1536, 8960), (128, 896, 4864)])
+def test_residual_row_statistics_above_64_rows_through_the_c_abi(hiplib, M, N, K):
+    """ns_gemm_residual_norm_stats on verify-sized batches (65-128 rows): the tile-16 kernel's 16-row token
+    blocks (K <= 2048) or the skinny kernel's 64-row blocks (longer K) with the residual sum and the
+    per-16-column row sums of squares in the epilogue; r against the fp64 product, the statistics exactly
+    the row sums of r^2 (every row, both token blocks' halves), and the norm applied from them against the
+    oracle's rms_norm of r."""
+    from nanoserve_amd import _lib
+    from nanoserve_amd.kernels.linear import NORM_ROWS, NormedRows
+    L = _lib.lib()
+    x, w = operands(M, N, K, seed=21)
+    res = torch.randn(M, N, generator=cpu_gen(22)).to(BF)
+    xd, wd, rd = x.cuda(), w.cuda(), res.cuda()
+    r = torch.empty(M, N, dtype=BF, device="cuda")
+    sq = torch.full((N // 16, NORM_ROWS), float("nan"), device="cuda")
+    ws = torch.zeros(max(L.ns_gemm_workspace_bytes(M, N, K), 256), dtype=torch.uint8, device="cuda")
+    rc = L.ns_gemm_residual_norm_stats(xd.data_ptr(), wd.data_ptr(), rd.data_ptr(), r.data_ptr(), sq.data_ptr(), M, N, K,
+                                       1, ws.data_ptr(), ws.numel(), _lib.stream_of(xd))
+    assert rc == 0, L.ns_last_error()
+    y = ref_linear(x, w)
+    bf16_check(r.cpu(), res + y, f"residual sum {M}x{N}x{K}", dot_bound(x, w) + ulp(y))
+    want = r.float().pow(2).view(M, N // 16, 16).sum(-1).t()
+    assert torch.allclose(sq[:, :M], want, rtol=1e-5, atol=1e-6)
+    nw = (1 + 0.1 * torch.randn(N, generator=cpu_gen(23))).to(BF).cuda()
+    h = NormedRows(r, sq, nw, 1e-6).tensor().cpu()
+    same, ulps = ops.bf16_ulp_close(h, ops.rms_norm(r.cpu(), nw.cpu(), 1e-6))
+    assert same >= 0.99 and ulps <= 1.0, (same, ulps)

@@ -53,12 +53,12 @@ def test_invalid_arguments_are_rejected_on_the_host():
     assert lib.ns_rms_norm(None, None, None, None, None, 4, 100000, 1e-6, 1, None) == 1
     assert lib.ns_silu_mul(None, None, 4, 8, 7, None) == 1
     assert lib.ns_rope_qkv(None, None, None, None, None, None, None, None, None, 4, 12, 2, 127, 1, None) == 1
-    # hidden not a multiple of 16; row statistics for more than 64 tokens
+    # hidden not a multiple of 16; row statistics for more than NS_NORM_ROWS (128) tokens
     assert lib.ns_embed_rope(None, None, 4, None, 10, 100, None, 64, None, None, None, None, 1, None) == 1
     assert b"hidden" in lib.ns_last_error()
     sq = ctypes.c_float()
-    assert lib.ns_embed_rope(None, None, 65, None, 10, 128, None, 64, None, None, None, ctypes.byref(sq), 1, None) == 1
-    assert b"64 tokens" in lib.ns_last_error()
+    assert lib.ns_embed_rope(None, None, 129, None, 10, 128, None, 64, None, None, None, ctypes.byref(sq), 1, None) == 1
+    assert b"128 tokens" in lib.ns_last_error()
 
 
 def test_missing_library_fails_loudly(tmp_path):
