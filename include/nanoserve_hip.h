@@ -81,6 +81,24 @@ int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ns_paged_attn_decode with entries that share a block table computed together: pairs[b] = 1 when entry b + 1
+ * reads the same block table as entry b (any context lengths; pairs[b + 1] is then -1), 0 for an entry on its
+ * own. A pair runs as one workgroup row of the whole-row kernel, its two query-head groups side by side in
+ * the 16 MFMA columns, so each page is read once for both (speculative verification: the k + 1 rows of a
+ * sequence share its table, nanoserve/speculative.py:193-211). Results are bitwise those of
+ * ns_paged_attn_decode (a column's arithmetic does not depend on the other columns). Shapes where two
+ * groups do not fit in 16 columns, or outside the whole-row kernel, ignore pairs.
+ */
+int ns_paged_attn_decode_pairs(const void* q, int64_t q_sb, int64_t q_sh,
+                               const void* k_pool, const void* v_pool,
+                               int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                               const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                               const int32_t* pairs, void* out, int64_t o_sb, int64_t o_sh,
+                               int B, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                               int max_blocks, int num_blocks, float scale, int dtype,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * ns_paged_attn_decode with the two products on the vector ALUs instead of the matrix cores: same arguments,
  * partitions, loads and merge; per lane fp32 FMAs over its 8 dims of a token and wave64 shuffle sums for the
  * scores (probabilities rounded to bf16 before P.V as in the MFMA kernel). bf16 whole-row shapes only

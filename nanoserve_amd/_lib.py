@@ -35,6 +35,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         _c_int, _c_int, _c_int, _c_int, _c_int,  # B, n_heads, n_kv_heads, head_dim, block_size
         _c_int, _c_int, _c_f32, _c_int,         # max_blocks, num_blocks, scale, dtype
         _c_vp, _c_sz, _c_vp]),                  # workspace, workspace_bytes, stream
+    "ns_paged_attn_decode_pairs": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64,
+        _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f32, _c_int, _c_vp, _c_sz, _c_vp]),
     "ns_paged_attn_decode_valu": (_c_int, [
         _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f32, _c_int, _c_vp, _c_sz, _c_vp]),

@@ -379,6 +379,10 @@ struct RowsArgs {
   int64_t s_tok, s_h;
   const int64_t* qrows;
   int cstride;
+  // optional, one per entry: 1 = entries b and b + 1 read the same block table (speculative verify rows of
+  // one sequence) and run as one workgroup row, their query heads side by side in the 16 MFMA columns;
+  // -1 = entry b was taken with b - 1; 0 = alone. Only when twice the workgroup's query heads fit in 16.
+  const int32_t* pair;
 };
 template <int HD>
 constexpr int rows_lds_bytes() {
@@ -425,24 +429,34 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   const int L = bid, part = L / R;
   const int row = (L - part * R + part) % R;
   const int b = row / nkv_grid, g = row - b * nkv_grid;
+  const int prw = (!VALU && ra.pair != nullptr) ? ra.pair[b] : 0;
+  if (prw < 0) return;   // entry b runs in the workgroups of entry b - 1
+  const int np_ = prw > 0 ? 2 : 1;   // entries in this workgroup row
   const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
+  const int64_t qb1 = np_ > 1 ? (qrows != nullptr ? qrows[b + 1] : int64_t(b + 1)) : qb;
   const int nq_w = nkv_grid > 1 ? G : nq;   // query heads of this workgroup: heads g G .. g G + nq_w - 1
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
   const int p0 = part * pp;
+  // MFMA column c16 = (entry c16 / nq_w, query head c16 % nq_w) of the workgroup row
+  const int cj = c16 >= nq_w ? 1 : 0, ch = c16 - cj * nq_w;
 
-  // ctx, this wave's block ids (lane i < PPW holds page i's) and Q go out together
-  const int ctx = ctxl[b];
+  // ctx, this wave's block ids (lane i < PPW holds page i's) and Q go out together; a pair walks the longer
+  // context's pages and masks each column's scores at its own entry's context
+  const int ctx0 = ctxl[b];
+  const int ctx1 = np_ > 1 ? ctxl[b + 1] : ctx0;
+  const int ctx = max(ctx0, ctx1);
+  const int ctx_col = cj ? ctx1 : ctx0;
   int blk_lane;
   {
     const int p = p0 + w + NW * (lane < PPW ? lane : 0);
     blk_lane = p < max_blocks ? bt[int64_t(b) * bt_sb + p] : -1;
   }
-  const bool qlive = c16 < nq_w;
-  const int gq = qlive ? c16 / G : NKV;   // KV head (within the token row) of this lane's query column
+  const bool qlive = c16 < np_ * nq_w;
+  const int gq = qlive ? ch / G : NKV;   // KV head (within the token row) of this lane's query column
   bf16x8_t qf[KS];
   {
-    const bf16_t* qrow = q + qb * q_sb + int64_t(g * G + (qlive ? c16 : 0)) * q_sh;
+    const bf16_t* qrow = q + (cj ? qb1 : qb) * q_sb + int64_t(g * G + (qlive ? ch : 0)) * q_sh;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       rk_u32x4_t u = *reinterpret_cast<const rk_u32x4_t*>(qrow + 32 * s + 8 * r4);
@@ -474,8 +488,10 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   if (n_pages > max_blocks) n_pages = max_blocks;
   if (ctx <= 0) {   // no keys: zeros
     if (part == 0)
-      for (int i = tid; i < nq_w * HD; i += NW * 64)
-        out[qb * o_sb + int64_t(g * G + i / HD) * o_sh + (i % HD)] = bf16_t(0);
+      for (int i = tid; i < np_ * nq_w * HD; i += NW * 64) {
+        const int c = i / HD, j = c >= nq_w ? 1 : 0;
+        out[(j ? qb1 : qb) * o_sb + int64_t(g * G + c - j * nq_w) * o_sh + (i % HD)] = bf16_t(0);
+      }
     return;
   }
   if (p0 >= n_pages) return;
@@ -591,12 +607,13 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
       }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the next page's K writes stay behind these reads
     // lane (c16, r4) holds rows 4 r4 + k = tokens 4k + r4 of the page
-    bool valid[4];
+    bool valid[4], vtok[4];   // vtok: a written key (its V row kept); valid: visible to this lane's column
     float sv[4];
     float mx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      valid[k] = okp && (p * PAGE + 4 * k + r4) < ctx;
+      vtok[k] = okp && (p * PAGE + 4 * k + r4) < ctx;
+      valid[k] = vtok[k] && (p * PAGE + 4 * k + r4) < ctx_col;
       sv[k] = valid[k] ? st[k] * scale_log2 : -INFINITY;
       mx = fmaxf(mx, sv[k]);
     }
@@ -617,8 +634,8 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
 #pragma unroll
     for (int k = 0; k < 4; ++k) pb[k] = short(f32_to_bf16(pv[k]));
     // V^T tile t: row c16 = 16-byte chunk c16 (dim 8 c16 + t of the row), k = token 4j + r4
-    const uint32_t m01 = (valid[0] ? 0x0000ffffu : 0u) | (valid[1] ? 0xffff0000u : 0u);
-    const uint32_t m23 = (valid[2] ? 0x0000ffffu : 0u) | (valid[3] ? 0xffff0000u : 0u);
+    const uint32_t m01 = (vtok[0] ? 0x0000ffffu : 0u) | (vtok[1] ? 0xffff0000u : 0u);
+    const uint32_t m23 = (vtok[2] ? 0x0000ffffu : 0u) | (vtok[3] ? 0xffff0000u : 0u);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int wd = t >> 1;
@@ -729,10 +746,11 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
     const uint2 pk = make_uint2(uint32_t(f32_to_bf16(A[0] * inv)) | (uint32_t(f32_to_bf16(A[1] * inv)) << 16),
                                 uint32_t(f32_to_bf16(A[2] * inv)) | (uint32_t(f32_to_bf16(A[3] * inv)) << 16));
-    *reinterpret_cast<uint2*>(out + qb * o_sb + int64_t(g * G + h) * o_sh + 4 * d4) = pk;
+    const int j = h >= nq_w ? 1 : 0;   // column h = (entry j, query head h - j nq_w)
+    *reinterpret_cast<uint2*>(out + (j ? qb1 : qb) * o_sb + int64_t(g * G + h - j * nq_w) * o_sh + 4 * d4) = pk;
   };
   constexpr int ITEMS = (16 * (HD / 4) + NW * 64 - 1) / (NW * 64);
-  const int n_items = nq_w * (HD / 4);
+  const int n_items = np_ * nq_w * (HD / 4);
   if (n_active == 1) {
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
@@ -982,7 +1000,7 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
                                int n_heads, int n_kv_heads, int head_dim, int block_size, int max_blocks,
                                int num_blocks, float scale, int dtype, void* workspace, size_t workspace_bytes,
                                void* stream, const int64_t* qrows = nullptr, RowsLaunch* defer = nullptr,
-                               bool valu = false) {
+                               bool valu = false, const int32_t* pairs = nullptr) {
   NS_REQUIRE(dtype == NS_DTYPE_F32 || dtype == NS_DTYPE_BF16, "paged_attention_decode: dtype %d not supported",
              dtype);
   NS_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention_decode: head_dim %d not in {64, 128}", head_dim);
@@ -1049,6 +1067,7 @@ static int paged_decode_launch(const void* q, int64_t q_sb, int64_t q_sh, const 
                 static_cast<const bf16_t*>(v_pool), kv_sblk, block_tables, bt_sb, context_lens,
                 static_cast<bf16_t*>(out), o_sb, o_sh, G, n_heads, max_blocks, num_blocks, sl2, rcnt, racc, rml, B,
                 rparts, rgh, rgh > 1 ? kv_spos : int64_t(128), kv_sh, qrows, rstride};
+    if (pairs != nullptr && !valu && 2 * (rgh > 1 ? G : n_heads) <= 16) ra.pair = pairs;
     const unsigned rgrid = unsigned(rparts) * unsigned(rrows);
     if (defer != nullptr) {   // the caller launches these workgroups (beside others)
       *defer = RowsLaunch{ra, rgrid, rgh, head_dim};
@@ -1171,6 +1190,20 @@ extern "C" int ns_paged_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, c
   return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
                              context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
                              num_blocks, scale, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ns_paged_attn_decode_pairs(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,
+                                          const void* v_pool, int64_t kv_sblk, int64_t kv_spos, int64_t kv_sh,
+                                          const int32_t* block_tables, int64_t bt_sb, const int32_t* context_lens,
+                                          const int32_t* pairs, void* out, int64_t o_sb, int64_t o_sh, int B,
+                                          int n_heads, int n_kv_heads, int head_dim, int block_size, int max_blocks,
+                                          int num_blocks, float scale, int dtype, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  NS_REQUIRE(pairs != nullptr, "paged_attention_decode_pairs: pairs is NULL");
+  return paged_decode_launch(q, q_sb, q_sh, k_pool, v_pool, kv_sblk, kv_spos, kv_sh, block_tables, bt_sb,
+                             context_lens, out, o_sb, o_sh, B, n_heads, n_kv_heads, head_dim, block_size, max_blocks,
+                             num_blocks, scale, dtype, workspace, workspace_bytes, stream, nullptr, nullptr, false,
+                             pairs);
 }
 
 extern "C" int ns_paged_attn_decode_valu(const void* q, int64_t q_sb, int64_t q_sh, const void* k_pool,

@@ -40,6 +40,7 @@ import time
 
 import torch
 
+from nanoserve_amd.kernels.paged_attention import pair_rows
 from nanoserve_amd.kv_cache import PagedKVCache
 from nanoserve_amd.model import DecodeMeta, Qwen2Model, SeqInput
 
@@ -91,7 +92,7 @@ class StepGraph:
         self.B, self.W = B, runner.max_blocks
         self.garbage_slot = runner.garbage_block * runner.block_size
         self.garbage_block = runner.garbage_block
-        nbytes = 28 * B + 4 * B * self.W
+        nbytes = 32 * B + 4 * B * self.W
         dev = runner.model.device
         self.dev_buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         self.twins = [torch.zeros(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
@@ -103,8 +104,8 @@ class StepGraph:
         for v in self.np:
             self._pad(v, 0)
         self.dev_buf.copy_(self.twins[0])
-        tok, pos, slots, lens, tables = self._views(self.dev_buf)
-        meta = DecodeMeta(runner.token_idx[:B], tables, lens, all_rows=True)
+        tok, pos, slots, lens, pairs, tables = self._views(self.dev_buf)
+        meta = DecodeMeta(runner.token_idx[:B], tables, lens, all_rows=True, pairs=pairs)
         seqs = [SeqInput(1, ctx_len=1, use_kernel=True)] * B
 
         def forward():
@@ -115,15 +116,17 @@ class StepGraph:
         self.graph, self.logits = capture(forward, runner.mempool)
 
     def _views(self, buf: torch.Tensor, numpy: bool = False):
-        """tokens, positions, slots (int64 [B]); context lengths (int32 [B]); tables (int32 [B, W])."""
+        """tokens, positions, slots (int64 [B]); context lengths, row pairing (int32 [B]); tables (int32 [B, W])."""
         B = self.B
-        o = (0, 8 * B, 16 * B, 24 * B, 28 * B)
+        o = (0, 8 * B, 16 * B, 24 * B, 28 * B, 32 * B)
         v = (buf[o[0]:o[1]].view(torch.int64), buf[o[1]:o[2]].view(torch.int64), buf[o[2]:o[3]].view(torch.int64),
-             buf[o[3]:o[4]].view(torch.int32), buf[o[4]:].view(torch.int32).view(B, self.W))
+             buf[o[3]:o[4]].view(torch.int32), buf[o[4]:o[5]].view(torch.int32),
+             buf[o[5]:].view(torch.int32).view(B, self.W))
         return tuple(x.numpy() for x in v) if numpy else v
 
     def _pad(self, views, lo: int) -> None:
-        tok, pos, slots, lens, tables = views
+        tok, pos, slots, lens, pairs, tables = views
+        pairs[lo:] = 0
         tok[lo:] = 0
         pos[lo:] = 0
         slots[lo:] = self.garbage_slot
@@ -134,7 +137,7 @@ class StepGraph:
     def stage(self, par: int, tokens, positions, slots, tables, lens) -> None:
         """Write a step into pinned twin `par` (tokens None: left for later)."""
         n = len(positions)
-        tok, pos, sl, ln, tb = self.np[par]
+        tok, pos, sl, ln, pr, tb = self.np[par]
         if tokens is not None:
             tok[:n] = tokens
         pos[:n] = positions
@@ -155,6 +158,7 @@ class StepGraph:
             rows[i] = (t, L)
         for i in range(n, self.B):
             rows[i] = None
+        pair_rows(tables, pr)   # rows of one sequence (speculative verification) share its table
         self._pad(self.np[par], n)
 
     def launch(self, par: int) -> None:

@@ -57,9 +57,11 @@ def decode_workspace(device: torch.device, B: int, n_kv_heads: int, head_dim: in
 
 def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                            block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
-                           products: str = "mfma") -> torch.Tensor:
+                           products: str = "mfma", pairs: torch.Tensor | None = None) -> torch.Tensor:
     """products="valu" runs the same kernel with the QK^T and P.V products on the vector ALUs
-    (ns_paged_attn_decode_valu: bf16 whole-row shapes only), for measuring the matrix-core design choice."""
+    (ns_paged_attn_decode_valu: bf16 whole-row shapes only), for measuring the matrix-core design choice.
+    pairs (int32 [B], device; see pair_rows) lets rows that share a block table run together
+    (ns_paged_attn_decode_pairs): the same result, each page read once per pair."""
     if products not in ("mfma", "valu"):
         raise ValueError(f"products must be 'mfma' or 'valu', got {products!r}")
     B, n_heads, head_dim = q.shape
@@ -77,11 +79,15 @@ def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
     max_blocks = block_tables.shape[1]
     ws = decode_workspace(q.device, B, n_kv_heads, head_dim, max_blocks, q.dtype)
     L = _lib.lib()
-    fn = L.ns_paged_attn_decode if products == "mfma" else L.ns_paged_attn_decode_valu
+    if pairs is not None and products == "mfma":
+        assert pairs.dtype == torch.int32 and pairs.shape == (B,) and pairs.is_contiguous()
+        fn, extra = L.ns_paged_attn_decode_pairs, (pairs.data_ptr(),)
+    else:
+        fn, extra = (L.ns_paged_attn_decode if products == "mfma" else L.ns_paged_attn_decode_valu), ()
     _lib.check(fn(
         q.data_ptr(), q.stride(0), q.stride(1),
         k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
-        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
+        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), *extra,
         out.data_ptr(), out.stride(0), out.stride(1),
         B, n_heads, n_kv_heads, head_dim, block_size, max_blocks, num_blocks, float(scale), _lib.dtype_code(q),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _lib.stream_of(q)),
@@ -216,3 +222,17 @@ def paged_attention_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         _lib.dtype_code(q), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
         _lib.stream_of(q)), "paged_attention_prefill")
     return out
+
+
+def pair_rows(tables: list, out) -> None:
+    """Fill `out` (int32 array-like, len >= len(tables)) with the row pairing of ns_paged_attn_decode_pairs:
+    consecutive rows whose block tables are the same list (or equal) are paired left to right (1 for the
+    first of a pair, -1 for the second), every other row 0."""
+    n, i = len(tables), 0
+    while i < n:
+        if i + 1 < n and (tables[i + 1] is tables[i] or tables[i + 1] == tables[i]):
+            out[i], out[i + 1] = 1, -1
+            i += 2
+        else:
+            out[i] = 0
+            i += 1

@@ -157,6 +157,7 @@ class DecodeMeta:
     block_tables: torch.Tensor    # [Bd, max_blocks] int32
     context_lens: torch.Tensor    # [Bd] int32, including this step's token
     all_rows: bool = False        # token_idx is arange(N): rows map 1:1 to the step's tokens (no gather)
+    pairs: torch.Tensor | None = None   # [Bd] int32: rows sharing a block table, run together (pair_rows)
 
 
 def random_state_dict(cfg: ModelConfig, seed: int = 0, dtype: torch.dtype = torch.bfloat16,
@@ -315,7 +316,7 @@ class Qwen2Model:
         scale = hd ** -0.5
         if decode_meta is not None and decode_meta.all_rows:
             o = paged_attention_decode(q[0], paged.k[i], paged.v[i], decode_meta.block_tables,
-                                       decode_meta.context_lens, scale)
+                                       decode_meta.context_lens, scale, pairs=decode_meta.pairs)
             if out is None:
                 return o.view(1, N, nh * hd)
             out[0].copy_(o.view(N, nh * hd))

@@ -305,3 +305,44 @@ def test_valu_products_variant(hiplib, n_heads, n_kv, hd, ctx_lens):
     print(f"valu ({n_heads},{n_kv},{hd}) vs oracle {e_ref:.2e}, vs mfma {e_mfma:.2e}")
     assert e_ref <= 1e-2 and e_mfma <= 1e-2
     assert torch.equal(valu, valu2)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd", [(12, 2, 128), (16, 2, 128), (14, 2, 64)])
+def test_paired_rows_equal_unpaired(hiplib, n_heads, n_kv, hd):
+    """Speculative-verify rows: k + 1 rows per sequence share its block table with contexts ctx + 1 .. ctx + k + 1.
+    With the pairing (pair_rows) two such rows run in one workgroup row of the whole-row kernel; every output
+    equals the unpaired kernel's bitwise, including contexts on and next to page (16) and partition (512)
+    boundaries, odd group sizes (a row left alone) and rows of other sequences between them. At 14 / 2 heads
+    with hd 64 (one workgroup holds all 14 heads) the pairing does not fit and is ignored."""
+    from nanoserve_amd.kernels.paged_attention import pair_rows, paged_attention_decode
+    g = cpu_gen(41)
+    bases = [15, 16, 511, 510, 1023, 700, 31, 2000]
+    ks = [4, 2, 4, 1, 3, 0, 4, 2]
+    nb = sum(-(-(b + k + 1) // 16) for b, k in zip(bases, ks)) + 8
+    k = torch.randn(nb, 16, n_kv, hd, generator=g).to(torch.bfloat16)
+    v = torch.randn(nb, 16, n_kv, hd, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(nb, generator=g)
+    width = max(-(-(b + kk + 1) // 16) for b, kk in zip(bases, ks))
+    tables_l, lens, used = [], [], 0
+    for b, kk in zip(bases, ks):
+        n = -(-(b + kk + 1) // 16)
+        t = perm[used:used + n].tolist() + [0] * (width - n)
+        used += n
+        for j in range(kk + 1):
+            tables_l.append(t)              # one list object per sequence, as the verify step stages them
+            lens.append(b + j + 1)
+    B = len(lens)
+    q = torch.randn(B, n_heads, hd, generator=g).to(torch.bfloat16).cuda()
+    tables = torch.tensor(tables_l, dtype=torch.int32).cuda()
+    ctx = torch.tensor(lens, dtype=torch.int32).cuda()
+    pairs_h = [9] * B
+    pair_rows(tables_l, pairs_h)
+    assert pairs_h.count(1) == sum((kk + 1) // 2 for kk in ks) and pairs_h.count(-1) == pairs_h.count(1)
+    pairs = torch.tensor(pairs_h, dtype=torch.int32).cuda()
+    kd, vd, scale = k.cuda(), v.cuda(), hd ** -0.5
+    plain = paged_attention_decode(q, kd, vd, tables, ctx, scale)
+    paired = paged_attention_decode(q, kd, vd, tables, ctx, scale, pairs=pairs)
+    paired2 = paged_attention_decode(q, kd, vd, tables, ctx, scale, pairs=pairs)
+    assert torch.equal(plain, paired) and torch.equal(paired, paired2)
+    ref = paged_attention_reference(q.cpu().float(), k.float(), v.float(), tables.cpu(), ctx.cpu(), scale)
+    assert (paired.cpu().float() - ref).abs().max().item() <= 1e-2
