@@ -839,26 +839,29 @@ __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(Ro
   decode_rows_body<HD, PH, VALU>(a, int(blockIdx.x), lds, sm_m, sm_l, s_last);
 }
 
-// A mixed step's attention in one launch: workgroups [0, n_dec) are the whole-row decode kernel's for the
-// step's decode rows, the rest the chunked-prefill kernel's (prefill_body.h). The two write disjoint rows of
-// the output and keep their merges in separate workspaces. Issued as two kernels on one stream the second
-// would wait for the first's last workgroup. Here the decode workgroups are dispatched first (workgroups
-// start in index order) and finish while the prefill's longest work units, which the prefill numbers first,
-// run on the other CUs; the prefill's last, shortest units take the CUs they free. (Two streams overlap them
-// too, but a graph's cross-queue fork and join idle the GPU for longer than that saves.)
+// A mixed step's attention in one launch: workgroups [0, n_pf) are the chunked-prefill kernel's
+// (prefill_body.h), the rest the whole-row decode kernel's for the step's decode rows. The two write disjoint
+// rows of the output and keep their merges in separate workspaces; neither waits on a workgroup of the
+// other kind. Issued as two kernels on one stream the second would wait for the first's last workgroup.
+// Workgroups start in index order and every one reserves the launch's LDS (the prefill's 128 KB, one per
+// CU), so the prefill units, planned to fill the CUs in one round, go first; the decode workgroups start on
+// the CUs left over and on those the prefill's shorter units free. (With the decode workgroups first, the
+// prefill units that found no free CU started ~10 us late and the launch took 37 us against 28 us for the
+// prefill alone. Two streams overlap them too, but a graph's cross-queue fork and join idle the GPU for
+// longer than that saves.)
 template <int HD, bool PH>
 __global__ __launch_bounds__(PF_WG_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void mixed_attn_kernel(
-    PrefillArgs pa, int n_dec, RowsArgs ra) {
+    PrefillArgs pa, int n_pf, RowsArgs ra) {
   static_assert(PF_WG_THREADS == ROWK_NW * 64, "one workgroup size for both kinds");
   constexpr int PF_BYTES = PF_GROUPS * 2 * PfLds<HD>::STAGE;
   constexpr int BYTES = PF_BYTES > rows_lds_bytes<HD>() ? PF_BYTES : rows_lds_bytes<HD>();
   __shared__ __align__(16) unsigned char lds[BYTES];
   __shared__ float sm_m[ROWK_NW][16], sm_l[ROWK_NW][16];
   __shared__ unsigned s_last;
-  if (int(blockIdx.x) < n_dec)
-    decode_rows_body<HD, PH>(ra, int(blockIdx.x), lds, sm_m, sm_l, s_last);
+  if (int(blockIdx.x) < n_pf)
+    prefill_body<HD>(pa, int(blockIdx.x), lds, s_last);
   else
-    prefill_body<HD>(pa, int(blockIdx.x) - n_dec, lds, s_last);
+    decode_rows_body<HD, PH>(ra, int(blockIdx.x) - n_pf, lds, sm_m, sm_l, s_last);
 }
 
 // fp32: one wave per (row, KV head). Lane owns dims lane and lane + 64 (hd 128).
@@ -1162,22 +1165,25 @@ extern "C" int ns_paged_attn_mixed(const void* q, int64_t q_sb, int64_t q_sh, co
     if (n_pf > 0) {
       const dim3 grid{unsigned(n_pf)};
       if (head_dim == 64)   // every workgroup a prefill one
-        hipLaunchKernelGGL((mixed_attn_kernel<64, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, 0, rl.a);
+        hipLaunchKernelGGL((mixed_attn_kernel<64, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, int(n_pf), rl.a);
       else
-        hipLaunchKernelGGL((mixed_attn_kernel<128, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, 0, rl.a);
+        hipLaunchKernelGGL((mixed_attn_kernel<128, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, int(n_pf), rl.a);
     }
     return check_launch("paged_attention_mixed");
   }
-  NS_REQUIRE(n_pf + int64_t(rl.grid) < (int64_t(1) << 31), "paged_attention_mixed: %lld workgroups",
-             (long long)(n_pf + rl.grid));
-  const dim3 grid{unsigned(n_pf + rl.grid)};
-  const int n_dec = int(rl.grid);
+  // the prefill part padded to a multiple of 8 workgroups (the extra ones find no unit and return), so the
+  // decode workgroups keep the XCD rotation they have in their own kernel (workgroup i runs on XCD i % 8)
+  const int64_t n_pf8 = (n_pf + 7) & ~int64_t(7);
+  NS_REQUIRE(n_pf8 + int64_t(rl.grid) < (int64_t(1) << 31), "paged_attention_mixed: %lld workgroups",
+             (long long)(n_pf8 + rl.grid));
+  const dim3 grid{unsigned(n_pf8 + rl.grid)};
+  const int npf = int(n_pf8);
   if (rl.rgh > 1)
-    hipLaunchKernelGGL((mixed_attn_kernel<128, true>), grid, dim3(PF_WG_THREADS), 0, s, pa, n_dec, rl.a);
+    hipLaunchKernelGGL((mixed_attn_kernel<128, true>), grid, dim3(PF_WG_THREADS), 0, s, pa, npf, rl.a);
   else if (rl.head_dim == 64)
-    hipLaunchKernelGGL((mixed_attn_kernel<64, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, n_dec, rl.a);
+    hipLaunchKernelGGL((mixed_attn_kernel<64, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, npf, rl.a);
   else
-    hipLaunchKernelGGL((mixed_attn_kernel<128, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, n_dec, rl.a);
+    hipLaunchKernelGGL((mixed_attn_kernel<128, false>), grid, dim3(PF_WG_THREADS), 0, s, pa, npf, rl.a);
   return check_launch("paged_attention_mixed");
 }
 

@@ -196,7 +196,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, int bid, unsi
   const int qbase = tile * PF_QT;
   const int kv_total = ctx + T;             // keys that exist
   const int n_sub = 2 * n_parts;
-  const int tid_wg = threadIdx.x, gi = tid_wg >> 8;   // group
+  const int tid_wg = threadIdx.x, gi = __builtin_amdgcn_readfirstlane(tid_wg >> 8);   // group (wave-uniform)
   const int sub = 2 * part + gi;
   const int st0 = sub * n_st / n_sub, st1 = (sub + 1) * n_st / n_sub;
   // both groups run the same number of stage-loop iterations (their barriers are the workgroup's)
