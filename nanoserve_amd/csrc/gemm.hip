@@ -1056,10 +1056,11 @@ constexpr int TG_MAX_SPLITS = 16;            // K slices at most
 constexpr int TG_PLAN_SPLITS = 6;             // K slices the plan chooses at most
 constexpr int TG_RSRC3 = 0x00020000;          // buffer resource word 3: raw (untyped) 32-bit accesses
 
-template <int FM, int FN, int NW_>
+// NW waves in a WM x (NW / WM) grid (wave w at m-block w % WM, n-block w / WM), each a (16 FM) x (16 FN) block.
+template <int FM, int FN, int NW_, int WM_ = 2>
 struct TgShape {
-  static constexpr int NW = NW_, NT = 64 * NW, WNW = NW / 2;   // waves, threads, waves along N
-  static constexpr int BM = 32 * FM, BN = 16 * FN * WNW;      // X rows, W rows of a tile
+  static constexpr int NW = NW_, NT = 64 * NW, WM = WM_, WNW = NW / WM;   // waves, threads, waves along M / N
+  static constexpr int BM = 16 * FM * WM, BN = 16 * FN * WNW;            // X rows, W rows of a tile
   static constexpr int WG_PER_CU = NW == 8 ? 1 : 2;
   static constexpr int S = 4;                                 // ring stages
   static constexpr int AROWS = BM * TG_BK * 2;                // bytes of the X rows of a stage
@@ -1129,9 +1130,11 @@ __device__ __forceinline__ int tg_wrow(int r, int tn, int half) {
   }
 }
 
-template <int EPI, int FM, int FN, int NW>
-__global__ __launch_bounds__((TgShape<FM, FN, NW>::NT), (TgShape<FM, FN, NW>::WG_PER_CU)) void tiled_gemm_kernel(TgArgs a) {
-  using SH = TgShape<FM, FN, NW>;
+template <int EPI, int FM, int FN, int NW, int WM>
+__global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW, WM>::WG_PER_CU)) void tiled_gemm_kernel(
+    TgArgs a) {
+  using SH = TgShape<FM, FN, NW, WM>;
+  static_assert(EPI == EPI_STORE || WM == 2, "the SiLU epilogue pairs the waves of a 2-row wave grid");
   constexpr int BM = SH::BM, BN = SH::BN, NT = SH::NT, S = SH::S;
   __shared__ __align__(16) unsigned char lds[SH::LDS];
   __shared__ unsigned s_last;
@@ -1178,7 +1181,7 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW>::NT), (TgShape<FM, FN, NW>::WG
 
   // fragment offsets within a stage: lane -> row l % 16 of the 16-row tile, 16-byte chunk l / 16; the swizzle
   // of rows 16 i + l % 16 does not depend on i, so fragment i sits 1024 i bytes further
-  const int wm = w & 1, wn = w >> 1;
+  const int wm = w % WM, wn = w / WM;
   const int ra = 16 * FM * wm + (l & 15), rb = 16 * FN * wn + (l & 15);
   const uint32_t foa = uint32_t(ra * 64 + 16 * ((l >> 4) ^ ((ra >> 1) & 3)));
   const uint32_t fob = uint32_t(SH::AROWS + rb * 64 + 16 * ((l >> 4) ^ ((rb >> 1) & 3)));
@@ -1555,46 +1558,72 @@ static int bind_xnorm(GemmArgs& a, const float* x_sumsq, const void* x_norm_w, f
 }
 
 // ---- tiled GEMM plan and launch (M > 64)
+enum TgTile { TG_SMALL = 0, TG_BIG = 1, TG_TALL = 2 };
 struct TgPlan {
-  int big;   // 256 x 256 tiles (8 waves), else 128 x 128 (4 waves)
+  int shape;   // TgTile: 128 x 128 (4 waves, two per CU), 256 x 256 or 256 x 128 (8 waves, one per CU)
   int tiles_m, tiles_n, splits, kps;
   size_t bytes;   // workspace (0: no K slices)
 };
 using TgBig = TgShape<8, 4, 8>;
 using TgSmall = TgShape<4, 4, 4>;
+using TgTall = TgShape<4, 4, 8, 4>;   // 256 X rows x 128 W rows: waves in a 4 x 2 grid of 64 x 64 blocks
+static int tg_bm(int shape) { return shape == TG_BIG ? TgBig::BM : shape == TG_TALL ? TgTall::BM : TgSmall::BM; }
+static int tg_bn(int shape) { return shape == TG_BIG ? TgBig::BN : shape == TG_TALL ? TgTall::BN : TgSmall::BN; }
 static void tg_tiles(TgPlan& p, int M, int N, bool silu) {
-  const int bm = p.big ? TgBig::BM : TgSmall::BM, bn = p.big ? TgBig::BN : TgSmall::BN;
+  const int bm = tg_bm(p.shape), bn = tg_bn(p.shape);
   p.tiles_m = (M + bm - 1) / bm;
   p.tiles_n = silu ? (N / 2 + bn / 2 - 1) / (bn / 2) : (N + bn - 1) / bn;
 }
 // 256 x 256 tiles (one workgroup per CU) when there is one for every CU; otherwise 128 x 128 tiles (two per
-// CU). K is sliced only when it is long (at least 128 steps) and the tiles leave workgroup slots free: as many
-// slices as keep every workgroup resident in one round, at most TG_PLAN_SPLITS (the last slice's merge reads
-// every partial tile, and more slices cost more there than they win), each at least eight 32-wide steps.
-// Measured (1552 x 1536 x 8960: 3 slices 70.7 us, 2: 88.4, 4: 98.7; 96 x 1536 x 8960: 6 slices 29.6 us,
-// 8: 30.9, 3: 35.3; K = 1536 shapes were never faster sliced).
+// CU), unsliced: K = 1536 shapes were never faster sliced. Long K (at least 128 steps, a STORE epilogue) with
+// fewer tiles than CUs: one round of at most one workgroup per CU -- a CU that runs two workgroups of a
+// launch finishes last, at about twice the time of the others -- either 128 x 128 tiles in at most
+// TG_PLAN_SPLITS K slices or 256 x 128 tiles in at most 4 (the last slice's merge reads every partial tile),
+// whichever fills more CUs, the 256 x 128 tiles on a tie (they move 25 % fewer bytes per flop through the
+// CU's load path). Each slice holds at least eight 32-wide steps. Measured, 1536 x 8960 weights (us):
+//   rows                    256   512   768  1024  1280  1552  2048
+//   128^2, slices to fill   36.0  40.6  50.0  65.2  68.8  83.5 109.6   (6, 5, 3, 2, 2, 1 (3 at 1552), 1)
+//   256 x 128, to fill        -     -     -   63.7  69.9  76.7  96.0   (4, 4, 3, 2 slices)
+//   the earlier plan (128^2 slices for two per CU)  36.0  60.6  57.6  63.9  73.0  83.0 116.8
+static inline void tg_plan_override(TgPlan&, int, int, bool, int&) {}
+static int tg_fill_splits(int tiles, int max_splits, int steps) {
+  int s = target_workgroups() / tiles;
+  if (s > max_splits) s = max_splits;
+  if (s > steps / 8) s = steps / 8;
+  return s < 1 ? 1 : s;
+}
 static TgPlan tg_plan(int M, int N, int K, bool silu) {
   TgPlan p;
   const int T = target_workgroups(), steps = K / TG_BK;
-  p.big = 1;
+  p.shape = TG_BIG;
   tg_tiles(p, M, N, silu);
   if (int64_t(p.tiles_m) * p.tiles_n < T) {
-    p.big = 0;
+    p.shape = TG_SMALL;
     tg_tiles(p, M, N, silu);
   }
-  const int tiles = p.tiles_m * p.tiles_n, slots = p.big ? T : 2 * T;
+  int tiles = p.tiles_m * p.tiles_n;
   int splits = 1;
-  if (steps >= 128 && tiles < slots) {
-    splits = slots / tiles;
-    if (splits > TG_PLAN_SPLITS) splits = TG_PLAN_SPLITS;
-    if (splits > steps / 8) splits = steps / 8;
+  if (steps >= 128 && !silu && p.shape == TG_SMALL && tiles < T) {
+    const int s_small = tg_fill_splits(tiles, TG_PLAN_SPLITS, steps);
+    TgPlan t = p;
+    t.shape = TG_TALL;
+    tg_tiles(t, M, N, silu);
+    const int tt = t.tiles_m * t.tiles_n, s_tall = tt < T ? tg_fill_splits(tt, 4, steps) : 1;
+    if (tt < T && tt * s_tall >= tiles * s_small) {
+      p = t;
+      splits = s_tall;
+    } else {
+      splits = s_small;
+    }
   }
+  tg_plan_override(p, M, N, silu, splits);
+  tiles = p.tiles_m * p.tiles_n;
   if (splits > TG_MAX_SPLITS) splits = TG_MAX_SPLITS;
   if (splits > steps) splits = steps;
   if (splits < 1) splits = 1;
   p.kps = (steps + splits - 1) / splits;
   p.splits = (steps + p.kps - 1) / p.kps;   // every slice non-empty
-  const int part = p.big ? TgBig::PART : TgSmall::PART;
+  const int part = tg_bm(p.shape) * tg_bn(p.shape);
   p.bytes = p.splits > 1 ? G_CNT_BYTES + align256(sizeof(float) * size_t(tiles) * p.splits * part) : 0;
   return p;
 }
@@ -1628,10 +1657,12 @@ static int launch_tiled(const void* x, const void* w, const void* bias, void* y,
     a.part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + G_CNT_BYTES);
   }
   const dim3 grid(unsigned(p.tiles_m * p.tiles_n * p.splits));
-  if (p.big)
-    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 8, 4, 8>), grid, dim3(TgBig::NT), 0, st, a);
+  if (p.shape == TG_BIG)
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 8, 4, 8, 2>), grid, dim3(TgBig::NT), 0, st, a);
+  else if (EPI == EPI_STORE && p.shape == TG_TALL)
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPI_STORE, 4, 4, 8, 4>), grid, dim3(TgTall::NT), 0, st, a);
   else
-    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 4, 4, 4>), grid, dim3(TgSmall::NT), 0, st, a);
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 4, 4, 4, 2>), grid, dim3(TgSmall::NT), 0, st, a);
   return check_launch("gemm(tiled)");
 }
 

@@ -5,8 +5,8 @@ once-rounded product and every element within 1 bf16 ulp plus Higham's determini
 nanoserve/model.py:231,256-257 on the large-token path. At 1552 rows the check covers every 128-row tile
 (its first, middle and last rows and the partial last tile) and every column. Routes: up to 192 rows the
 K <= 2048 projections run the tile-16 kernel in 16-token blocks and the 8960-long ones the skinny kernel in
-64-row token blocks; otherwise the tiled kernel (1552 x 17920 on 256 x 256 tiles, the rest on 128 x 128,
-K-sliced where K is long and the tiles are few).
+64-row token blocks; otherwise the tiled kernel (1552 x 17920 on 256 x 256 tiles; long K (>= 128 steps)
+on 256 x 128 or 128 x 128 tiles K-sliced to one workgroup per CU; the rest on 128 x 128).
 Also: K-sliced products are deterministic and share the skinny kernels' workspace."""
 import pytest
 import torch
@@ -38,6 +38,20 @@ def test_tiled_linear(hiplib, M, N, K, bias):
     rows = check_rows(M)
     xs = x[rows]
     bf16_check(y[rows], ref_linear(xs, w, b), f"tiled linear M={M} N={N} K={K} bias={bias}", dot_bound(xs, w))
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(2048, 1536, 8960, False), (1300, 1003, 4864, True), (512, 1536, 8960, False)])
+def test_long_k_plans(hiplib, M, N, K, bias):
+    """Long-K shapes on each one-round plan: 256 x 128 tiles in 2 K slices (2048 rows), 256 x 128 tiles in 4
+    slices with a partial last tile in both dimensions and a bias (1300 x 1003), 128 x 128 tiles in 5 slices
+    (512 rows)."""
+    from nanoserve_amd.kernels.linear import linear
+    x, w = operands(M, N, K, seed=M + 3 * N)
+    b = (torch.randn(N, generator=cpu_gen(2)) * 0.1).to(BF) if bias else None
+    y = linear(x.cuda(), w.cuda(), b.cuda() if bias else None).cpu()
+    rows = torch.tensor(sorted({r for t0 in range(0, M, 128) for r in (t0, t0 + 127) if r < M} | {M - 1}))
+    xs = x[rows]
+    bf16_check(y[rows], ref_linear(xs, w, b), f"long-K linear M={M} N={N} K={K} bias={bias}", dot_bound(xs, w))
 
 
 @pytest.mark.parametrize("M", [65, 96, 120, 1552])
