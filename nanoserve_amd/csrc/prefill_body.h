@@ -87,13 +87,24 @@ struct PfLds {
   static constexpr int IPP = PF_PAGE / TPI;           // such loads per page and tensor
   // K rows are stored with their 16-byte chunks XOR-swizzled by the row, so the 16 rows one fragment
   // read touches land in 16 different bank groups: logical chunk c of stage row t sits at c ^ key(t).
-  static __device__ __forceinline__ int key(int t) { return HD == 128 ? (t & 15) : ((t >> 1) & 7); }
+  static __host__ __device__ constexpr int key(int t) { return HD == 128 ? (t & 15) : ((t >> 1) & 7); }
   // V rows likewise, by an even key from the row's low bits: a transpose read takes a 32-byte chunk pair
   // (2 chunks) from each of four consecutive rows, and XOR by even values moves whole pairs, so the four
   // rows' pairs land in four different bank groups.
-  static __device__ __forceinline__ int vkey(int t) { return (t & (CH / 2 - 1)) << 1; }
+  static __host__ __device__ constexpr int vkey(int t) { return (t & (CH / 2 - 1)) << 1; }
+  // A load's token rows are TPI i + r (r = lane / CH < TPI); both keys split over that sum without carries,
+  // key(TPI i + r) = key(TPI i) ^ key(r), so a lane's swizzled chunk offsets are fixed per lane up to a
+  // compile-time XOR per load (checked for every token of a page below).
+  static constexpr bool keys_split() {
+    for (int t = 0; t < PF_PAGE; ++t) {
+      const int i = t / TPI, r = t % TPI;
+      if (key(t) != (key(TPI * i) ^ key(r)) || vkey(t) != (vkey(TPI * i) ^ vkey(r))) return false;
+    }
+    return true;
+  }
 };
 static_assert(PF_NP == PF_WAVES, "each wave stages one page of a stage");
+static_assert(PfLds<64>::keys_split() && PfLds<128>::keys_split(), "row keys split over a load's token rows");
 
 // two fp32 -> packed bf16 (round to nearest even; v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pf_bf16x2(float lo, float hi) {
@@ -239,22 +250,27 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, int bid, unsi
   unsigned char* glds = lds + gi * (2 * L::STAGE);   // this group's two stage buffers
   const uint32_t lds0 = pf_lds_addr(glds);
   const uint32_t spos2 = uint32_t(a.s_pos) * 2u;   // token stride in bytes (checked < 2^26 by the host)
+  const uint32_t lane_row = uint32_t(lane / L::CH) * spos2;
+  const uint32_t lane_kx = 16u * uint32_t((lane % L::CH) ^ L::key(lane / L::CH));
+  const uint32_t lane_vx = 16u * uint32_t((lane % L::CH) ^ L::vkey(lane / L::CH));
   auto dma_stage = [&](int n, int buf) __attribute__((always_inline)) {
     const int id = __builtin_amdgcn_readlane(pid, PF_NP * (n - win0) + w);
     const int64_t base = (int64_t(id) * a.s_blk + int64_t(g) * a.s_h) * 2;
     const char* kb = reinterpret_cast<const char*>(a.kp) + base;
     const char* vb = reinterpret_cast<const char*>(a.vp) + base;
     const uint32_t kd = __builtin_amdgcn_readfirstlane(lds0 + uint32_t(buf * L::STAGE + w * (PF_PAGE * L::ROW)));
-    // Load i fills LDS slot (token row t, chunk cp) with the token's chunk cp ^ key(t) (K) or cp ^ vkey(t)
-    // (V). The lane's byte offsets are the same for every page; they are recomputed here from an opaque
-    // copy of the lane index rather than kept in registers across the stage loop.
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
+    // Load i fills LDS slot (token row t = TPI i + r, chunk cp) with the token's chunk cp ^ key(t) (K) or
+    // cp ^ vkey(t) (V): the lane's row offset r * spos2 and its chunk offsets for load 0 are kept for the
+    // launch, load i flips the chunk offset by the constant 16 key(TPI i) and adds TPI i token rows to the
+    // scalar page base. (Opaque copies, so the compiler keeps three registers instead of hoisting all eight
+    // offsets.)
+    uint32_t lrow = lane_row, kx = lane_kx, vx = lane_vx;
+    asm volatile("" : "+v"(lrow), "+v"(kx), "+v"(vx));
 #pragma unroll
     for (int i = 0; i < L::IPP; ++i) {
-      const int t = L::TPI * i + ln / L::CH, cp = ln % L::CH;
-      pf_dma16(kb, uint32_t(t) * spos2 + 16u * uint32_t(cp ^ L::key(t)), kd + 1024 * i);
-      pf_dma16(vb, uint32_t(t) * spos2 + 16u * uint32_t(cp ^ L::vkey(t)), kd + L::K_BYTES + 1024 * i);
+      const int64_t rows = int64_t(L::TPI * i) * spos2;
+      pf_dma16(kb + rows, lrow + (kx ^ uint32_t(16 * L::key(L::TPI * i))), kd + 1024 * i);
+      pf_dma16(vb + rows, lrow + (vx ^ uint32_t(16 * L::vkey(L::TPI * i))), kd + L::K_BYTES + 1024 * i);
     }
   };
 
