@@ -390,9 +390,11 @@ constexpr int rows_lds_bytes() {
 }
 
 // PH: each KV head is a workgroup row of its own (hd 128, several KV heads); otherwise a row is a token's
-// whole 256-byte K row. bid: the workgroup's index among the launch's decode-row workgroups; lds (at least
-// rows_lds_bytes<HD>()), sm_m, sm_l, s_last: the launch's LDS.
-template <int HD, bool PH, bool VALU = false>
+// whole 256-byte K row. PAIR: entries that share a block table may run as one workgroup row (ra.pair); a
+// compile-time switch, so launches without pairs carry none of the per-column context logic (+0.57 us per
+// config-2 call when it was a runtime test). bid: the workgroup's index among the launch's decode-row
+// workgroups; lds (at least rows_lds_bytes<HD>()), sm_m, sm_l, s_last: the launch's LDS.
+template <int HD, bool PH, bool VALU = false, bool PAIR = false>
 __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, unsigned char* lds,
                                                  float (*sm_m)[16], float (*sm_l)[16], unsigned& s_last) {
   const bf16_t* __restrict__ q = ra.q;
@@ -429,9 +431,10 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   const int L = bid, part = L / R;
   const int row = (L - part * R + part) % R;
   const int b = row / nkv_grid, g = row - b * nkv_grid;
-  const int prw = (!VALU && ra.pair != nullptr) ? ra.pair[b] : 0;
+  static_assert(!(PAIR && VALU), "pairs run on the matrix-core products only");
+  const int prw = PAIR ? ra.pair[b] : 0;
   if (prw < 0) return;   // entry b runs in the workgroups of entry b - 1
-  const int np_ = prw > 0 ? 2 : 1;   // entries in this workgroup row
+  const int np_ = PAIR && prw > 0 ? 2 : 1;   // entries in this workgroup row
   const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
   const int64_t qb1 = np_ > 1 ? (qrows != nullptr ? qrows[b + 1] : int64_t(b + 1)) : qb;
   const int nq_w = nkv_grid > 1 ? G : nq;   // query heads of this workgroup: heads g G .. g G + nq_w - 1
@@ -439,14 +442,14 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   const int c16 = lane & 15, r4 = lane >> 4;
   const int p0 = part * pp;
   // MFMA column c16 = (entry c16 / nq_w, query head c16 % nq_w) of the workgroup row
-  const int cj = c16 >= nq_w ? 1 : 0, ch = c16 - cj * nq_w;
+  const int cj = PAIR && c16 >= nq_w ? 1 : 0, ch = c16 - cj * nq_w;
 
   // ctx, this wave's block ids (lane i < PPW holds page i's) and Q go out together; a pair walks the longer
   // context's pages and masks each column's scores at its own entry's context
   const int ctx0 = ctxl[b];
-  const int ctx1 = np_ > 1 ? ctxl[b + 1] : ctx0;
-  const int ctx = max(ctx0, ctx1);
-  const int ctx_col = cj ? ctx1 : ctx0;
+  const int ctx1 = PAIR && np_ > 1 ? ctxl[b + 1] : ctx0;
+  const int ctx = PAIR ? max(ctx0, ctx1) : ctx0;
+  const int ctx_col = PAIR && cj ? ctx1 : ctx0;
   int blk_lane;
   {
     const int p = p0 + w + NW * (lane < PPW ? lane : 0);
@@ -613,7 +616,7 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       vtok[k] = okp && (p * PAGE + 4 * k + r4) < ctx;
-      valid[k] = vtok[k] && (p * PAGE + 4 * k + r4) < ctx_col;
+      valid[k] = PAIR ? vtok[k] && (p * PAGE + 4 * k + r4) < ctx_col : vtok[k];
       sv[k] = valid[k] ? st[k] * scale_log2 : -INFINITY;
       mx = fmaxf(mx, sv[k]);
     }
@@ -746,7 +749,7 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
     const uint2 pk = make_uint2(uint32_t(f32_to_bf16(A[0] * inv)) | (uint32_t(f32_to_bf16(A[1] * inv)) << 16),
                                 uint32_t(f32_to_bf16(A[2] * inv)) | (uint32_t(f32_to_bf16(A[3] * inv)) << 16));
-    const int j = h >= nq_w ? 1 : 0;   // column h = (entry j, query head h - j nq_w)
+    const int j = PAIR && h >= nq_w ? 1 : 0;   // column h = (entry j, query head h - j nq_w)
     *reinterpret_cast<uint2*>(out + (j ? qb1 : qb) * o_sb + int64_t(g * G + h - j * nq_w) * o_sh + 4 * d4) = pk;
   };
   constexpr int ITEMS = (16 * (HD / 4) + NW * 64 - 1) / (NW * 64);
@@ -831,12 +834,12 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   }
 }
 
-template <int HD, bool PH, bool VALU>
+template <int HD, bool PH, bool VALU, bool PAIR>
 __global__ __launch_bounds__(ROWK_NW * 64) void paged_decode_rows_bf16_kernel(RowsArgs a) {
   __shared__ __align__(16) unsigned char lds[rows_lds_bytes<HD>()];
   __shared__ float sm_m[ROWK_NW][16], sm_l[ROWK_NW][16];
   __shared__ unsigned s_last;
-  decode_rows_body<HD, PH, VALU>(a, int(blockIdx.x), lds, sm_m, sm_l, s_last);
+  decode_rows_body<HD, PH, VALU, PAIR>(a, int(blockIdx.x), lds, sm_m, sm_l, s_last);
 }
 
 // A mixed step's attention in one launch: workgroups [0, n_pf) are the chunked-prefill kernel's
@@ -979,20 +982,22 @@ struct RowsLaunch {
   unsigned grid;
   int rgh, head_dim;
 };
-template <bool VALU>
+template <bool VALU, bool PAIR>
 static void launch_rows_v(const RowsArgs& a, unsigned grid, int rgh, int head_dim, hipStream_t s) {
   if (rgh > 1)
-    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true, VALU>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, true, VALU, PAIR>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
   else if (head_dim == 64)
-    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false, VALU>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<64, false, VALU, PAIR>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false, VALU>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
+    hipLaunchKernelGGL((paged_decode_rows_bf16_kernel<128, false, VALU, PAIR>), dim3(grid), dim3(ROWK_NW * 64), 0, s, a);
 }
 static void launch_rows(const RowsArgs& a, unsigned grid, int rgh, int head_dim, hipStream_t s, bool valu = false) {
   if (valu)
-    launch_rows_v<true>(a, grid, rgh, head_dim, s);
+    launch_rows_v<true, false>(a, grid, rgh, head_dim, s);
+  else if (a.pair != nullptr)
+    launch_rows_v<false, true>(a, grid, rgh, head_dim, s);
   else
-    launch_rows_v<false>(a, grid, rgh, head_dim, s);
+    launch_rows_v<false, false>(a, grid, rgh, head_dim, s);
 }
 
 // defer: when the whole-row kernel takes the call, fill *defer instead of launching (other kernels launch
