@@ -417,7 +417,7 @@ def spec_verify_bench(model, cfg, ctx: int = 1024, reps: int = 20) -> dict:
         g = torch.Generator(device="cuda").manual_seed(5)
         pool.k.normal_(generator=g)
         pool.v.normal_(generator=g)
-        runner = DecodeGraphRunner(model, pool, max_seq_len=ctx + k1 + 16)
+        runner = DecodeGraphRunner(model, pool, max_seq_len=ctx + k1 + 16, pair_rows=True)
         tables = []
         for _ in range(nseq):
             t = BlockTable(16)

@@ -432,11 +432,18 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
   const int row = (L - part * R + part) % R;
   const int b = row / nkv_grid, g = row - b * nkv_grid;
   static_assert(!(PAIR && VALU), "pairs run on the matrix-core products only");
+  // the pair entry, both entries' context lengths and q rows load together (entry b + 1's clamped in
+  // bounds and used only for a pair), so pairing adds no dependent round trip before the page stream
+  const int bn = b + 1 < B ? b + 1 : b;
   const int prw = PAIR ? ra.pair[b] : 0;
+  const int ctx0 = ctxl[b];
+  const int ctx1_any = PAIR ? ctxl[bn] : ctx0;
+  const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
+  const int64_t qb1_any = PAIR ? (qrows != nullptr ? qrows[bn] : int64_t(bn)) : qb;
+  if constexpr (PAIR) asm volatile("" : : "s"(prw), "s"(ctx0), "s"(ctx1_any), "s"(qb), "s"(qb1_any));   // one wait
   if (prw < 0) return;   // entry b runs in the workgroups of entry b - 1
   const int np_ = PAIR && prw > 0 ? 2 : 1;   // entries in this workgroup row
-  const int64_t qb = qrows != nullptr ? qrows[b] : int64_t(b);   // q / out row of entry b
-  const int64_t qb1 = np_ > 1 ? (qrows != nullptr ? qrows[b + 1] : int64_t(b + 1)) : qb;
+  const int64_t qb1 = np_ > 1 ? qb1_any : qb;
   const int nq_w = nkv_grid > 1 ? G : nq;   // query heads of this workgroup: heads g G .. g G + nq_w - 1
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, r4 = lane >> 4;
@@ -446,8 +453,7 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
 
   // ctx, this wave's block ids (lane i < PPW holds page i's) and Q go out together; a pair walks the longer
   // context's pages and masks each column's scores at its own entry's context
-  const int ctx0 = ctxl[b];
-  const int ctx1 = PAIR && np_ > 1 ? ctxl[b + 1] : ctx0;
+  const int ctx1 = PAIR && np_ > 1 ? ctx1_any : ctx0;
   const int ctx = PAIR ? max(ctx0, ctx1) : ctx0;
   const int ctx_col = PAIR && cj ? ctx1 : ctx0;
   int blk_lane;

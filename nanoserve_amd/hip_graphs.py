@@ -105,7 +105,10 @@ class StepGraph:
             self._pad(v, 0)
         self.dev_buf.copy_(self.twins[0])
         tok, pos, slots, lens, pairs, tables = self._views(self.dev_buf)
-        meta = DecodeMeta(runner.token_idx[:B], tables, lens, all_rows=True, pairs=pairs)
+        # the row pairing only where rows can share a table (speculative verification): the paired attention
+        # kernel costs a plain decode step ~0.4 us per layer
+        self.pairing = runner.pair_rows
+        meta = DecodeMeta(runner.token_idx[:B], tables, lens, all_rows=True, pairs=pairs if self.pairing else None)
         seqs = [SeqInput(1, ctx_len=1, use_kernel=True)] * B
 
         def forward():
@@ -158,7 +161,8 @@ class StepGraph:
             rows[i] = (t, L)
         for i in range(n, self.B):
             rows[i] = None
-        pair_rows(tables, pr)   # rows of one sequence (speculative verification) share its table
+        if self.pairing:
+            pair_rows(tables, pr)   # rows of one sequence (speculative verification) share its table
         self._pad(self.np[par], n)
 
     def launch(self, par: int) -> None:
@@ -169,8 +173,12 @@ class StepGraph:
 
 
 class DecodeGraphRunner:
-    def __init__(self, model: Qwen2Model, pool: PagedKVCache, max_seq_len: int, max_batch: int = BUCKETS[-1]):
+    def __init__(self, model: Qwen2Model, pool: PagedKVCache, max_seq_len: int, max_batch: int = BUCKETS[-1],
+                 pair_rows: bool = False):
+        """pair_rows: stage the row pairing (rows that share a block table run as one attention workgroup
+        row) -- for speculative verification, whose rows of one sequence share its table."""
         self.model, self.pool = model, pool
+        self.pair_rows = pair_rows
         self.block_size = pool.block_size
         self.buckets = [b for b in BUCKETS if b <= max_batch]
         self.max_bucket = self.buckets[-1]

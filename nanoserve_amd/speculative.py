@@ -59,7 +59,7 @@ class Lane:
         self.graphs = None
         if cuda_graphs:
             from nanoserve_amd.hip_graphs import DecodeGraphRunner
-            self.graphs = DecodeGraphRunner(model, self.pool, span)
+            self.graphs = DecodeGraphRunner(model, self.pool, span, pair_rows=True)
         self.graph_steps = 0
         self.forwards = 0
 
