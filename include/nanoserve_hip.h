@@ -258,6 +258,15 @@ int ns_embed_rope(const int64_t* token_ids, const int64_t* positions, int64_t n_
                   void* sin_out, float* row_sumsq, int dtype, void* stream);
 
 /*
+ * dst[i] = src[rows[i]] for i < n_rows: rows of row_bytes bytes (a multiple of 16), src rows src_stride_bytes
+ * apart (n_src of them), dst rows dst_stride_bytes apart; a row index outside [0, n_src) gives a zero row.
+ * Replaces the LM head's row selection x[:, logits, :] / the last row of each sequence
+ * (nanoserve/model.py:353-356).
+ */
+int ns_gather_rows(const void* src, int64_t src_stride_bytes, int64_t n_src, const int64_t* rows, int64_t n_rows,
+                   int64_t row_bytes, void* dst, int64_t dst_stride_bytes, void* stream);
+
+/*
  * GEMMs of the decode loop (bf16, K a multiple of 32; skinny kernels for 1 <= M <= 64, and for ns_gemm and
  * ns_gemm_silu_mul a tiled kernel above that; W row-major [N, K], x [M, K],
  * outputs row-major, every pointer 16-byte aligned). They replace the F.linear calls of

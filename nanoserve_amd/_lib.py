@@ -98,6 +98,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "ns_gemm_residual_norm_stats": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp,      # x w residual res_out sumsq
                                              _c_int, _c_int, _c_int, _c_int, _c_vp, _c_sz, _c_vp]),
     "ns_rms_norm_apply": (_c_int, [_c_vp, _c_vp, _c_vp, _c_f32, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
+    "ns_gather_rows": (_c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]),
     "ns_gemm_rope_qkv_fits": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "ns_gemm_rope_qkv": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

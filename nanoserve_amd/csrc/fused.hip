@@ -473,3 +473,36 @@ extern "C" int ns_embed_rope(const int64_t* token_ids, const int64_t* positions,
                        static_cast<float*>(cos_out), static_cast<float*>(sin_out), row_sumsq);
   return check_launch("embed_rope");
 }
+
+// ------------------------------------------------------------------------------------------ row gather
+// dst[i] = src[rows[i]] for rows of row_bytes bytes (16-byte pieces), the rows the LM head scores
+// (nanoserve/model.py:353-356: x[:, logits, :] or each sequence's last row). A row index outside [0, n_src)
+// yields a zero row. One workgroup of 64 threads per output row.
+namespace ns {
+__global__ __launch_bounds__(64) void gather_rows_kernel(const unsigned char* __restrict__ src, int64_t src_stride,
+                                                         int64_t n_src, const int64_t* __restrict__ rows,
+                                                         int64_t row_bytes, unsigned char* __restrict__ dst,
+                                                         int64_t dst_stride) {
+  const int64_t i = blockIdx.x, r = rows[i];
+  const bool ok = r >= 0 && r < n_src;
+  const f_u32x4_t* s = reinterpret_cast<const f_u32x4_t*>(src + (ok ? r : 0) * src_stride);
+  f_u32x4_t* d = reinterpret_cast<f_u32x4_t*>(dst + i * dst_stride);
+  for (int64_t c = threadIdx.x; c < row_bytes / 16; c += 64) d[c] = ok ? s[c] : f_u32x4_t{0u, 0u, 0u, 0u};
+}
+}  // namespace ns
+
+extern "C" int ns_gather_rows(const void* src, int64_t src_stride_bytes, int64_t n_src, const int64_t* rows,
+                              int64_t n_rows, int64_t row_bytes, void* dst, int64_t dst_stride_bytes, void* stream) {
+  NS_REQUIRE(n_rows >= 0 && n_rows < (int64_t(1) << 31), "gather_rows: n_rows %lld out of range", (long long)n_rows);
+  NS_REQUIRE(row_bytes > 0 && row_bytes % 16 == 0 && src_stride_bytes % 16 == 0 && dst_stride_bytes % 16 == 0,
+             "gather_rows: row_bytes %lld and strides must be positive multiples of 16", (long long)row_bytes);
+  NS_REQUIRE(src_stride_bytes >= row_bytes && dst_stride_bytes >= row_bytes, "gather_rows: strides below row_bytes");
+  NS_REQUIRE(src != nullptr && dst != nullptr && rows != nullptr && n_src >= 0, "gather_rows: null operand");
+  NS_REQUIRE((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 == 0,
+             "gather_rows: src and dst must be 16-byte aligned");
+  if (n_rows == 0) return NS_OK;
+  hipLaunchKernelGGL(ns::gather_rows_kernel, dim3(unsigned(n_rows)), dim3(64), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const unsigned char*>(src), src_stride_bytes, n_src, rows, row_bytes,
+                     static_cast<unsigned char*>(dst), dst_stride_bytes);
+  return check_launch("gather_rows");
+}

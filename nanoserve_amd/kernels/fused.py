@@ -107,3 +107,19 @@ def embed_rope(token_ids: torch.Tensor, positions: torch.Tensor, embed: torch.Te
                                         inv_freq.data_ptr(), head_dim, x.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                                         _lib.ptr(sumsq), _lib.dtype_code(embed), _lib.stream_of(embed)), "embed_rope")
     return x, cos, sin, sumsq
+
+
+def gather_rows(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """x[idx] for a 2-D x with contiguous rows (row bytes a multiple of 16) and int64 indices on its device, by
+    the HIP row gather (the LM head's row selection, nanoserve/model.py:353-356); other shapes index with torch."""
+    assert x.dim() == 2 and idx.dim() == 1
+    row_bytes = x.shape[1] * x.element_size()
+    if (x.stride(1) != 1 or row_bytes % 16 or (x.stride(0) * x.element_size()) % 16 or x.data_ptr() % 16
+            or idx.dtype != torch.int64 or idx.device != x.device or not idx.is_contiguous()):
+        return x[idx]
+    _lib.require_gpu(x, idx)
+    out = torch.empty(idx.shape[0], x.shape[1], device=x.device, dtype=x.dtype)
+    _lib.check(_lib.lib().ns_gather_rows(x.data_ptr(), x.stride(0) * x.element_size(), x.shape[0], idx.data_ptr(),
+                                         idx.shape[0], row_bytes, out.data_ptr(), row_bytes, _lib.stream_of(x)),
+               "gather_rows")
+    return out

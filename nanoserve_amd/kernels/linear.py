@@ -94,7 +94,8 @@ class NormedRows:
         n = idx.shape[0]
         sq = torch.zeros(self.sumsq.shape[0], NORM_ROWS, dtype=self.sumsq.dtype, device=self.sumsq.device)
         sq[:, :n] = self.sumsq[:, idx]
-        return NormedRows(self.r[idx].contiguous(), sq, self.weight, self.eps)
+        from nanoserve_amd.kernels.fused import gather_rows
+        return NormedRows(gather_rows(self.r, idx), sq, self.weight, self.eps)
 
 
 PACK_ROWS, PACK_GATE_UP, PACK_ROPE = 0, 1, 2   # tile row orders of csrc/packed_gemm.hip

@@ -437,6 +437,7 @@ class Qwen2Model:
         """Final-normed hidden states ([1, N, H] / [N, H] tensor, or a NormedRows) -> logits of the requested
         rows; with `greedy_out` (int64 [rows]) their argmax is written there too (fused into the LM head's
         launch where the kernel takes the shape)."""
+        from nanoserve_amd.kernels.fused import gather_rows
         from nanoserve_amd.kernels.linear import NormedRows, linear, linear_argmax
         if isinstance(x, torch.Tensor) and x.dim() == 3:
             x = x[0]
@@ -444,10 +445,13 @@ class Qwen2Model:
         if isinstance(logits, torch.Tensor):
             idx = logits
         elif logits == "last":
-            ends = torch.tensor([s.n_tokens for s in seqs], device=x.device).cumsum(0) - 1
-            idx = ends
+            ends, acc = [], -1
+            for s in seqs:
+                acc += s.n_tokens
+                ends.append(acc)
+            idx = torch.tensor(ends, dtype=torch.int64, device=x.device)   # each sequence's last row
         if idx is not None:
-            x = x.rows(idx) if isinstance(x, NormedRows) else x[idx]
+            x = x.rows(idx) if isinstance(x, NormedRows) else gather_rows(x, idx)
         # The packed LM head (up to 64 rows) and the row-major persistent one (up to 32 rows, K <= 2048) run on
         # persistent workgroups that normalise their activation fragments once, so they take the NormedRows
         # itself; beyond that every 64-row tile would repeat the row-statistics prologue, so the final norm is

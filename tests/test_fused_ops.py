@@ -143,3 +143,26 @@ def test_embed_rope_out_of_range_id_gives_a_zero_row(hiplib):
     x, _, _, _ = embed_rope(ids, torch.arange(4).cuda(), embed, torch.ones(32).cuda(), 64)
     assert torch.equal(x[0], embed[3]) and torch.equal(x[3], embed[9])
     assert not x[1].any() and not x[2].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gather_rows(hiplib, dtype):
+    """ns_gather_rows (the LM head's row selection, nanoserve/model.py:353-356): bitwise equal to x[idx] for
+    repeated, unordered indices, from a strided view; an index outside [0, n) gives a zero row; no rows is a no-op."""
+    from nanoserve_amd import _lib
+    from nanoserve_amd.kernels.fused import gather_rows
+    g = cpu_gen(71)
+    base = torch.randn(40, 1600, generator=g).to(dtype).cuda()
+    x = base[:, :1536]                                   # rows 1600 elements apart
+    idx = torch.tensor([39, 0, 7, 7, 21, 38], dtype=torch.int64, device="cuda")
+    assert torch.equal(gather_rows(x, idx).cpu(), x[idx].cpu())
+    out = torch.full((3, 1536), 5.0, dtype=dtype, device="cuda")
+    bad = torch.tensor([2, 40, -1], dtype=torch.int64, device="cuda")
+    L = _lib.lib()
+    rb = 1536 * x.element_size()
+    assert L.ns_gather_rows(x.data_ptr(), x.stride(0) * x.element_size(), 40, bad.data_ptr(), 3, rb, out.data_ptr(), rb,
+                            _lib.stream_of(x)) == 0, L.ns_last_error()
+    assert torch.equal(out[0].cpu(), x[2].cpu()) and not out[1:].cpu().any()
+    assert L.ns_gather_rows(x.data_ptr(), x.stride(0) * x.element_size(), 40, bad.data_ptr(), 0, rb, out.data_ptr(), rb,
+                            _lib.stream_of(x)) == 0
+    assert L.ns_gather_rows(x.data_ptr(), 8, 40, bad.data_ptr(), 3, rb, out.data_ptr(), rb, _lib.stream_of(x)) != 0
