@@ -355,9 +355,11 @@ int ns_rms_norm_apply(const void* r, const float* row_sumsq, const void* norm_w,
  * ns_rope_qkv contract on it (q, k, v outputs; k/v stored at slots when k_cache is given).
  * head_dim 64 or 128. Replaces rope_qkv(F.linear(h, qkv_w, qkv_b), ...) (nanoserve/model.py:231-234).
  */
-/* 1 when ns_gemm_rope_qkv takes M rows (normed: a normalised input): any M <= 64, and above that a plain input
- * with K <= 2048 up to 192 rows (the tile-16 kernel token-split: speculative verify batches). No counterpart
- * in the reference; it tells the caller when to run the GEMM and ns_rope_qkv separately instead. */
+/* 1 when ns_gemm_rope_qkv takes M rows (normed: a normalised input): any M <= 64; above that any plain input
+ * (up to 192 rows with K <= 2048 the tile-16 kernel token-split: speculative verify batches; otherwise the tiled
+ * kernel, whose epilogue rotates whole heads of its output tile: prefill chunks and mixed steps), and a
+ * normalised one with K <= 2048 up to NS_NORM_ROWS rows. No counterpart in the reference; it tells the caller
+ * when to run the GEMM and ns_rope_qkv separately instead. */
 int ns_gemm_rope_qkv_fits(int M, int K, int n_heads, int n_kv_heads, int head_dim, int normed);
 int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void* cos, const void* sin,
                      void* q, void* k, void* v, void* k_cache, void* v_cache, const int64_t* slots, int M,

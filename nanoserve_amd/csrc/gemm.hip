@@ -1087,6 +1087,13 @@ struct TgArgs {
   int tiles_m, tiles_n, splits, kps;   // kps: 32-wide k-steps per slice
   unsigned* cnt;
   float* part;
+  // ROPE epilogue (the ns_rope_qkv contract): per-row cos/sin tables [M, hd], outputs q [M, nh, hd],
+  // k / v [M, nkv, hd], optional caches at slots[m]
+  const bf16_t* cosb;
+  const bf16_t* sinb;
+  bf16_t *q, *k, *v, *kc, *vc;
+  const int64_t* slots;
+  int nh, nkv, hd;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tg_rsrc(const void* p, uint32_t bytes) {
@@ -1130,11 +1137,79 @@ __device__ __forceinline__ int tg_wrow(int r, int tn, int half) {
   }
 }
 
+// ROPE epilogue item c of a staged output row (fp32 products, columns n0 .. of the tile): dims d0 .. d0+7 and
+// d0 + hd/2 .. of one head of row gm. The values are rounded as the STORE epilogue stores them (bias added,
+// then bf16), then rotated with the roundings of rope_qkv: lo = round(xl cl) - round(xh sl), hi = round(xh ch)
+// + round(xl sh); value heads pass through. A tile holds whole heads (its width is a multiple of hd).
+__device__ __forceinline__ void tg_rope_item(const TgArgs& a, const float* crow, int gm, int n0, int c) {
+  const int gph = a.hd >> 4, hh = a.hd >> 1;   // 8-dim groups per half head
+  const int ht = c / gph, d0 = 8 * (c - ht * gph), col = ht * a.hd + d0, gn = n0 + col;
+  if (gm >= a.M || gn >= a.N) return;
+  const int head = gn / a.hd;
+  float xl[8], xh[8], lo[8], hi[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xl[e] = crow[col + e];
+    xh[e] = crow[col + hh + e];
+  }
+  if (a.bias != nullptr) {
+    float bl[8], bh[8];
+    load_bf16x8(a.bias + gn, bl);
+    load_bf16x8(a.bias + gn + hh, bh);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xl[e] += bl[e];
+      xh[e] += bh[e];
+    }
+  }
+  if (head < a.nh + a.nkv) {
+    float cl[8], ch[8], sl[8], sh[8];
+    const bf16_t* cr = a.cosb + int64_t(gm) * a.hd + d0;
+    const bf16_t* sr = a.sinb + int64_t(gm) * a.hd + d0;
+    load_bf16x8(cr, cl);
+    load_bf16x8(cr + hh, ch);
+    load_bf16x8(sr, sl);
+    load_bf16x8(sr + hh, sh);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float l = tg_round(xl[e]), h = tg_round(xh[e]);
+      lo[e] = tg_round(l * cl[e]) - tg_round(h * sl[e]);
+      hi[e] = tg_round(h * ch[e]) + tg_round(l * sh[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      lo[e] = xl[e];
+      hi[e] = xh[e];
+    }
+  }
+  bf16_t* dst;
+  bf16_t* cdst = nullptr;
+  if (head < a.nh) {
+    dst = a.q + (int64_t(gm) * a.nh + head) * a.hd;
+  } else if (head < a.nh + a.nkv) {
+    const int kh = head - a.nh;
+    dst = a.k + (int64_t(gm) * a.nkv + kh) * a.hd;
+    if (a.kc != nullptr) cdst = a.kc + (a.slots[gm] * a.nkv + kh) * a.hd;
+  } else {
+    const int vh = head - a.nh - a.nkv;
+    dst = a.v + (int64_t(gm) * a.nkv + vh) * a.hd;
+    if (a.vc != nullptr) cdst = a.vc + (a.slots[gm] * a.nkv + vh) * a.hd;
+  }
+  store_bf16x8(dst + d0, lo);
+  store_bf16x8(dst + d0 + hh, hi);
+  if (cdst != nullptr) {
+    store_bf16x8(cdst + d0, lo);
+    store_bf16x8(cdst + d0 + hh, hi);
+  }
+}
+
 template <int EPI, int FM, int FN, int NW, int WM>
 __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW, WM>::WG_PER_CU)) void tiled_gemm_kernel(
     TgArgs a) {
   using SH = TgShape<FM, FN, NW, WM>;
-  static_assert(EPI == EPI_STORE || (WM == 2 && FN % 4 == 0), "the SiLU epilogue pairs gate and up tiles of a 2-row wave grid");
+  static_assert(EPI != EPI_SILU || (WM == 2 && FN % 4 == 0), "the SiLU epilogue pairs gate and up tiles of a 2-row wave grid");
+  static_assert(EPI != EPI_RESNORM, "no residual epilogue on the tiled kernel");
   constexpr int BM = SH::BM, BN = SH::BN, NT = SH::NT, S = SH::S;
   __shared__ __align__(16) unsigned char lds[SH::LDS];
   __shared__ unsigned s_last;
@@ -1277,11 +1352,12 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
   }
 
   // Lane layout of acc[i][j]: column 16 FN wn + 16 j + l % 16 of the tile, rows 16 FM wm + 16 i + 4 (l / 16) + r.
-  if constexpr (EPI == EPI_STORE) {
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ROPE) {
     // the fp32 tile through LDS in passes of 64 rows (pass p: the waves with wm == p / (FM / 4), their
-    // m-tiles 4 (p % (FM / 4)) .. + 3), then items (row m, 8 columns) of 16 bytes
+    // m-tiles 4 (p % (FM / 4)) .. + 3), then items (row m, 8 columns) of 16 bytes; ROPE: items (row m,
+    // 8 dims of a head's low half and the matching 8 of its high half)
     float* C = reinterpret_cast<float*>(lds);
-    constexpr int CP = SH::CP, PASSES = BM / TG_CROWS, PW = FM / 4, IPR = BN / 8;
+    constexpr int CP = SH::CP, PASSES = BM / TG_CROWS, PW = FM / 4, IPR = EPI == EPI_ROPE ? BN / 16 : BN / 8;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       if (wm == p / PW) {
@@ -1298,6 +1374,10 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
 #pragma unroll 2
       for (int it = tid; it < TG_CROWS * IPR; it += NT) {
         const int m = it / IPR, c8 = it % IPR, gm = mb + m, gn = BN * tn + 8 * c8;
+        if constexpr (EPI == EPI_ROPE) {
+          tg_rope_item(a, C + m * CP, gm, BN * tn, c8);
+          continue;
+        }
         if (gm >= M || gn >= N) continue;
         float v[8];
 #pragma unroll
@@ -1634,13 +1714,7 @@ static TgPlan tg_plan(int M, int N, int K, bool silu) {
   p.bytes = p.splits > 1 ? G_CNT_BYTES + align256(sizeof(float) * size_t(tiles) * p.splits * part) : 0;
   return p;
 }
-template <int EPI>
-static int launch_tiled(const void* x, const void* w, const void* bias, void* y, int M, int N, int K, void* ws,
-                        size_t ws_bytes, hipStream_t st) {
-  // 32-bit buffer offsets: every row offset of X and W (plus a tile's overhang) must fit
-  NS_REQUIRE((int64_t(M) + 256) * K * 2 < (int64_t(1) << 31) && (int64_t(N) + 256) * K * 2 < (int64_t(1) << 31),
-             "gemm: X [%d, %d] or W [%d, %d] too large for 32-bit buffer offsets", M, K, N, K);
-  const TgPlan p = tg_plan(M, N, K, EPI == EPI_SILU);
+static TgArgs tg_args(const void* x, const void* w, const void* bias, void* y, int M, int N, int K) {
   TgArgs a{};
   a.x = static_cast<const bf16_t*>(x);
   a.w = static_cast<const bf16_t*>(w);
@@ -1649,6 +1723,17 @@ static int launch_tiled(const void* x, const void* w, const void* bias, void* y,
   a.M = M;
   a.N = N;
   a.K = K;
+  return a;
+}
+// a: operands, shape and (ROPE) the epilogue's fields; the plan fills the rest
+template <int EPI>
+static int launch_tiled(TgArgs a, void* ws, size_t ws_bytes, hipStream_t st) {
+  const int M = a.M, N = a.N, K = a.K;
+  // 32-bit buffer offsets: every row offset of X and W (plus a tile's overhang) must fit
+  NS_REQUIRE((int64_t(M) + 256) * K * 2 < (int64_t(1) << 31) && (int64_t(N) + 256) * K * 2 < (int64_t(1) << 31),
+             "gemm: X [%d, %d] or W [%d, %d] too large for 32-bit buffer offsets", M, K, N, K);
+  const TgPlan p = tg_plan(M, N, K, EPI == EPI_SILU);
+  NS_REQUIRE(EPI != EPI_ROPE || (tg_bn(p.shape) % a.hd == 0), "gemm(tiled): head_dim %d does not divide the tile", a.hd);
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
   a.splits = p.splits;
@@ -1664,12 +1749,13 @@ static int launch_tiled(const void* x, const void* w, const void* bias, void* y,
     a.part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + G_CNT_BYTES);
   }
   const dim3 grid(unsigned(p.tiles_m * p.tiles_n * p.splits));
+  constexpr int EPIT = EPI == EPI_SILU ? EPI_STORE : EPI;   // the 256 x 128 and 8-wave 128^2 tiles: no SiLU
   if (p.shape == TG_BIG)
     hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 8, 4, 8, 2>), grid, dim3(TgBig::NT), 0, st, a);
-  else if (EPI == EPI_STORE && p.shape == TG_TALL)
-    hipLaunchKernelGGL((tiled_gemm_kernel<EPI_STORE, 4, 4, 8, 4>), grid, dim3(TgTall::NT), 0, st, a);
-  else if (EPI == EPI_STORE && p.shape == TG_SMALL8)
-    hipLaunchKernelGGL((tiled_gemm_kernel<EPI_STORE, 4, 2, 8, 2>), grid, dim3(TgSmall8::NT), 0, st, a);
+  else if (EPI != EPI_SILU && p.shape == TG_TALL)
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPIT, 4, 4, 8, 4>), grid, dim3(TgTall::NT), 0, st, a);
+  else if (EPI != EPI_SILU && p.shape == TG_SMALL8)
+    hipLaunchKernelGGL((tiled_gemm_kernel<EPIT, 4, 2, 8, 2>), grid, dim3(TgSmall8::NT), 0, st, a);
   else
     hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 4, 4, 4, 2>), grid, dim3(TgSmall::NT), 0, st, a);
   return check_launch("gemm(tiled)");
@@ -1743,7 +1829,7 @@ extern "C" int ns_gemm(const void* x, const void* w, const void* bias, void* y, 
       if ((st = bind_workspace(a, pm, ws, ws_bytes)) != NS_OK) return st;
       return launch<EPI_STORE>(a, reinterpret_cast<hipStream_t>(stream));
     }
-    return launch_tiled<EPI_STORE>(x, w, bias, y, M, N, K, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+    return launch_tiled<EPI_STORE>(tg_args(x, w, bias, y, M, N, K), ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
   }
   GemmArgs a = base_args(x, w, M, N, K);
   a.bias = static_cast<const bf16_t*>(bias);
@@ -1792,7 +1878,7 @@ extern "C" int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out,
   NS_REQUIRE(out != nullptr && aligned16(out), "gemm_silu_mul: output must be 16-byte aligned");
   if (M > G_MAX_M) {
     NS_REQUIRE(x_sumsq == nullptr, "gemm_silu_mul: a normalised input (x_sumsq) needs M <= %d", G_MAX_M);
-    return launch_tiled<EPI_SILU>(x, w_gate_up, nullptr, out, M, N2, K, ws, ws_bytes,
+    return launch_tiled<EPI_SILU>(tg_args(x, w_gate_up, nullptr, out, M, N2, K), ws, ws_bytes,
                                   reinterpret_cast<hipStream_t>(stream));
   }
   GemmArgs a = base_args(x, w_gate_up, M, N2, K);
@@ -1850,7 +1936,8 @@ extern "C" int ns_rms_norm_apply(const void* r, const float* row_sumsq, const vo
 extern "C" int ns_gemm_rope_qkv_fits(int M, int K, int n_heads, int n_kv_heads, int head_dim, int normed) {
   const int N = (n_heads + 2 * n_kv_heads) * head_dim;
   if (M < 1 || K < 32 || K % 32 != 0 || n_heads < 1 || n_kv_heads < 1 || (head_dim != 64 && head_dim != 128)) return 0;
-  return M <= G_MAX_M || t16_large_m(M, K, N / 16, normed != 0) ? 1 : 0;
+  // above 64 rows: the tile-16 kernel, else (a plain input) the tiled kernel's ROPE epilogue
+  return M <= G_MAX_M || t16_large_m(M, K, N / 16, normed != 0) || normed == 0 ? 1 : 0;
 }
 
 extern "C" int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, const void* cos, const void* sin,
@@ -1862,9 +1949,9 @@ extern "C" int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, 
   const int N = (n_heads + 2 * n_kv_heads) * head_dim;
   int st = check_common(x, w, M, N, K, dtype, INT_MAX);
   if (st != NS_OK) return st;
-  NS_REQUIRE(M <= G_MAX_M || t16_large_m(M, K, N / 16, x_sumsq != nullptr),
-             "gemm_rope_qkv: M=%d above %d needs a plain input, K <= %d and at most %d rows (ns_gemm_rope_qkv_fits)", M,
-             G_MAX_M, T16_MAX_K, t16_max_m());
+  NS_REQUIRE(M <= G_MAX_M || t16_large_m(M, K, N / 16, x_sumsq != nullptr) || x_sumsq == nullptr,
+             "gemm_rope_qkv: a normalised input above %d rows needs K <= %d and at most %d rows (ns_gemm_rope_qkv_fits)",
+             G_MAX_M, T16_MAX_K, G_NORM_ROWS);
   NS_REQUIRE((k_cache == nullptr) == (v_cache == nullptr) && (k_cache == nullptr || slots != nullptr),
              "gemm_rope_qkv: give both caches and slots, or none");
   NS_REQUIRE(cos != nullptr && sin != nullptr && q != nullptr && k != nullptr && v != nullptr,
@@ -1872,6 +1959,22 @@ extern "C" int ns_gemm_rope_qkv(const void* x, const void* w, const void* bias, 
   NS_REQUIRE(aligned16(cos) && aligned16(sin) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(k_cache) &&
                  aligned16(v_cache),
              "gemm_rope_qkv: operands must be 16-byte aligned");
+  if (M > G_MAX_M && !t16_large_m(M, K, N / 16, x_sumsq != nullptr)) {
+    TgArgs t = tg_args(x, w, bias, nullptr, M, N, K);
+    t.cosb = static_cast<const bf16_t*>(cos);
+    t.sinb = static_cast<const bf16_t*>(sin);
+    t.q = static_cast<bf16_t*>(q);
+    t.k = static_cast<bf16_t*>(k);
+    t.v = static_cast<bf16_t*>(v);
+    t.kc = static_cast<bf16_t*>(k_cache);
+    t.vc = static_cast<bf16_t*>(v_cache);
+    t.slots = slots;
+    t.nh = n_heads;
+    t.nkv = n_kv_heads;
+    t.hd = head_dim;
+    NS_REQUIRE(bias == nullptr || aligned16(bias), "gemm_rope_qkv: bias must be 16-byte aligned");
+    return launch_tiled<EPI_ROPE>(t, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+  }
   GemmArgs a = base_args(x, w, M, N, K);
   a.bias = static_cast<const bf16_t*>(bias);
   a.cosb = static_cast<const bf16_t*>(cos);

@@ -139,24 +139,26 @@ def test_linear_residual_rms_norm(hiplib, M, N, K, norm):
         assert h is None
 
 
-@pytest.mark.parametrize("M", [1, 20, 32, 64, 65, 96, 120, 192, 193])
+@pytest.mark.parametrize("M", [1, 20, 32, 64, 65, 96, 120, 192, 193, 1552])
 @pytest.mark.parametrize("nh,nkv,hd,K", [(12, 2, 128, 1536), (14, 2, 64, 896), (16, 2, 128, 2048)])
 def test_linear_rope_qkv_and_cache_write(hiplib, M, nh, nkv, hd, K):
     """M <= 64: the skinny kernels; 65..192 rows: the tile-16 kernel in 16-token blocks (verify batches);
-    193: the GEMM and the RoPE kernel separately."""
+    193 and 1552 (the config-4 mixed step): the tiled kernel with the RoPE epilogue."""
     from nanoserve_amd import _lib
     from nanoserve_amd.kernels.linear import linear_rope_qkv
-    assert _lib.lib().ns_gemm_rope_qkv_fits(M, K, nh, nkv, hd, 0) == (1 if M <= 192 else 0)
+    assert _lib.lib().ns_gemm_rope_qkv_fits(M, K, nh, nkv, hd, 0) == 1
+    assert _lib.lib().ns_gemm_rope_qkv_fits(M, K, nh, nkv, hd, 1) == (1 if M <= 128 else 0)
     N = (nh + 2 * nkv) * hd
     x, w = operands(M, N, K, seed=7)
     g = cpu_gen(8)
     b = (torch.randn(N, generator=g) * 0.1).to(BF)
     cos, sin = ops.rope_tables(torch.randint(0, 4000, (M,), generator=g), hd, 1e6, BF)
-    slots = torch.randperm(16 * 16, generator=g)[:M]
-    kc = torch.zeros(16, 16, nkv, hd, dtype=BF, device="cuda")
+    nb = max(16, 2 * (M // 16 + 1))   # cache blocks of 16 slots, twice the rows
+    slots = torch.randperm(nb * 16, generator=g)[:M]
+    kc = torch.zeros(nb, 16, nkv, hd, dtype=BF, device="cuda")
     vc = torch.zeros_like(kc)
     q, k, v = linear_rope_qkv(x.cuda(), w.cuda(), b.cuda(), cos.cuda(), sin.cuda(), nh, nkv, hd, kc, vc, slots.cuda())
-    rk, rv = torch.zeros(16, 16, nkv, hd, dtype=BF), torch.zeros(16, 16, nkv, hd, dtype=BF)
+    rk, rv = torch.zeros(nb, 16, nkv, hd, dtype=BF), torch.zeros(nb, 16, nkv, hd, dtype=BF)
     qkv = ref_linear(x, w, b)
     q0, k0, v0 = ops.rope_qkv(qkv, cos, sin, nh, nkv, hd, rk, rv, slots)
     # rotation mixes two inputs with |cos|, |sin| <= 1: an input error e becomes <= 2e (+ roundings)
@@ -168,7 +170,7 @@ def test_linear_rope_qkv_and_cache_write(hiplib, M, nh, nkv, hd, K):
     bf16_check(v, v0, "v", e.view(M, -1, hd)[:, nh + nkv:])
     flat_k, flat_v = kc.cpu().view(-1, nkv, hd), vc.cpu().view(-1, nkv, hd)
     assert torch.equal(flat_k[slots], k.cpu()) and torch.equal(flat_v[slots], v.cpu())
-    untouched = torch.ones(16 * 16, dtype=torch.bool)
+    untouched = torch.ones(nb * 16, dtype=torch.bool)
     untouched[slots] = False
     assert not flat_k[untouched].any() and not flat_v[untouched].any()
 

@@ -139,3 +139,38 @@ def test_residual_row_statistics_above_64_rows_through_the_c_abi(hiplib, M, N, K
     h = NormedRows(r, sq, nw, 1e-6).tensor().cpu()
     same, ulps = ops.bf16_ulp_close(h, ops.rms_norm(r.cpu(), nw.cpu(), 1e-6))
     assert same >= 0.99 and ulps <= 1.0, (same, ulps)
+
+
+@pytest.mark.parametrize("M,nh,nkv,hd,K,bias,cache", [
+    (193, 12, 2, 128, 1536, True, True),     # 4-wave 128 x 128 tiles, a partial last row tile
+    (1552, 12, 2, 128, 1536, True, True),    # 8-wave 128 x 128 tiles: the config-4 mixed step's QKV
+    (1552, 14, 2, 64, 896, True, False),     # two 64-wide heads per tile, no cache
+    (300, 16, 2, 128, 2048, False, True),
+    (512, 16, 2, 128, 4096, True, True),     # long K: K slices merged before the epilogue
+    (8192, 12, 2, 128, 1536, True, True),    # 256 x 256 tiles (two heads each)
+])
+def test_tiled_rope_epilogue_equals_gemm_then_rope(hiplib, M, nh, nkv, hd, K, bias, cache):
+    """Above 192 rows ns_gemm_rope_qkv rotates in the tiled kernel's epilogue: q, k, v and the cache pages
+    are bit-identical to the tiled STORE product followed by the RoPE kernel (the unfused route, each
+    checked against the oracle elsewhere), on the same plan."""
+    from nanoserve_amd.kernels.fused import rope_qkv
+    from nanoserve_amd.kernels.linear import linear, linear_rope_qkv
+    N = (nh + 2 * nkv) * hd
+    x, w = operands(M, N, K, seed=M + hd)
+    g = cpu_gen(M)
+    b = (torch.randn(N, generator=g) * 0.1).to(BF).cuda() if bias else None
+    cos, sin = ops.rope_tables(torch.randint(0, 32768, (M,), generator=g), hd, 1e6, BF)
+    cos, sin = cos.cuda(), sin.cuda()
+    nb = 2 * (M // 16 + 1)
+    slots = torch.randperm(nb * 16, generator=g)[:M].cuda() if cache else None
+    caches = []
+    for _ in range(2):
+        kc = torch.zeros(nb, 16, nkv, hd, dtype=BF, device="cuda") if cache else None
+        caches.append((kc, torch.zeros_like(kc) if cache else None))
+    dx, dw = x.cuda(), w.cuda()
+    fused = linear_rope_qkv(dx, dw, b, cos, sin, nh, nkv, hd, *caches[0], slots)
+    plain = rope_qkv(linear(dx, dw, b), cos, sin, nh, nkv, hd, *caches[1], slots)
+    for name, a, r in zip("qkv", fused, plain):
+        assert torch.equal(a, r), f"{name}: {(a.float() - r.float()).abs().max().item()}"
+    if cache:
+        assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
