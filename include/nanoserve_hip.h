@@ -333,7 +333,9 @@ int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out, int M, int
 /*
  * Projection + residual add + the statistics of the RMSNorm that follows: o = round(x W^T);
  * res_out = round(residual + o); row_sumsq[p][m] = sum over columns 16p .. 16p+15 of res_out[m]^2 (fp32,
- * [ceil(N/16)][NS_NORM_ROWS], may be NULL). N a multiple of 8.
+ * [ceil(N/16)][NS_NORM_ROWS], may be NULL). N a multiple of 8. M <= NS_NORM_ROWS, or any M above 192 with
+ * row_sumsq NULL (the tiled kernel's residual epilogue: prefill chunks and mixed steps, whose RMSNorm then
+ * runs as ns_rms_norm on res_out).
  * With a normalised consumer (or ns_rms_norm_apply) this replaces rms_norm(F.linear(o, o_w), ln2, eps,
  * residual=x) (nanoserve/model.py:256, fused.py:45) and x + F.linear(a, down_w) followed by the next
  * layer's rms_norm (model.py:257, :227-231).

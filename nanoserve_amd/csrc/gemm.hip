@@ -1087,6 +1087,7 @@ struct TgArgs {
   int tiles_m, tiles_n, splits, kps;   // kps: 32-wide k-steps per slice
   unsigned* cnt;
   float* part;
+  const bf16_t* res;   // RESNORM epilogue: y = round(res + round(X W^T)) (the residual sum, no statistics)
   // ROPE epilogue (the ns_rope_qkv contract): per-row cos/sin tables [M, hd], outputs q [M, nh, hd],
   // k / v [M, nkv, hd], optional caches at slots[m]
   const bf16_t* cosb;
@@ -1209,7 +1210,6 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
     TgArgs a) {
   using SH = TgShape<FM, FN, NW, WM>;
   static_assert(EPI != EPI_SILU || (WM == 2 && FN % 4 == 0), "the SiLU epilogue pairs gate and up tiles of a 2-row wave grid");
-  static_assert(EPI != EPI_RESNORM, "no residual epilogue on the tiled kernel");
   constexpr int BM = SH::BM, BN = SH::BN, NT = SH::NT, S = SH::S;
   __shared__ __align__(16) unsigned char lds[SH::LDS];
   __shared__ unsigned s_last;
@@ -1266,6 +1266,23 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = g_float4_t{0.f, 0.f, 0.f, 0.f};
   const uint32_t lds0 = tg_lds_addr(lds);
+
+  // RESNORM: the thread's residual pieces for the epilogue's items (item k of 64-row pass p: it = tid + k NT,
+  // row it / (BN / 8), 8 columns it % (BN / 8)), loaded before the K loop so their latency hides under it,
+  // when they fit in 8 registers of 16 bytes (else each item loads its own). Addresses are clamped into the
+  // residual, so the loads are unconditional; pieces past M or N are never used.
+  constexpr int RIPR = BN / 8, RIPT = TG_CROWS * RIPR / NT;
+  static_assert(TG_CROWS * RIPR % NT == 0 && TG_CROWS * (BN / 16) % NT == 0, "epilogue items per thread");
+  constexpr int RPRE = EPI == EPI_RESNORM && BM / TG_CROWS * RIPT <= 8 ? BM / TG_CROWS * RIPT : 0;
+  g_u32x4_t rres[RPRE > 0 ? RPRE : 1];
+  if constexpr (RPRE > 0) {
+#pragma unroll
+    for (int u = 0; u < RPRE; ++u) {
+      const int it = tid + (u % RIPT) * NT;
+      const int gm = min(m0 + TG_CROWS * (u / RIPT) + it / RIPR, M - 1), gn = min(BN * tn + 8 * (it % RIPR), N - 8);
+      rres[u] = *reinterpret_cast<const g_u32x4_t*>(a.res + int64_t(gm) * N + gn);
+    }
+  }
 
   // Step q: the MFMAs of step q, row by row, from A and Bc; between them the DMA of stage q + S, and the
   // reads of step q + 1: A[i] as soon as row i is issued, Bn spread over the step.
@@ -1352,10 +1369,10 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
   }
 
   // Lane layout of acc[i][j]: column 16 FN wn + 16 j + l % 16 of the tile, rows 16 FM wm + 16 i + 4 (l / 16) + r.
-  if constexpr (EPI == EPI_STORE || EPI == EPI_ROPE) {
+  if constexpr (EPI != EPI_SILU) {
     // the fp32 tile through LDS in passes of 64 rows (pass p: the waves with wm == p / (FM / 4), their
-    // m-tiles 4 (p % (FM / 4)) .. + 3), then items (row m, 8 columns) of 16 bytes; ROPE: items (row m,
-    // 8 dims of a head's low half and the matching 8 of its high half)
+    // m-tiles 4 (p % (FM / 4)) .. + 3), then items (row m, 8 columns) of 16 bytes (RESNORM: plus the
+    // residual's 8); ROPE: items (row m, 8 dims of a head's low half and the matching 8 of its high half)
     float* C = reinterpret_cast<float*>(lds);
     constexpr int CP = SH::CP, PASSES = BM / TG_CROWS, PW = FM / 4, IPR = EPI == EPI_ROPE ? BN / 16 : BN / 8;
 #pragma unroll
@@ -1371,9 +1388,10 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
       }
       tg_barrier();   // LDS only: the global stores of the previous pass need not land first
       const int mb = m0 + TG_CROWS * p;
-#pragma unroll 2
-      for (int it = tid; it < TG_CROWS * IPR; it += NT) {
-        const int m = it / IPR, c8 = it % IPR, gm = mb + m, gn = BN * tn + 8 * c8;
+      constexpr int IPT = TG_CROWS * IPR / NT;   // items per thread and pass
+#pragma unroll
+      for (int k = 0; k < IPT; ++k) {
+        const int it = tid + k * NT, m = it / IPR, c8 = it % IPR, gm = mb + m, gn = BN * tn + 8 * c8;
         if constexpr (EPI == EPI_ROPE) {
           tg_rope_item(a, C + m * CP, gm, BN * tn, c8);
           continue;
@@ -1391,6 +1409,18 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
           } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] += gn + e < N ? bf16_to_f32(a.bias[gn + e]) : 0.f;
+          }
+        }
+        if constexpr (EPI == EPI_RESNORM) {   // N % 8 == 0 (checked by the entry point)
+          g_u32x4_t u;
+          if constexpr (RPRE > 0)
+            u = rres[p * IPT + k];
+          else
+            u = *reinterpret_cast<const g_u32x4_t*>(a.res + int64_t(gm) * N + gn);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[2 * e] = __uint_as_float(u[e] << 16) + tg_round(v[2 * e]);
+            v[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u) + tg_round(v[2 * e + 1]);
           }
         }
         bf16_t* dst = a.y + int64_t(gm) * N + gn;
@@ -1892,11 +1922,17 @@ extern "C" int ns_gemm_silu_mul(const void* x, const void* w_gate_up, void* out,
 extern "C" int ns_gemm_residual_norm_stats(const void* x, const void* w, const void* residual, void* res_out,
                                            float* row_sumsq, int M, int N, int K, int dtype, void* ws,
                                            size_t ws_bytes, void* stream) {
-  int st = check_common(x, w, M, N, K, dtype, G_NORM_ROWS);
+  const bool tiled = row_sumsq == nullptr && M > t16_max_m();   // prefill chunks and mixed steps: the sum only
+  int st = check_common(x, w, M, N, K, dtype, tiled ? INT_MAX : G_NORM_ROWS);
   if (st != NS_OK) return st;
   NS_REQUIRE(N % 8 == 0, "gemm_residual_norm_stats: row length %d must be a multiple of 8", N);
   NS_REQUIRE(residual != nullptr && res_out != nullptr, "gemm_residual_norm_stats: residual and res_out required");
   NS_REQUIRE(aligned16(residual) && aligned16(res_out), "gemm_residual_norm_stats: operands must be 16-byte aligned");
+  if (tiled) {
+    TgArgs t = tg_args(x, w, nullptr, res_out, M, N, K);
+    t.res = static_cast<const bf16_t*>(residual);
+    return launch_tiled<EPI_RESNORM>(t, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+  }
   GemmArgs a = base_args(x, w, M, N, K);
   a.residual = static_cast<const bf16_t*>(residual);
   a.res_out = static_cast<bf16_t*>(res_out);

@@ -35,6 +35,7 @@ from nanoserve_amd import _lib
 from nanoserve_amd.kernels.fused import rms_norm, rope_qkv, silu_mul
 
 SKINNY_MAX_M = 64
+TILED_MIN_M = 193   # above 192 rows every plain product runs the tiled kernel (csrc/gemm.hip T16_LARGE_M)
 NORM_COLS = 16   # columns per row-sum partial of a NormedRows
 NORM_ROWS = 128  # rows the row-sum buffer holds (NS_NORM_ROWS: decode batches and verify batches)
 
@@ -302,7 +303,22 @@ def linear_residual_rms_norm(x: torch.Tensor, w, residual: torch.Tensor, norm_w:
             return None, res_out
         return NormedRows(res_out, sumsq, norm_w, eps), res_out
     # above 64 rows the plain product and the RMSNorm kernel: the GEMMs' residual epilogue plus a consumer that
-    # normalises on load (or the materialised norm) measured slower on verify batches than the separate pass
+    # normalises on load (or the materialised norm) measured slower on verify batches than the separate pass.
+    # Above 192 rows (the tiled kernel) the product's epilogue adds the residual and the norm kernel reads only
+    # the sum (half the norm pass's traffic).
+    if (x.shape[0] >= TILED_MIN_M and hip_ok(x, w) and residual.is_contiguous() and w.shape[0] % 8 == 0
+            and residual.data_ptr() % 16 == 0 and residual.dtype == w.dtype and residual.shape == (x.shape[0], w.shape[0])):
+        x = _tiled_input(x)
+        M, K = x.shape
+        N = w.shape[0]
+        res_out = torch.empty(M, N, device=x.device, dtype=x.dtype)
+        wsp, wsn = _ws_args(x, N)
+        _lib.check(_lib.lib().ns_gemm_residual_norm_stats(
+            x.data_ptr(), w.data_ptr(), residual.data_ptr(), res_out.data_ptr(), None, M, N, K, 1, wsp, wsn,
+            _lib.stream_of(x)), "linear_residual_rms_norm (tiled)")
+        if norm_w is None:
+            return None, res_out
+        return rms_norm(res_out, norm_w, eps), res_out
     if not skinny_ok(x, w) or not residual.is_contiguous() or w.shape[0] % 8 != 0:
         y = linear(x, w)
         if norm_w is None:

@@ -174,3 +174,24 @@ def test_tiled_rope_epilogue_equals_gemm_then_rope(hiplib, M, nh, nkv, hd, K, bi
         assert torch.equal(a, r), f"{name}: {(a.float() - r.float()).abs().max().item()}"
     if cache:
         assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+
+
+@pytest.mark.parametrize("M,N,K", [(193, 1536, 1536), (1552, 1536, 1536), (1552, 1536, 8960), (1665, 2048, 4864),
+                                   (8192, 1536, 1536)])
+def test_tiled_residual_epilogue_equals_product_then_norm(hiplib, M, N, K):
+    """Above 192 rows linear_residual_rms_norm adds the residual in the tiled kernel's epilogue and runs the
+    RMSNorm kernel on the sum alone: the sum and the normalised rows are bit-identical to the plain product
+    followed by the residual RMSNorm kernel (8960-long K: K-sliced plans merge before the epilogue)."""
+    from nanoserve_amd.kernels.fused import rms_norm
+    from nanoserve_amd.kernels.linear import linear, linear_residual_rms_norm
+    x, w = operands(M, N, K, seed=M + K)
+    g = cpu_gen(M + 1)
+    res = torch.randn(M, N, generator=g).to(BF).cuda()
+    nw = (1 + 0.1 * torch.randn(N, generator=g)).to(BF).cuda()
+    dx, dw = x.cuda(), w.cuda()
+    h, r = linear_residual_rms_norm(dx, dw, res, nw, 1e-6)
+    h0, r0 = rms_norm(linear(dx, dw), nw, 1e-6, residual=res)
+    assert torch.equal(r, r0), f"sum: {(r.float() - r0.float()).abs().max().item()}"
+    assert torch.equal(h, h0), f"norm: {(h.float() - h0.float()).abs().max().item()}"
+    none, r1 = linear_residual_rms_norm(dx, dw, res, None, 1e-6)
+    assert none is None and torch.equal(r1, r0)
