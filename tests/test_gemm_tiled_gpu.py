@@ -27,7 +27,7 @@ def check_rows(M):
     return torch.tensor(rows)
 
 
-@pytest.mark.parametrize("M", [65, 96, 120, 1552])
+@pytest.mark.parametrize("M", [65, 96, 120, 300, 1552])
 @pytest.mark.parametrize("N,K,bias", [(2048, 1536, True), (1536, 8960, False), (1536, 1536, False), (1003, 896, True),
                                       (17920, 1536, True)])
 def test_tiled_linear(hiplib, M, N, K, bias):
