@@ -1020,10 +1020,12 @@ __global__ __launch_bounds__(64) void rms_norm_apply_kernel(const bf16_t* __rest
 
 // ------------------------------------------------------------------------------------- tiled GEMM (M > 64)
 // Prefill chunks, mixed steps and speculative verify batches: Y[M, N] = X[M, K] . W[N, K]^T for any M, bf16
-// in, fp32 accumulate, with the STORE (+ bias) and SILU epilogues of the skinny kernels.
-//   * BM x BN output tiles, NW waves in a 2 x (NW / 2) grid, each a (16 FM) x (16 FN) block of
-//     mfma_f32_16x16x32_bf16 tiles. Shapes: 256 x 256 (8 waves of 128 x 64, one workgroup per CU) and
-//     128 x 128 (4 waves of 64 x 64, two per CU). A CU's vector memory path moves about 64 bytes per clock
+// in, fp32 accumulate, with the STORE (+ bias), SILU, residual-add (RESNORM) and RoPE + K/V-write (ROPE)
+// epilogues of the skinny kernels.
+//   * BM x BN output tiles, NW waves in a WM x (NW / WM) grid, each a (16 FM) x (16 FN) block of
+//     mfma_f32_16x16x32_bf16 tiles. Shapes: 256 x 256 (8 waves of 128 x 64, one workgroup per CU), 256 x 128
+//     (8 of 64 x 64), 128 x 128 (8 of 64 x 32, or 4 of 64 x 64 two per CU) and 128 x 96 (8 of 32 x 48, the
+//     tile plan below). A CU's vector memory path moves about 64 bytes per clock
 //     (L2-resident loads into LDS or VGPRs alike); a 256 x 256 tile asks 7.8 bytes per kFLOP of it, half of
 //     what the MFMA rate allows, a 128 x 128 tile 15.6 -- all of it -- so the plan takes the larger tile
 //     whenever it alone fills the GPU.
@@ -1046,8 +1048,9 @@ __global__ __launch_bounds__(64) void rms_norm_apply_kernel(const bf16_t* __rest
 //   * Few tiles, or long K with fewer tiles than CUs: K is cut into `splits` slices; each publishes its fp32
 //     tile to the workspace (agent-scope stores, a per-tile arrival counter in the fixed counter region) and
 //     the last to arrive sums the slices in slice order -- deterministic -- and runs the epilogue.
-//   * Epilogues: STORE passes the fp32 tile through LDS in 64-row passes; SILU stages only the bf16 outputs
-//     (one pass). All threads then write row-contiguous 16-byte pieces. Roundings to bf16 use the hardware
+//   * Epilogues: STORE passes the fp32 tile through LDS in 64-row passes (RESNORM adds the residual's
+//     pieces, ROPE rotates a head's low and high dims together); SILU stages only the bf16 outputs (one
+//     pass). All threads then write row-contiguous 16-byte pieces. Roundings to bf16 use the hardware
 //     conversion (round to nearest even); the SiLU is g * rcp(1 + exp2(-g log2 e)) on the transcendental
 //     unit (within 2 ulp of fp32 division before the bf16 rounding).
 constexpr int TG_BK = 32;
@@ -1068,12 +1071,23 @@ struct TgShape {
   static constexpr int CP = BN + 4;                           // floats per row of the staged STORE tile
   static constexpr int OCP = BN / 2 + 8;                      // bf16 per row of the staged SILU tile
   static constexpr int CBYTES = TG_CROWS * CP * 4 > BM * OCP * 2 ? TG_CROWS * CP * 4 : BM * OCP * 2;
-  static constexpr int LDS = S * STAGE > CBYTES ? S * STAGE : CBYTES;
   static constexpr int PART = BM * BN;                        // floats of one published slice of a tile
-  static constexpr int AJ = BM / (16 * NW), BJ = BN / (16 * NW);   // DMA instructions per wave per stage
-  static constexpr int DMA = AJ + BJ;
+  // DMA instructions of a stage: 16-row groups, GA of X rows then GB of W rows. EVEN: wave w stages X groups
+  // AJ w .. AJ w + AJ - 1 and W groups BJ w .. likewise. Otherwise instruction d of wave w stages group
+  // d NW + w, and the waves left without one issue a no-traffic copy of zeros into a spare 1 KB (DUMMY), so
+  // that every wave counts DMA copies per stage.
+  static constexpr int GA = BM / 16, GB = BN / 16;
+  static constexpr bool EVEN = GA % NW == 0 && GB % NW == 0;
+  static constexpr int AJ = EVEN ? GA / NW : 0, BJ = EVEN ? GB / NW : 0;
+  static constexpr int DMA = EVEN ? AJ + BJ : (GA + GB + NW - 1) / NW;
+  static constexpr int DUMMY = S * STAGE;                     // spare bytes after the ring (not EVEN)
+  static constexpr int RING = EVEN ? S * STAGE : S * STAGE + 1024;
+  static constexpr int LDS0 = RING > CBYTES ? RING : CBYTES;
+  // one workgroup per CU: more than half the CU's 160 KB
+  static constexpr int LDS = WG_PER_CU == 1 && LDS0 <= 80 * 1024 ? 80 * 1024 + 16 : LDS0;
   static constexpr int MF = FM * FN;                          // MFMAs per wave per step
-  static_assert(FM % 4 == 0 && FN % 2 == 0 && AJ >= 1 && BJ >= 1 && DMA <= MF && MF % 8 == 0 &&
+  static constexpr int RW = 16 * FM;                          // rows of a wave's block
+  static_assert((RW % TG_CROWS == 0 || TG_CROWS % RW == 0) && (!EVEN || (AJ >= 1 && BJ >= 1)) && DMA <= MF &&
                     WG_PER_CU * LDS <= 160 * 1024,
                 "tile shape");
 };
@@ -1225,17 +1239,28 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
   // DMA lanes: X instruction j of wave w stages rows 16 (AJ w + j) + l / 4, W instruction j rows
   // 16 (BJ w + j) + l / 4; slot l % 4 of a row holds chunk (l % 4) ^ ((row / 2) & 3). Row offsets go in the
   // per-lane offset, so rows past M / N fail the bounds.
-  constexpr int AJ = SH::AJ, BJ = SH::BJ;
-  uint32_t voa[AJ], vob[BJ];
+  constexpr int AJ = SH::AJ, BJ = SH::BJ, GA = SH::GA, GB = SH::GB;
+  uint32_t voa[AJ > 0 ? AJ : 1], vob[BJ > 0 ? BJ : 1], vo[SH::DMA];
+  const int wu = __builtin_amdgcn_readfirstlane(w);   // the wave index as a scalar (uniform branches)
+  if constexpr (SH::EVEN) {
 #pragma unroll
-  for (int j = 0; j < AJ; ++j) {
-    const int r = 16 * (AJ * w + j) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
-    voa[j] = (uint32_t(m0 + r) * uint32_t(K) + uint32_t(8 * c)) * 2u;
-  }
+    for (int j = 0; j < AJ; ++j) {
+      const int r = 16 * (AJ * w + j) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
+      voa[j] = (uint32_t(m0 + r) * uint32_t(K) + uint32_t(8 * c)) * 2u;
+    }
 #pragma unroll
-  for (int j = 0; j < BJ; ++j) {
-    const int r = 16 * (BJ * w + j) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
-    vob[j] = (uint32_t(tg_wrow<EPI, FN, BN>(r, tn, half)) * uint32_t(K) + uint32_t(8 * c)) * 2u;
+    for (int j = 0; j < BJ; ++j) {
+      const int r = 16 * (BJ * w + j) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
+      vob[j] = (uint32_t(tg_wrow<EPI, FN, BN>(r, tn, half)) * uint32_t(K) + uint32_t(8 * c)) * 2u;
+    }
+  } else {
+#pragma unroll
+    for (int d = 0; d < SH::DMA; ++d) {
+      const int gx = d * NW + wu, gw = gx - GA;
+      const int r = 16 * (gx < GA ? gx : gw) + (l >> 2), c = (l & 3) ^ ((r >> 1) & 3);
+      const uint32_t row = gx < GA ? uint32_t(m0 + r) : gw < GB ? uint32_t(tg_wrow<EPI, FN, BN>(r, tn, half)) : 0u;
+      vo[d] = (row * uint32_t(K) + uint32_t(8 * c)) * 2u;
+    }
   }
   const __amdgpu_buffer_rsrc_t xr = tg_rsrc(a.x, uint32_t(M) * uint32_t(K) * 2u), xnone = tg_rsrc(a.x, 0u);
   const __amdgpu_buffer_rsrc_t wr = tg_rsrc(a.w, uint32_t(N) * uint32_t(K) * 2u), wnone = tg_rsrc(a.w, 0u);
@@ -1244,14 +1269,28 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
     const bool live = q < nk;
     const int soff = __builtin_amdgcn_readfirstlane(live ? (kb + q) * TG_BK * 2 : 0);   // uniform: an SGPR
     unsigned char* st = lds + (q % S) * SH::STAGE;
-    if (d < AJ)
+    if constexpr (!SH::EVEN) {
+      const int gx = d * NW + wu, gw = gx - GA;
+      if (gx < GA)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? xr : xnone,
+                                                 (__attribute__((address_space(3))) void*)(st + 16 * gx * 64), 16,
+                                                 int(vo[d]), soff, 0, 0);
+      else if (gw < GB)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            live ? wr : wnone, (__attribute__((address_space(3))) void*)(st + SH::AROWS + 16 * gw * 64), 16,
+            int(vo[d]), soff, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xnone, (__attribute__((address_space(3))) void*)(lds + SH::DUMMY),
+                                                 16, 0, 0, 0, 0);
+    } else if (d < AJ) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? xr : xnone,
                                                (__attribute__((address_space(3))) void*)(st + 16 * (AJ * w + d) * 64),
                                                16, int(voa[d]), soff, 0, 0);
-    else
+    } else {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           live ? wr : wnone, (__attribute__((address_space(3))) void*)(st + SH::AROWS + 16 * (BJ * w + d - AJ) * 64), 16,
           int(vob[d - AJ]), soff, 0, 0);
+    }
   };
 
   // fragment offsets within a stage: lane -> row l % 16 of the 16-row tile, 16-byte chunk l / 16; the swizzle
@@ -1271,8 +1310,8 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
   // row it / (BN / 8), 8 columns it % (BN / 8)), loaded before the K loop so their latency hides under it,
   // when they fit in 8 registers of 16 bytes (else each item loads its own). Addresses are clamped into the
   // residual, so the loads are unconditional; pieces past M or N are never used.
-  constexpr int RIPR = BN / 8, RIPT = TG_CROWS * RIPR / NT;
-  static_assert(TG_CROWS * RIPR % NT == 0 && TG_CROWS * (BN / 16) % NT == 0, "epilogue items per thread");
+  constexpr int RIPR = BN / 8, RIPT = (TG_CROWS * RIPR + NT - 1) / NT;   // items per thread and pass, at most
+  static_assert(TG_CROWS * RIPR % 64 == 0 && TG_CROWS * (BN / 16) % 64 == 0, "epilogue items: whole waves");
   constexpr int RPRE = EPI == EPI_RESNORM && BM / TG_CROWS * RIPT <= 8 ? BM / TG_CROWS * RIPT : 0;
   g_u32x4_t rres[RPRE > 0 ? RPRE : 1];
   if constexpr (RPRE > 0) {
@@ -1374,24 +1413,40 @@ __global__ __launch_bounds__((TgShape<FM, FN, NW, WM>::NT), (TgShape<FM, FN, NW,
     // m-tiles 4 (p % (FM / 4)) .. + 3), then items (row m, 8 columns) of 16 bytes (RESNORM: plus the
     // residual's 8); ROPE: items (row m, 8 dims of a head's low half and the matching 8 of its high half)
     float* C = reinterpret_cast<float*>(lds);
-    constexpr int CP = SH::CP, PASSES = BM / TG_CROWS, PW = FM / 4, IPR = EPI == EPI_ROPE ? BN / 16 : BN / 8;
+    constexpr int CP = SH::CP, PASSES = BM / TG_CROWS, IPR = EPI == EPI_ROPE ? BN / 16 : BN / 8;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      if (wm == p / PW) {
+      if constexpr (SH::RW >= TG_CROWS) {   // a wave block spans PW passes
+        constexpr int PW = SH::RW / TG_CROWS;
+        if (wm == p / PW) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              C[(16 * i + 4 * (l >> 4) + r) * CP + 16 * FN * wn + 16 * j + (l & 15)] = acc[4 * (p % PW) + i][j][r];
+              for (int r = 0; r < 4; ++r)
+                C[(16 * i + 4 * (l >> 4) + r) * CP + 16 * FN * wn + 16 * j + (l & 15)] = acc[4 * (p % PW) + i][j][r];
+        }
+      } else {   // a pass holds WPP wave blocks
+        constexpr int WPP = TG_CROWS / SH::RW;
+        if (wm / WPP == p) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                C[(SH::RW * (wm % WPP) + 16 * i + 4 * (l >> 4) + r) * CP + 16 * FN * wn + 16 * j + (l & 15)] =
+                    acc[i][j][r];
+        }
       }
       tg_barrier();   // LDS only: the global stores of the previous pass need not land first
       const int mb = m0 + TG_CROWS * p;
-      constexpr int IPT = TG_CROWS * IPR / NT;   // items per thread and pass
+      constexpr int IPT = (TG_CROWS * IPR + NT - 1) / NT;   // items per thread and pass, at most
 #pragma unroll
       for (int k = 0; k < IPT; ++k) {
         const int it = tid + k * NT, m = it / IPR, c8 = it % IPR, gm = mb + m, gn = BN * tn + 8 * c8;
+        if (TG_CROWS * IPR % NT != 0 && it >= TG_CROWS * IPR) continue;   // whole waves (checked above)
         if constexpr (EPI == EPI_ROPE) {
           tg_rope_item(a, C + m * CP, gm, BN * tn, c8);
           continue;
@@ -1669,7 +1724,7 @@ static int bind_xnorm(GemmArgs& a, const float* x_sumsq, const void* x_norm_w, f
 }
 
 // ---- tiled GEMM plan and launch (M > 64)
-enum TgTile { TG_SMALL = 0, TG_BIG = 1, TG_TALL = 2, TG_SMALL8 = 3 };
+enum TgTile { TG_SMALL = 0, TG_BIG = 1, TG_TALL = 2, TG_SMALL8 = 3, TG_N96 = 4 };
 struct TgPlan {
   int shape;   // TgTile: 128 x 128 (4 waves, two per CU), 256 x 256 or 256 x 128 (8 waves, one per CU)
   int tiles_m, tiles_n, splits, kps;
@@ -1679,9 +1734,12 @@ using TgBig = TgShape<8, 4, 8>;
 using TgSmall = TgShape<4, 4, 4>;
 using TgTall = TgShape<4, 4, 8, 4>;   // 256 X rows x 128 W rows: waves in a 4 x 2 grid of 64 x 64 blocks
 using TgSmall8 = TgShape<4, 2, 8, 2>; // 128 x 128 with 8 waves in a 2 x 4 grid of 64 x 32 blocks
+using TgN96 = TgShape<2, 3, 8, 4>;    // 128 x 96 with 8 waves in a 4 x 2 grid of 32 x 48 blocks
 static_assert(TgSmall8::BM == TgSmall::BM && TgSmall8::BN == TgSmall::BN, "same tile, twice the waves");
 static int tg_bm(int shape) { return shape == TG_BIG ? TgBig::BM : shape == TG_TALL ? TgTall::BM : TgSmall::BM; }
-static int tg_bn(int shape) { return shape == TG_BIG ? TgBig::BN : shape == TG_TALL ? TgTall::BN : TgSmall::BN; }
+static int tg_bn(int shape) {
+  return shape == TG_BIG ? TgBig::BN : shape == TG_TALL ? TgTall::BN : shape == TG_N96 ? TgN96::BN : TgSmall::BN;
+}
 static void tg_tiles(TgPlan& p, int M, int N, bool silu) {
   const int bm = tg_bm(p.shape), bn = tg_bn(p.shape);
   p.tiles_m = (M + bm - 1) / bm;
@@ -1705,7 +1763,8 @@ static int tg_fill_splits(int tiles, int max_splits, int steps) {
   if (s > steps / 8) s = steps / 8;
   return s < 1 ? 1 : s;
 }
-static TgPlan tg_plan(int M, int N, int K, bool silu) {
+static TgPlan tg_plan(int M, int N, int K, int epi) {
+  const bool silu = epi == EPI_SILU;
   TgPlan p;
   const int T = target_workgroups(), steps = K / TG_BK;
   p.shape = TG_BIG;
@@ -1733,6 +1792,16 @@ static TgPlan tg_plan(int M, int N, int K, bool silu) {
   // one, so one wave's LDS reads and barrier overlap the other's products (1552 x 1536 x 1536: 18.8 -> 17.4 us;
   // 512 x 1536 x 8960 in 5 slices: 40.4 -> 38.0)
   if (!silu && p.shape == TG_SMALL && tiles * splits <= T) p.shape = TG_SMALL8;
+  // ... and an unsliced one (no RoPE: its heads are 64 or 128 wide) that leaves CUs idle takes 128 x 96 tiles
+  // (8 waves of 32 x 48) when they too fit one round and cover N exactly: more CUs, each SIMD with three
+  // quarters of the work (1552 x 1536 x 1536: 19.1 -> 18.7 us, 20.0 -> 19.3 with the residual add; 300 rows
+  // 18.8 -> 17.2; 1552 x 1003 x 896, a partial last column tile: 14.3 -> 14.6, hence N % 96 == 0)
+  if ((epi == EPI_STORE || epi == EPI_RESNORM) && p.shape == TG_SMALL8 && splits == 1 && N % TgN96::BN == 0) {
+    TgPlan t = p;
+    t.shape = TG_N96;
+    tg_tiles(t, M, N, false);
+    if (t.tiles_m * t.tiles_n <= T) p = t;
+  }
   tg_plan_override(p, M, N, silu, splits);
   tiles = p.tiles_m * p.tiles_n;
   if (splits > TG_MAX_SPLITS) splits = TG_MAX_SPLITS;
@@ -1762,7 +1831,7 @@ static int launch_tiled(TgArgs a, void* ws, size_t ws_bytes, hipStream_t st) {
   // 32-bit buffer offsets: every row offset of X and W (plus a tile's overhang) must fit
   NS_REQUIRE((int64_t(M) + 256) * K * 2 < (int64_t(1) << 31) && (int64_t(N) + 256) * K * 2 < (int64_t(1) << 31),
              "gemm: X [%d, %d] or W [%d, %d] too large for 32-bit buffer offsets", M, K, N, K);
-  const TgPlan p = tg_plan(M, N, K, EPI == EPI_SILU);
+  const TgPlan p = tg_plan(M, N, K, EPI);
   NS_REQUIRE(EPI != EPI_ROPE || (tg_bn(p.shape) % a.hd == 0), "gemm(tiled): head_dim %d does not divide the tile", a.hd);
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
@@ -1786,6 +1855,10 @@ static int launch_tiled(TgArgs a, void* ws, size_t ws_bytes, hipStream_t st) {
     hipLaunchKernelGGL((tiled_gemm_kernel<EPIT, 4, 4, 8, 4>), grid, dim3(TgTall::NT), 0, st, a);
   else if (EPI != EPI_SILU && p.shape == TG_SMALL8)
     hipLaunchKernelGGL((tiled_gemm_kernel<EPIT, 4, 2, 8, 2>), grid, dim3(TgSmall8::NT), 0, st, a);
+  else if (p.shape == TG_N96) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_RESNORM)
+      hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 2, 3, 8, 4>), grid, dim3(TgN96::NT), 0, st, a);
+  }
   else
     hipLaunchKernelGGL((tiled_gemm_kernel<EPI, 4, 4, 4, 2>), grid, dim3(TgSmall::NT), 0, st, a);
   return check_launch("gemm(tiled)");
@@ -1821,7 +1894,7 @@ static size_t skinny_large_m_bytes(const Plan& p, int mblocks) {
 extern "C" size_t ns_gemm_workspace_bytes(int M, int N, int K) {
   if (M < 1 || N < 1 || K < 32) return 0;
   if (M > G_MAX_M) {
-    size_t a = tg_plan(M, N, K, false).bytes, b = tg_plan(M, N, K, true).bytes;
+    size_t a = tg_plan(M, N, K, EPI_STORE).bytes, b = tg_plan(M, N, K, EPI_SILU).bytes;
     // the 64-row token blocks of the skinny kernel (STORE with long K; residual + statistics at any K)
     if (M <= t16_max_m() && (M + G_MAX_M - 1) / G_MAX_M * ((N + 63) / 64) <= G_MAX_TILES) {
       const size_t c = skinny_large_m_bytes(make_plan((N + 63) / 64, K), (M + G_MAX_M - 1) / G_MAX_M);
