@@ -42,6 +42,21 @@ def test_workspace_sizing():
     assert n >= slots * 16 * (64 + 2) * 4
 
 
+def test_gemm_routes_on_the_host():
+    """Host-only queries of the GEMM entry points (no GPU call): which merged-QKV shapes the fused RoPE
+    epilogue takes, and which plans need a K-slice workspace."""
+    lib = _lib.load_library()
+    fits = lib.ns_gemm_rope_qkv_fits
+    for M in (1, 64, 65, 192, 193, 1552, 8192):   # a plain input: any M (skinny, tile-16, tiled epilogue)
+        assert fits(M, 1536, 12, 2, 128, 0) == 1 and fits(M, 896, 14, 2, 64, 0) == 1
+    assert fits(128, 1536, 12, 2, 128, 1) == 1 and fits(129, 1536, 12, 2, 128, 1) == 0   # normalised: <= 128
+    assert fits(1552, 1536, 12, 2, 96, 0) == 0 and fits(1552, 1000, 12, 2, 128, 0) == 0  # head_dim, K % 32
+    # K = 1536 products never split K; the 1552-row down projection (K = 8960) runs K slices
+    assert lib.ns_gemm_workspace_bytes(1552, 1536, 1536) == 0
+    assert lib.ns_gemm_workspace_bytes(1552, 2048, 1536) == 0
+    assert lib.ns_gemm_workspace_bytes(1552, 1536, 8960) > 0
+
+
 def test_invalid_arguments_are_rejected_on_the_host():
     lib = _lib.load_library()
     args = [None, 0, 0, None, None, 0, 0, 0, None, 0, None, None, 0, 0,
