@@ -36,8 +36,10 @@ from __future__ import annotations
 
 import gc
 import math
+import struct
 import time
 
+import numpy as np
 import torch
 
 from nanoserve_amd.kernels.paged_attention import pair_rows
@@ -350,9 +352,9 @@ class MixedStepGraph:
         self._pad_all(v)
         tok, pos, slots, dec_idx, rows, info, dec_lens, pf_tab, dec_tab = v
         n = len(sb.token_ids)
-        tok[:n] = sb.token_ids
-        pos[:n] = sb.positions
-        slots[:n] = sb.slots
+        _put_int64(tok, sb.token_ids)
+        _put_int64(pos, sb.positions)
+        _put_int64(slots, sb.slots)
         start, j = 0, 0
         for i, s in enumerate(sb.seqs):
             T = s.n_tokens
@@ -377,6 +379,17 @@ class MixedStepGraph:
             self.graph.replay()
         else:
             self.logits = self.forward()
+
+
+def _put_int64(dst, values) -> None:
+    """values (Python ints) into the head of the int64 array dst. A long list goes through one struct.pack (about
+    12 ns per value against 28 for numpy's list assignment, token-sized values; a 1552-row step stages three
+    such lists)."""
+    n = len(values)
+    if n > 64 and isinstance(values, list):
+        dst[:n] = np.frombuffer(struct.pack(f"{n}q", *values), dtype=np.int64)
+    else:
+        dst[:n] = values
 
 
 MIXED_GRAPH_MAX_ROWS = 512   # default bound: mixed steps of more rows run staged, unrecorded (launches are a
