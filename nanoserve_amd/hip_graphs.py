@@ -35,6 +35,7 @@ K slices depend on the row count, so an unpadded step may round differently).
 from __future__ import annotations
 
 import gc
+import itertools
 import math
 import struct
 import time
@@ -368,9 +369,14 @@ class MixedStepGraph:
         nd = len(sb.dec_idx)
         dec_idx[:nd] = sb.dec_idx
         dec_lens[:nd] = sb.dec_lens
-        for i, t in enumerate(sb.dec_tables):
-            dec_tab[i] = 0
-            dec_tab[i, :len(t)] = t
+        if nd:   # the decode rows' tables through one conversion (zeros past each table's end)
+            dec_tab[:nd] = 0
+            flat = np.frombuffer(struct.pack(f"{sum(len(t) for t in sb.dec_tables)}i",
+                                             *itertools.chain.from_iterable(sb.dec_tables)), dtype=np.int32)
+            o = 0
+            for i, t in enumerate(sb.dec_tables):
+                dec_tab[i, :len(t)] = flat[o:o + len(t)]
+                o += len(t)
 
     def launch(self, par: int) -> None:
         self.par = par
