@@ -522,8 +522,13 @@ __device__ __forceinline__ void decode_rows_body(const RowsArgs& ra, int bid, un
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t off = base + int64_t(4 * j + r4) * s_tok + c16 * 8;
-      kr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(kp + off);
-      vr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(vp + off);
+      if constexpr (PH) {   // a KV head's half of a token row: the other head's workgroup reads the rest
+        kr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(kp + off);
+        vr[sl][j] = *reinterpret_cast<const rk_u32x4_t*>(vp + off);
+      } else {                // whole token rows, read once: streamed past the caches
+        kr[sl][j] = __builtin_nontemporal_load(reinterpret_cast<const rk_u32x4_t*>(kp + off));
+        vr[sl][j] = __builtin_nontemporal_load(reinterpret_cast<const rk_u32x4_t*>(vp + off));
+      }
     }
   };
   unsigned char* kpg = lds + w * (16 * 256);
