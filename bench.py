@@ -302,9 +302,10 @@ def mixed_step_bench(model, cfg, reps: int = 5) -> dict:
         times.append(time.perf_counter() - t0)
     ms = statistics.median(times) * 1e3
 
-    # the same step as the engine runs it: MixedGraphRunner stages the rows into its bucket (1664 rows + a
-    # padding row) and launches the forward; steps above MIXED_GRAPH_MAX_ROWS (512) rows are not recorded as a
-    # graph (their launches are a small share of the step), so this one launches its kernels eagerly
+    # the same step as the engine runs it: MixedGraphRunner stages the rows and launches the forward; steps
+    # above MIXED_GRAPH_MAX_ROWS (512) rows are not recorded as a graph (their launches are a small share of
+    # the step), so this one launches its kernels eagerly, on its 1552 rows + a padding row (a recorded step
+    # would run its whole 128-row bucket + a padding row)
     from nanoserve_amd.hip_graphs import MixedGraphRunner
     from nanoserve_amd.kv_manager import StepBatch
     sb = StepBatch()
@@ -324,7 +325,7 @@ def mixed_step_bench(model, cfg, reps: int = 5) -> dict:
         torch.cuda.synchronize()
         gtimes.append(time.perf_counter() - t0)
     g_ms = statistics.median(gtimes) * 1e3
-    bucket = runner.last.N
+    rows_run = runner.last.rows_run
     recorded = runner.last.graph is not None
     del runner
     H, I, L, V = cfg.hidden_size, cfg.intermediate_size, cfg.n_layers, cfg.vocab_size
@@ -350,7 +351,7 @@ def mixed_step_bench(model, cfg, reps: int = 5) -> dict:
     del pool
     return {"workload": "BASELINE config 4: 1.5B bf16 mixed step, a 1536-token chunk on 512 cached tokens + 16 "
                         "decode rows (ctx U[256, 2048]), 1552 rows; ms_per_step: the engine's mixed-step path "
-                        f"(MixedGraphRunner: bucket {bucket} rows + 1 padding row, host staging and the H2D copy "
+                        f"(MixedGraphRunner: {rows_run - 1} rows + 1 padding row, host staging and the H2D copy "
                         f"included; {'a graph replay' if recorded else 'above its 512-row graph bound, so launched eagerly'}); "
                         "eager_ms_per_step: the unpadded eager forward",
             "ms_per_step": round(g_ms, 3), "eager_ms_per_step": round(ms, 3), "tflop_per_step": round(flops / 1e12, 3),

@@ -30,7 +30,9 @@ decode entries attend over the garbage block from the padding row, and padding r
 the garbage block. The greedy tokens go into pinned host memory inside the graph, as in the decode graph.
 A runner made with capture=False stages the same padded rows and runs the same forward without recording
 it, so an engine without graphs computes its mixed steps exactly as one with them (the kernels' tilings and
-K slices depend on the row count, so an unpadded step may round differently).
+K slices depend on the row count, so an unpadded step may round differently). Steps above the graph bound are
+never recorded by either, so they run tight: their n rows plus one padding row (at index n), not the bucket's
+N + 1, which saves the GEMM work of up to 127 padding rows.
 """
 from __future__ import annotations
 
@@ -281,8 +283,10 @@ MIXED_SEQ_BUCKETS = (1, 2, 4, 8)
 class MixedStepGraph:
     """One mixed-step bucket: N + 1 rows, S prefill entries, D decode entries (see the module docstring)."""
 
-    def __init__(self, runner: "MixedGraphRunner", N: int, S: int, record: bool):
+    def __init__(self, runner: "MixedGraphRunner", N: int, S: int, record: bool, tight: bool = False):
         self.N, self.S, self.D, self.W = N, S, runner.max_decode, runner.max_blocks
+        self.tight = tight and not record   # unrecorded, sized per step: n rows + padding row n
+        self.rows_run = N + 1
         R, D, W = N + 1, self.D, self.W
         self.garbage_block = runner.garbage_block
         self.garbage_slot = runner.garbage_block * runner.block_size
@@ -304,11 +308,11 @@ class MixedStepGraph:
         meta = DecodeMeta(dec_idx, dec_tab, dec_lens)
         # a sequence's new tokens fit both the rows and its table
         prefill = ("chunks", pf_tab, info, min(N, W * runner.block_size), W * runner.block_size)
-        seqs = [SeqInput(R)]
 
-        def forward():
-            return runner.model.forward_batch(tok, pos, seqs, logits=rows, paged=runner.pool, slot_mapping=slots,
-                                              decode_meta=meta, prefill_meta=prefill, greedy_out=self.greedy)
+        def forward(r: int = R):
+            return runner.model.forward_batch(tok[:r], pos[:r], [SeqInput(r)], logits=rows, paged=runner.pool,
+                                              slot_mapping=slots[:r], decode_meta=meta, prefill_meta=prefill,
+                                              greedy_out=self.greedy)
 
         self.forward = forward
         self.graph, self.logits = None, None
@@ -377,6 +381,11 @@ class MixedStepGraph:
             for i, t in enumerate(sb.dec_tables):
                 dec_tab[i, :len(t)] = flat[o:o + len(t)]
                 o += len(t)
+        self.rows_run = self.N + 1
+        if self.tight:   # the padding row is row n: unused decode entries and logit rows point there
+            dec_idx[nd:] = n
+            rows[len(sb.seqs):] = n
+            self.rows_run = n + 1
 
     def launch(self, par: int) -> None:
         self.par = par
@@ -384,7 +393,7 @@ class MixedStepGraph:
         if self.graph is not None:
             self.graph.replay()
         else:
-            self.logits = self.forward()
+            self.logits = self.forward(self.rows_run)
 
 
 def _put_int64(dst, values) -> None:
@@ -407,7 +416,8 @@ class MixedGraphRunner:
     max_graph_rows times the prefill capacities a step of at most max_decode sequences can need
     (graph_keys); capture_all records all of them up front (largest first, so the smaller ones reuse the shared
     pool's segments), a key of that set met before capture_all is recorded on first use, and bigger steps run
-    the same staged forward without a graph. With capture=False nothing is recorded."""
+    the same staged forward without a graph, on their own rows plus one padding row. With capture=False
+    nothing is recorded (steps up to max_graph_rows still run their whole padded bucket)."""
 
     def __init__(self, model: Qwen2Model, pool: PagedKVCache, max_seq_len: int, max_decode: int,
                  max_rows: int, garbage_block: int, capture: bool = True, max_graph_rows: int = MIXED_GRAPH_MAX_ROWS):
@@ -472,7 +482,7 @@ class MixedGraphRunner:
                 g = self._record(key)
                 self.captures_in_run += self.captured_up_front
             else:
-                g = self.staged[key] = MixedStepGraph(self, *key, record=False)
+                g = self.staged[key] = MixedStepGraph(self, *key, record=False, tight=key[0] > self.max_graph_rows)
         par = g.par ^ 1
         torch.cuda.current_stream().synchronize()   # the twin about to be rewritten may still be copying
         g.stage(par, sb)

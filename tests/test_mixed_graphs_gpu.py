@@ -2,7 +2,8 @@
 nanoserve/cuda_graphs.py:151-259, PiecewiseGraphRunner):
   * the replay of a captured mixed step equals, bitwise, the eager forward of the same staged rows; at the
     BASELINE config-4 shape (a 1536-token chunk on 512 cached tokens + 16 decode rows, 2 layers of the 1.5B
-    shape) it agrees with the unpadded eager step and with the fp32 oracle as the eager step does;
+    shape) it agrees with the unpadded eager step and with the fp32 oracle as the eager step does, and so does
+    the same step run tight (unrecorded, its own rows + one padding row) under the default graph bound;
   * an engine whose steps mix chunked prefills with decoding rows gives the same greedy streams with the
     mixed graphs as with the eager forward, and actually replays them.
 """
@@ -93,6 +94,19 @@ def test_config4_mixed_graph_equals_eager_and_follows_the_oracle(hiplib):
           f"(eager vs oracle {d_eager_ref:.3e})")
     assert d_eager <= 0.05
     assert d_graph_ref <= max(2 * d_eager_ref, 0.05)
+
+    # under the default 512-row graph bound the step is not recorded and runs tight: its 1552 rows + padding row
+    # 1552 (the K/V it writes are the chunk's own, rewritten)
+    tight_runner = MixedGraphRunner(model, pool, 2048 + 16, 16, 2048, garbage)
+    tight = tight_runner.run(sb).float().cpu()
+    tg = tight_runner.last
+    assert tg.graph is None and tg.rows_run == 1553
+    assert tight_runner.greedy_tokens(17) == tight.argmax(-1).tolist()
+    d_tight, d_tight_ref = (tight - eager).abs().max().item(), (tight - ref).abs().max().item()
+    print(f"config 4 tight staged step: vs unpadded eager {d_tight:.3e} (bitwise {torch.equal(tight, eager)}), "
+          f"vs oracle {d_tight_ref:.3e}")
+    assert d_tight <= 0.05
+    assert d_tight_ref <= max(2 * d_eager_ref, 0.05)
 
 
 SMALL = ModelConfig(vocab_size=2048, hidden_size=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64,
